@@ -1,0 +1,102 @@
+"""ctypes binding of ``libbsamd.so`` (the C ABI declared in include/bsamd.h).
+
+The library is built in-tree by ``blockstreamer_amd.build``.  There is no
+fallback: if the library is missing or a device tensor is not on a ROCm GPU,
+the calls raise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libbsamd.so"
+
+BSA_OK, BSA_EINVAL, BSA_EHIP = 0, 1, 2
+DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_ptr = ctypes.c_void_p
+_f32 = ctypes.c_float
+
+# name -> argtypes; every symbol returns int unless listed in _RESTYPE.
+_SIGNATURES = {
+    "bsa_last_error": [],
+    "bsa_version": [],
+    "bsa_dequant_mxfp4": [_ptr, _ptr, _ptr, _int, _i64, _i64, _i64, _ptr],
+    "bsa_dequant_mxfp4_mode": [_ptr, _ptr, _ptr, _int, _i64, _i64, _i64, _int, _ptr],
+}
+_RESTYPE = {"bsa_last_error": ctypes.c_char_p}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load ``libbsamd.so`` once and declare its signatures."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m blockstreamer_amd.build`"
+            )
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, args in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPE.get(name, ctypes.c_int)
+        _lib = handle
+    return _lib
+
+
+def symbols() -> list[str]:
+    """Names of the C entry points this binding declares."""
+    return list(_SIGNATURES)
+
+
+def check(rc: int, what: str) -> None:
+    """Raise for a non-zero status: ValueError for bad arguments, else RuntimeError."""
+    if rc == BSA_OK:
+        return
+    msg = lib().bsa_last_error().decode(errors="replace")
+    if rc == BSA_EINVAL:
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg} (status {rc})")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)
+
+
+def stream_handle(device: torch.device) -> int:
+    """The current torch stream of ``device`` as a raw hipStream_t."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_gpu(*tensors: torch.Tensor) -> torch.device:
+    """All tensors on one ROCm device; returns it.  No CPU path exists."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError(
+                "blockstreamer_amd runs on the GPU only: got a tensor on "
+                f"{t.device}; move inputs to a ROCm device"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise ValueError("no device tensor given")
+    return dev
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return DTYPE_CODE[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}; expected bfloat16, float16 or float32")

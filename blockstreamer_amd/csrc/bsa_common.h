@@ -1,0 +1,165 @@
+// Shared definitions for the blockstreamer_amd HIP library (gfx950 / CDNA4).
+//
+// Error model: every extern "C" entry point returns an int status
+// (BSA_OK, BSA_EINVAL for bad shapes/dtypes/alignment, BSA_EHIP for a HIP
+// launch or runtime error) and leaves a thread-local message readable through
+// bsa_last_error().  Entry points never synchronise the stream and never
+// allocate: the caller passes every buffer, workspace included.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/bsamd.h"
+
+namespace bsa {
+
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define BSA_REQUIRE(cond, ...)                 \
+  do {                                         \
+    if (!(cond)) {                             \
+      ::bsa::set_error(__VA_ARGS__);           \
+      return BSA_EINVAL;                       \
+    }                                          \
+  } while (0)
+
+#define BSA_LAUNCH_CHECK(what)                                               \
+  do {                                                                       \
+    hipError_t _e = hipGetLastError();                                       \
+    if (_e != hipSuccess) {                                                  \
+      ::bsa::set_error("%s: %s", (what), hipGetErrorString(_e));             \
+      return BSA_EHIP;                                                       \
+    }                                                                        \
+  } while (0)
+
+typedef uint16_t bf16_bits;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+
+// ---------------------------------------------------------------------------
+// MXFP4 element decode.
+//
+// An element is an OCP MX E2M1 code (bit 3 sign, 2 exponent bits, 1 mantissa
+// bit: magnitudes 0, .5, 1, 1.5, 2, 3, 4, 6) times 2^(s-127) for the block's
+// E8M0 byte s, evaluated the way the reference does it: a float32 product of
+// the value and float32 pow(2, s-127) (2^128 = inf, so s = 255 gives +-inf for
+// nonzero codes and NaN for +-0 codes), rounded once to the output type.  All
+// finite products below are exact in bfloat16 and float32.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;  // v_cvt_f16_f32, round to nearest even
+  return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+// Exact float32 bit pattern of code * 2^(s-127), built with integer
+// arithmetic so that it does not depend on the float denormal mode.
+__device__ __forceinline__ uint32_t mx_fp32_bits(uint32_t code, uint32_t s) {
+  const uint32_t sign = (code & 8u) << 28;
+  const uint32_t m = code & 7u;
+  if (s == 255u) return m ? (sign | 0x7F800000u) : 0x7FC00000u;
+  if (m == 0u) return sign;
+  // m == 1 is the E2M1 subnormal 0.5 = 1.0 * 2^-1; m >= 2 is
+  // (1 + (m & 1) / 2) * 2^((m >> 1) - 1).
+  const int eoff = (m == 1u) ? -1 : (int)(m >> 1) - 1;
+  const uint32_t mant = (m == 1u) ? 0u : (m & 1u);
+  const int be = (int)s + eoff;  // biased exponent of the product
+  if (be >= 255) return sign | 0x7F800000u;
+  if (be >= 1) return sign | ((uint32_t)be << 23) | (mant << 22);
+  // be in {0, -1}: a float32 subnormal, (1 + mant/2) * 2^(be-127)
+  return sign | ((2u + mant) << (21 + be));
+}
+
+// Two codes of one packed byte -> bfloat16x2 (low nibble in the low half),
+// exact path.
+__device__ __forceinline__ uint32_t mx_byte_to_bf16x2_exact(uint32_t byte, uint32_t s) {
+  const uint32_t lo = mx_fp32_bits(byte & 15u, s) >> 16;
+  const uint32_t hi = mx_fp32_bits((byte >> 4) & 15u, s) >> 16;
+  return lo | (hi << 16);
+}
+
+// float16 element: torch.ldexp on a float16 tensor rounds pow(2, s-127) to
+// float16 first, so the scale is inf for s >= 143 (2^16) and 0 for s <= 102
+// (2^-25 rounds to 0); in between the float32 product is rounded once.
+__device__ __forceinline__ uint32_t mx_f16_bits(uint32_t code, uint32_t s) {
+  const uint32_t sign = (code & 8u) << 12;
+  if (s >= 143u) return (code & 7u) ? (sign | 0x7C00u) : 0x7E00u;
+  if (s <= 102u) return sign;
+  return f32_to_f16_bits(__uint_as_float(mx_fp32_bits(code, s)));
+}
+
+__device__ __forceinline__ uint32_t mx_byte_to_f16x2(uint32_t byte, uint32_t s) {
+  return mx_f16_bits(byte & 15u, s) | (mx_f16_bits((byte >> 4) & 15u, s) << 16);
+}
+
+// Scale bytes for which the gfx950 hardware converter is used.  Measured
+// over every (byte, scale) pair on an MI355X, v_cvt_scalef32_pk_bf16_fp4
+// reproduces the reference bit for bit for scale bytes 0..254 (subnormal and
+// overflowing products included); 255, the E8M0 NaN code, gives NaN for
+// every code where the reference gives +-inf, so it takes the integer path.
+__device__ __forceinline__ bool mx_scale_hw_ok(uint32_t s) { return s != 255u; }
+
+// The converter reads the E8M0 scale from the exponent field of a float32.
+__device__ __forceinline__ float mx_scale_f32(uint32_t s) { return __uint_as_float(s << 23); }
+
+// Byte `sel` of `dword` -> bfloat16x2 with the gfx950 converter
+// (v_cvt_scalef32_pk_bf16_fp4).  Only valid for mx_scale_hw_ok(s).
+template <int SEL>
+__device__ __forceinline__ uint32_t mx_byte_to_bf16x2_hw(uint32_t dword, float scale) {
+  bf16x2_t v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(dword, scale, SEL);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Four packed bytes (8 codes) -> 4 dwords of bfloat16x2, in code order.
+__device__ __forceinline__ void mx_dword_to_bf16x8(uint32_t dword, uint32_t s, bool hw,
+                                                   uint32_t out[4]) {
+  if (hw) {
+    const float sf = mx_scale_f32(s);
+    out[0] = mx_byte_to_bf16x2_hw<0>(dword, sf);
+    out[1] = mx_byte_to_bf16x2_hw<1>(dword, sf);
+    out[2] = mx_byte_to_bf16x2_hw<2>(dword, sf);
+    out[3] = mx_byte_to_bf16x2_hw<3>(dword, sf);
+  } else {
+    out[0] = mx_byte_to_bf16x2_exact(dword & 0xFFu, s);
+    out[1] = mx_byte_to_bf16x2_exact((dword >> 8) & 0xFFu, s);
+    out[2] = mx_byte_to_bf16x2_exact((dword >> 16) & 0xFFu, s);
+    out[3] = mx_byte_to_bf16x2_exact(dword >> 24, s);
+  }
+}
+
+__device__ __forceinline__ uint32_t pack_lo16(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);  // a.lo | b.lo << 16
+}
+__device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);  // a.hi | b.hi << 16
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+  return __uint_as_float(b << 16);
+}
+
+// float32 -> bfloat16 bits, round to nearest even, NaN -> 0x7FC0.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+
+// Activation / weight element types accepted by the kernels.
+enum DType : int { DT_BF16 = BSA_DTYPE_BF16, DT_F16 = BSA_DTYPE_F16, DT_F32 = BSA_DTYPE_F32 };
+
+}  // namespace bsa

@@ -1,0 +1,233 @@
+// MXFP4 -> dense dequantisation (the K1 kernel).
+//
+// Replaces transformers integrations/mxfp4.py:257-313
+// (_convert_moe_packed_tensors), reached from block_streamer/gptoss.py:41.
+// The reference builds int32 index temporaries, gathers a LUT twice, scales
+// in place with ldexp and then transposes with a full copy; here one pass
+// reads each packed byte once and writes each output element once.
+//
+// Vectorised path: a workgroup owns 64 consecutive packed rows r of one
+// expert (a contiguous 64 * G * 16-byte span) and walks all G groups.  Each
+// lane decodes 8 consecutive rows of one group (8 x 16-byte loads; for a
+// fixed row the 8 lanes of a row-group read 128 contiguous bytes), then
+// transposes in registers so that for each of the group's 32 output rows k it
+// stores the 8 adjacent columns r..r+7 as one 16-byte store (for a fixed k,
+// 8 lanes write 128 contiguous bytes).  Everything is HBM-bound: 2.53 bytes
+// of traffic per bf16 output element.
+#include "bsa_common.h"
+
+namespace bsa {
+
+constexpr int DQ_ROWG = 8;             // row-groups of 8 rows per wave
+constexpr int DQ_GPW = 64 / DQ_ROWG;   // groups per wave
+constexpr int DQ_ROWS = 8 * DQ_ROWG;   // rows per workgroup (64)
+
+template <int OUT>
+__device__ __forceinline__ void dq_store8(void* out, size_t elem_off, const uint32_t v2[4]) {
+  // v2 holds 8 16-bit values (columns r..r+7 of one output row): bfloat16
+  // for bf16 and f32 outputs (every f32 result is exact in bf16), float16
+  // for f16 outputs.
+  if constexpr (OUT == DT_F32) {
+    u32x4_t a = {v2[0] << 16, v2[0] & 0xFFFF0000u, v2[1] << 16, v2[1] & 0xFFFF0000u};
+    u32x4_t b = {v2[2] << 16, v2[2] & 0xFFFF0000u, v2[3] << 16, v2[3] & 0xFFFF0000u};
+    u32x4_t* p = reinterpret_cast<u32x4_t*>(static_cast<float*>(out) + elem_off);
+    p[0] = a;
+    p[1] = b;
+  } else {
+    u32x4_t v = {v2[0], v2[1], v2[2], v2[3]};
+    *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(out) + elem_off) = v;
+  }
+}
+
+template <int OUT, bool HW>
+__device__ __forceinline__ void dq_decode_store(const u32x4_t (&pk)[8], const uint32_t (&s)[8],
+                                                void* out, size_t out_base, int R) {
+  // out_base = element offset of (k = 32g, r) for this lane's first row.
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    uint32_t c[8][4];  // c[row][byte b] = bf16x2 of codes (2j, 2j+1), j = 4q + b
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t d = pk[i][q];
+      if constexpr (OUT == DT_F16) {
+        c[i][0] = mx_byte_to_f16x2(d & 0xFFu, s[i]);
+        c[i][1] = mx_byte_to_f16x2((d >> 8) & 0xFFu, s[i]);
+        c[i][2] = mx_byte_to_f16x2((d >> 16) & 0xFFu, s[i]);
+        c[i][3] = mx_byte_to_f16x2(d >> 24, s[i]);
+      } else if constexpr (HW) {
+        const float sf = mx_scale_f32(s[i]);
+        c[i][0] = mx_byte_to_bf16x2_hw<0>(d, sf);
+        c[i][1] = mx_byte_to_bf16x2_hw<1>(d, sf);
+        c[i][2] = mx_byte_to_bf16x2_hw<2>(d, sf);
+        c[i][3] = mx_byte_to_bf16x2_hw<3>(d, sf);
+      } else {
+        c[i][0] = mx_byte_to_bf16x2_exact(d & 0xFFu, s[i]);
+        c[i][1] = mx_byte_to_bf16x2_exact((d >> 8) & 0xFFu, s[i]);
+        c[i][2] = mx_byte_to_bf16x2_exact((d >> 16) & 0xFFu, s[i]);
+        c[i][3] = mx_byte_to_bf16x2_exact(d >> 24, s[i]);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int k = 2 * (4 * q + b);
+      uint32_t ev[4], od[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        ev[p] = pack_lo16(c[2 * p][b], c[2 * p + 1][b]);
+        od[p] = pack_hi16(c[2 * p][b], c[2 * p + 1][b]);
+      }
+      dq_store8<OUT>(out, out_base + (size_t)k * R, ev);
+      dq_store8<OUT>(out, out_base + (size_t)(k + 1) * R, od);
+    }
+  }
+}
+
+template <int OUT, bool ALIGN16>
+__global__ __launch_bounds__(256) void dequant_vec_kernel(const uint8_t* __restrict__ blocks,
+                                                          const uint8_t* __restrict__ scales,
+                                                          void* __restrict__ out, int R, int G,
+                                                          int row_tiles, int mode) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int e = blockIdx.x / row_tiles;
+  const int rt = blockIdx.x - e * row_tiles;
+  const int r = rt * DQ_ROWS + 8 * (lane % DQ_ROWG);
+  const int K = G * 32;
+  const int g_tiles = (G + DQ_GPW - 1) / DQ_GPW;
+  if (r >= R) return;  // R % 8 == 0, so a lane owns either 8 valid rows or none
+  const size_t row0 = (size_t)e * R + r;
+
+  for (int gt = wave; gt < g_tiles; gt += 4) {
+    const int g = gt * DQ_GPW + lane / DQ_ROWG;
+    const bool active = g < G;
+    u32x4_t pk[8];
+    uint32_t s[8];
+    bool in_range = true;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (active) {
+        const size_t rg = (row0 + i) * G + g;
+        const uint8_t* p = blocks + rg * 16;
+        if constexpr (ALIGN16) {
+          pk[i] = *reinterpret_cast<const u32x4_t*>(p);
+        } else {
+          const uint2 a = *reinterpret_cast<const uint2*>(p);
+          const uint2 b = *reinterpret_cast<const uint2*>(p + 8);
+          pk[i] = u32x4_t{a.x, a.y, b.x, b.y};
+        }
+        s[i] = scales[rg];
+      } else {
+        pk[i] = u32x4_t{0u, 0u, 0u, 0u};
+        s[i] = 127u;
+      }
+      in_range = in_range && mx_scale_hw_ok(s[i]);
+    }
+    const bool hw = (mode == 2) || (mode == 0 && __all(in_range));
+    if (active) {
+      const size_t out_base = ((size_t)e * K + (size_t)32 * g) * R + r;
+      if (hw && OUT != DT_F16)
+        dq_decode_store<OUT, true>(pk, s, out, out_base, R);
+      else
+        dq_decode_store<OUT, false>(pk, s, out, out_base, R);
+    }
+  }
+}
+
+// Fallback for any shape or alignment: one thread per packed byte.
+template <int OUT>
+__global__ __launch_bounds__(256) void dequant_generic_kernel(const uint8_t* __restrict__ blocks,
+                                                              const uint8_t* __restrict__ scales,
+                                                              void* __restrict__ out, int64_t E,
+                                                              int64_t R, int64_t G) {
+  const int64_t n = E * R * G * 16;
+  const int64_t K = G * 32;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t rg = i >> 4;
+    const int j = (int)(i & 15);
+    const int64_t g = rg % G;
+    const int64_t er = rg / G;
+    const int64_t r = er % R;
+    const int64_t e = er / R;
+    const uint32_t byte = blocks[i];
+    const uint32_t s = scales[rg];
+    const int64_t k = 32 * g + 2 * j;
+    const int64_t o0 = (e * K + k) * R + r;
+    const int64_t o1 = o0 + R;
+    const uint32_t v0 = mx_fp32_bits(byte & 15u, s);
+    const uint32_t v1 = mx_fp32_bits(byte >> 4, s);
+    if constexpr (OUT == DT_BF16) {
+      static_cast<uint16_t*>(out)[o0] = (uint16_t)(v0 >> 16);
+      static_cast<uint16_t*>(out)[o1] = (uint16_t)(v1 >> 16);
+    } else if constexpr (OUT == DT_F32) {
+      static_cast<uint32_t*>(out)[o0] = v0;
+      static_cast<uint32_t*>(out)[o1] = v1;
+    } else {
+      static_cast<uint16_t*>(out)[o0] = (uint16_t)mx_f16_bits(byte & 15u, s);
+      static_cast<uint16_t*>(out)[o1] = (uint16_t)mx_f16_bits(byte >> 4, s);
+    }
+  }
+}
+
+template <int OUT>
+static int launch_dequant(const uint8_t* blocks, const uint8_t* scales, void* out, int64_t E,
+                          int64_t R, int64_t G, int mode, hipStream_t stream) {
+  const uintptr_t bp = reinterpret_cast<uintptr_t>(blocks);
+  const uintptr_t op = reinterpret_cast<uintptr_t>(out);
+  // The vectorised kernel decodes in whichever way `mode` asks (mode 1 makes
+  // it take the integer decoder for every wave).
+  const bool vec = (R % 8 == 0) && (op % 16 == 0) && (bp % 8 == 0) && R <= INT32_MAX / 2 &&
+                   G <= INT32_MAX / 64;
+  if (vec) {
+    const int row_tiles = (int)((R + DQ_ROWS - 1) / DQ_ROWS);
+    const int64_t nblk = E * row_tiles;
+    if (nblk > INT32_MAX) {
+      set_error("dequant: grid too large (E=%lld R=%lld)", (long long)E, (long long)R);
+      return BSA_EINVAL;
+    }
+    if (bp % 16 == 0)
+      hipLaunchKernelGGL((dequant_vec_kernel<OUT, true>), dim3((unsigned)nblk), dim3(256), 0,
+                         stream, blocks, scales, out, (int)R, (int)G, row_tiles, mode);
+    else
+      hipLaunchKernelGGL((dequant_vec_kernel<OUT, false>), dim3((unsigned)nblk), dim3(256), 0,
+                         stream, blocks, scales, out, (int)R, (int)G, row_tiles, mode);
+  } else {
+    const int64_t n = E * R * G * 16;
+    int64_t nb = (n + 255) / 256;
+    if (nb > 65536) nb = 65536;
+    hipLaunchKernelGGL((dequant_generic_kernel<OUT>), dim3((unsigned)nb), dim3(256), 0, stream,
+                       blocks, scales, out, E, R, G);
+  }
+  BSA_LAUNCH_CHECK("dequant launch");
+  return BSA_OK;
+}
+
+}  // namespace bsa
+
+extern "C" int bsa_dequant_mxfp4_mode(const void* blocks, const void* scales, void* out,
+                                      int out_dtype, int64_t E, int64_t R, int64_t G, int mode,
+                                      void* stream) {
+  using namespace bsa;
+  clear_error();
+  BSA_REQUIRE(E >= 0 && R >= 0 && G >= 0, "dequant: negative shape E=%lld R=%lld G=%lld",
+              (long long)E, (long long)R, (long long)G);
+  BSA_REQUIRE(mode >= 0 && mode <= 2, "dequant: mode must be 0, 1 or 2 (got %d)", mode);
+  BSA_REQUIRE(out_dtype == DT_BF16 || out_dtype == DT_F16 || out_dtype == DT_F32,
+              "dequant: unsupported output dtype %d", out_dtype);
+  if (E == 0 || R == 0 || G == 0) return BSA_OK;
+  BSA_REQUIRE(blocks && scales && out, "dequant: null pointer");
+  BSA_REQUIRE(E <= INT64_MAX / 16 / (R * G) , "dequant: size overflow");
+  const uint8_t* b = static_cast<const uint8_t*>(blocks);
+  const uint8_t* s = static_cast<const uint8_t*>(scales);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (out_dtype) {
+    case DT_BF16: return launch_dequant<DT_BF16>(b, s, out, E, R, G, mode, st);
+    case DT_F16: return launch_dequant<DT_F16>(b, s, out, E, R, G, mode, st);
+    default: return launch_dequant<DT_F32>(b, s, out, E, R, G, mode, st);
+  }
+}
+
+extern "C" int bsa_dequant_mxfp4(const void* blocks, const void* scales, void* out,
+                                 int out_dtype, int64_t E, int64_t R, int64_t G, void* stream) {
+  return bsa_dequant_mxfp4_mode(blocks, scales, out, out_dtype, E, R, G, 0, stream);
+}

@@ -1,0 +1,21 @@
+"""The oracle: a CPU restatement of BlockStreamer's gpt-oss MoE expert path.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s ``cpu_baseline`` leg may import this package, and only as the
+checker (or, for ``cpu_baseline``, as the timed CPU port).  The product
+package ``blockstreamer_amd`` never imports it.
+"""
+
+from .oracle import (  # noqa: F401
+    FP4_VALUES,
+    apply_gate_ref,
+    dequant_c,
+    dequant_torch,
+    bits_equal_or_both_nan,
+    dequantize_expert_ref,
+    dequant_table_c,
+    experts_ref,
+    mlp_ref,
+    router_ref,
+    topk_softmax_ref,
+)

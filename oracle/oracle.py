@@ -1,0 +1,263 @@
+"""CPU restatement of BlockStreamer's gpt-oss MoE expert path (the oracle).
+
+TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()``
+and ``bench.py``'s ``cpu_baseline`` leg, never by the product package.
+
+Every function cites the reference line it restates.  The reference is
+hareramray/BlockStreamer ``block_streamer/gptoss.py``; its arithmetic lives in
+the third-party ``transformers`` package (installed version 5.15.0, the
+version this restatement follows), cited below as ``TF/<path>:<line>``.
+
+Pinning (how each function is checked, see ``tests/test_oracle.py``):
+
+* dequant (C and torch restatements): the closed form of OCP MX E2M1 x E8M0
+  over the exhaustive 16-code x 256-scale table, agreement between the two
+  independent restatements, and the installed transformers
+  ``convert_moe_packed_tensors`` on random inputs and on every (byte, scale)
+  pair.  NaN payloads for scale byte 255 are platform dependent (0 * inf), so
+  NaN is compared as NaN, not by bit pattern.
+* router: brute force over all k-subsets on tiny tie-free inputs, and the
+  installed transformers ``GptOssTopKRouter``.
+* experts: the installed transformers dense twin ``GptOssExperts``
+  (TF/models/gpt_oss/modeling_gpt_oss.py:68-114) fed the dequantised
+  weights, plus invariants (zero routing weight contributes nothing, token
+  permutation commutes, a single expert with k=1 and weight 1 equals the dense
+  chain of library GEMMs).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "_build" / "liboracle_mxfp4.so"
+_lib = None
+
+# TF/integrations/mxfp4.py:29-46 -- E2M1 code -> value, bit 3 is the sign.
+FP4_VALUES = [
+    +0.0, +0.5, +1.0, +1.5, +2.0, +3.0, +4.0, +6.0,
+    -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0,
+]
+
+_DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+def _load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not _LIB_PATH.exists():
+        subprocess.run(["make", "-C", str(_HERE)], check=True,
+                       stdout=subprocess.DEVNULL)
+    lib = ctypes.CDLL(str(_LIB_PATH))
+    lib.oracle_dequant_mxfp4.argtypes = [
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+        ctypes.c_int64, ctypes.c_int, ctypes.c_void_p,
+    ]
+    lib.oracle_dequant_mxfp4.restype = None
+    lib.oracle_dequant_one.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    lib.oracle_dequant_one.restype = ctypes.c_uint32
+    lib.oracle_f32_to_bf16.argtypes = [ctypes.c_float]
+    lib.oracle_f32_to_bf16.restype = ctypes.c_uint16
+    lib.oracle_f32_to_f16.argtypes = [ctypes.c_float]
+    lib.oracle_f32_to_f16.restype = ctypes.c_uint16
+    _lib = lib
+    return lib
+
+
+def dequant_c(blocks: torch.Tensor, scales: torch.Tensor,
+              dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """C restatement of TF/integrations/mxfp4.py:257-313 for [E,R,G,16] input.
+
+    Returns the dense ``[E, G*32, R]`` tensor in ``dtype`` (bf16/f16/f32).
+    """
+    lib = _load()
+    blocks = blocks.detach().to("cpu", torch.uint8).contiguous()
+    scales = scales.detach().to("cpu", torch.uint8).contiguous()
+    if blocks.dim() != 4 or blocks.shape[-1] != 16 or tuple(scales.shape) != tuple(blocks.shape[:-1]):
+        raise ValueError(f"bad packed shapes {tuple(blocks.shape)} / {tuple(scales.shape)}")
+    E, R, G, _ = blocks.shape
+    out = torch.empty((E, G * 32, R), dtype=dtype)
+    lib.oracle_dequant_mxfp4(blocks.data_ptr(), scales.data_ptr(), E, R, G,
+                             _DTYPE_CODE[dtype], out.data_ptr())
+    return out
+
+
+def dequant_table_c(dtype: torch.dtype = torch.bfloat16) -> np.ndarray:
+    """Exhaustive [256 scale, 16 code] table of output bit patterns."""
+    lib = _load()
+    code = _DTYPE_CODE[dtype]
+    tab = np.empty((256, 16), dtype=np.uint32)
+    for s in range(256):
+        for c in range(16):
+            tab[s, c] = lib.oracle_dequant_one(c, s, code)
+    return tab
+
+
+def dequant_torch(blocks: torch.Tensor, scales: torch.Tensor,
+                  dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """torch restatement of TF/integrations/mxfp4.py:257-313, op for op.
+
+    LUT gather on the low and high nibbles into even and odd columns
+    (mxfp4.py:294-304), ``ldexp`` by ``scale - 127`` (mxfp4.py:271, 307),
+    reshape to ``[..., R, G*32]`` and ``transpose(1, 2)`` (mxfp4.py:311-313).
+    """
+    blocks = blocks.to(torch.uint8)
+    exp = scales.to(torch.int32) - 127
+    lut = torch.tensor(FP4_VALUES, dtype=dtype, device=blocks.device)
+    *prefix, G, B = blocks.shape
+    rows = int(np.prod(prefix)) * G
+    blk = blocks.reshape(rows, B)
+    exp = exp.reshape(rows, 1)
+    out = torch.empty(rows, B * 2, dtype=dtype, device=blocks.device)
+    out[:, 0::2] = lut[(blk & 0x0F).to(torch.int)]
+    out[:, 1::2] = lut[(blk >> 4).to(torch.int)]
+    torch.ldexp(out, exp, out=out)
+    out = out.reshape(*prefix, G, B * 2).view(*prefix, G * B * 2)
+    return out.transpose(1, 2).contiguous()
+
+
+def dequantize_expert_ref(blocks: torch.Tensor, scales: torch.Tensor,
+                          dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """block_streamer/gptoss.py:24-42: [1,R,G,16] -> [G*32, R]."""
+    if blocks.dim() != 4:
+        raise ValueError(
+            f"Expected [1, rows, groups, 16] packed blocks, got {tuple(blocks.shape)}"
+        )
+    return dequant_torch(blocks, scales, dtype).squeeze(0)
+
+
+def topk_softmax_ref(logits: torch.Tensor, k: int):
+    """TF/models/gpt_oss/modeling_gpt_oss.py:128-129 on given logits.
+
+    ``topk`` sorted descending; equal logits are ordered lower index first (a
+    stable sort), which is the rule the HIP kernel implements.  Softmax over
+    the k selected values in their own dtype (``softmax(dtype=vals.dtype)``
+    computes in float32 internally for half types and rounds once).
+    """
+    order = torch.sort(logits.float(), dim=-1, descending=True, stable=True).indices
+    idx = order[..., :k].contiguous()
+    vals = torch.gather(logits, -1, idx)
+    scores = torch.softmax(vals.float(), dim=-1).to(logits.dtype)
+    return vals, scores, idx
+
+
+def router_ref(h: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, k: int,
+               dtype: torch.dtype = torch.float32):
+    """TF/models/gpt_oss/modeling_gpt_oss.py:126-131 (GptOssTopKRouter.forward).
+
+    Computed in ``dtype`` (float32 for the parity reference).  Returns
+    ``(logits [T,E], scores [T,k], indices [T,k] int64)``.
+    """
+    logits = F.linear(h.to(dtype), weight.to(dtype), bias.to(dtype))
+    _, scores, idx = topk_softmax_ref(logits, k)
+    return logits, scores, idx
+
+
+def apply_gate_ref(gate_up: torch.Tensor, alpha: float = 1.702,
+                   limit: float = 7.0) -> torch.Tensor:
+    """block_streamer/gptoss.py:130-135: interleaved clamped SwiGLU."""
+    gate, up = gate_up[..., ::2], gate_up[..., 1::2]
+    gate = gate.clamp(max=limit)
+    up = up.clamp(min=-limit, max=limit)
+    glu = gate * torch.sigmoid(gate * alpha)
+    return (up + 1) * glu
+
+
+def experts_ref(h: torch.Tensor, router_indices: torch.Tensor,
+                routing_weights: torch.Tensor,
+                gate_up_blocks: torch.Tensor, gate_up_scales: torch.Tensor,
+                gate_up_bias: torch.Tensor, down_blocks: torch.Tensor,
+                down_scales: torch.Tensor, down_bias: torch.Tensor,
+                alpha: float = 1.702, limit: float = 7.0,
+                dtype: torch.dtype = torch.float32,
+                dense_cache: dict | None = None) -> torch.Tensor:
+    """block_streamer/gptoss.py:137-177 (MXFP4Experts.forward), op for op.
+
+    Runs on the CPU in ``dtype`` (float32 for the parity reference).  ``h``
+    and ``routing_weights`` may require grad; the result is then
+    differentiable by torch autograd, which is the reference for the
+    input-gradient backward (gptoss.py:64-71 plus autograd of 130-176).
+    ``dense_cache`` (optional dict) memoises per-expert dense weights.
+    """
+    h = h.to(dtype)
+    routing_weights = routing_weights.to(dtype)
+    E = gate_up_blocks.shape[0]
+    next_states = torch.zeros_like(h)                                   # :143
+    with torch.no_grad():
+        mask = F.one_hot(router_indices.to(torch.int64), num_classes=E).permute(2, 1, 0)  # :145-147
+        hit = torch.greater(mask.sum(dim=(-1, -2)), 0).nonzero()       # :148
+    for entry in hit:                                                  # :149
+        expert = int(entry[0])
+        top_k_pos, token_idx = torch.where(mask[expert])               # :153
+        current = h[token_idx]                                         # :154
+        key = ("gu", expert)
+        if dense_cache is not None and key in dense_cache:
+            w_gu = dense_cache[key]
+        else:
+            w_gu = dequant_torch(gate_up_blocks[expert:expert + 1],
+                                 gate_up_scales[expert:expert + 1], dtype).squeeze(0)
+            if dense_cache is not None:
+                dense_cache[key] = w_gu
+        gate_up = current @ w_gu + gate_up_bias[expert].to(dtype)       # :158-165
+        gated = apply_gate_ref(gate_up, alpha, limit)                  # :166
+        key = ("dn", expert)
+        if dense_cache is not None and key in dense_cache:
+            w_dn = dense_cache[key]
+        else:
+            w_dn = dequant_torch(down_blocks[expert:expert + 1],
+                                 down_scales[expert:expert + 1], dtype).squeeze(0)
+            if dense_cache is not None:
+                dense_cache[key] = w_dn
+        out = gated @ w_dn + down_bias[expert].to(dtype)               # :167-174
+        out = out * routing_weights[token_idx, top_k_pos, None]        # :175
+        next_states = next_states.index_add(0, token_idx, out.to(h.dtype))  # :176
+    return next_states
+
+
+def mlp_ref(h: torch.Tensor, router_weight: torch.Tensor, router_bias: torch.Tensor,
+            k: int, *expert_params, alpha: float = 1.702, limit: float = 7.0,
+            dtype: torch.dtype = torch.float32):
+    """TF/models/gpt_oss/modeling_gpt_oss.py:140-146 (GptOssMLP.forward).
+
+    ``h`` is ``[B, S, H]``; returns ``(out [B,S,H], scores [T,k])``.
+    """
+    B, S, H = h.shape
+    flat = h.reshape(-1, H)
+    _, scores, idx = router_ref(flat, router_weight, router_bias, k, dtype)
+    out = experts_ref(flat, idx, scores, *expert_params, alpha=alpha, limit=limit,
+                      dtype=dtype)
+    return out.reshape(B, S, H), scores
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16 bit patterns, round to nearest even, NaN -> 0x7FC0."""
+    lib = _load()
+    flat = np.asarray(x, dtype=np.float32).ravel()
+    return np.array([lib.oracle_f32_to_bf16(float(v)) for v in flat],
+                    dtype=np.uint16).reshape(np.shape(x))
+
+
+def bits_equal_or_both_nan(a_bits: np.ndarray, b_bits: np.ndarray,
+                           dtype: torch.dtype) -> np.ndarray:
+    """Element-wise: identical bit patterns, or both NaN in ``dtype``."""
+    a_bits = np.asarray(a_bits).astype(np.uint32)
+    b_bits = np.asarray(b_bits).astype(np.uint32)
+    if dtype == torch.float32:
+        exp_mask, man_mask = 0x7F800000, 0x007FFFFF
+    elif dtype == torch.bfloat16:
+        exp_mask, man_mask = 0x7F80, 0x007F
+    else:
+        exp_mask, man_mask = 0x7C00, 0x03FF
+
+    def isnan(v):
+        return ((v & exp_mask) == exp_mask) & ((v & man_mask) != 0)
+
+    return (a_bits == b_bits) | (isnan(a_bits) & isnan(b_bits))
+

@@ -1,0 +1,258 @@
+"""Pin the oracle (CPU only).
+
+Each oracle function is checked against something independent of its own
+formula: the exhaustive closed form of E2M1 x E8M0, the other dequant
+restatement, the committed golden vectors produced by the transformers
+routines the reference calls, the installed transformers modules themselves,
+and invariants of the MoE layer.  A planted mistake in the oracle (wrong
+nibble order, dropped bias, wrong clamp side, transposed weight) fails at
+least one of these.
+"""
+
+from __future__ import annotations
+
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from blockstreamer_amd import synthetic
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+DTYPES = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+FLT_MAX = float(np.finfo(np.float32).max)
+
+
+def _decode(bits: int, name: str) -> float:
+    if name == "f32":
+        return float(np.array([bits], dtype=np.uint32).view(np.float32)[0])
+    if name == "bf16":
+        return float(np.array([bits << 16], dtype=np.uint32).view(np.float32)[0])
+    return float(np.array([bits], dtype=np.uint16).view(np.float16)[0])
+
+
+@pytest.mark.parametrize("name", list(DTYPES))
+def test_dequant_table_closed_form(name):
+    """Every (code, scale) of the C oracle against value * 2^(s-127)."""
+    tab = oracle.dequant_table_c(DTYPES[name])
+    for s in range(256):
+        for c in range(16):
+            got = _decode(int(tab[s, c]), name)
+            mag = oracle.FP4_VALUES[c]
+            if s == 255:
+                # float32 pow(2, 128) = inf: +-0 * inf = NaN, else +-inf
+                if c in (0, 8):
+                    assert math.isnan(got), (s, c, got)
+                else:
+                    assert math.isinf(got) and math.copysign(1, got) == math.copysign(1, mag)
+                continue
+            exact = math.ldexp(mag, s - 127)  # exact in double
+            if name == "f16":
+                # torch.ldexp on float16 rounds pow(2, s-127) to float16 first
+                p2 = float(np.float16(math.ldexp(1.0, s - 127))) if s - 127 < 16 else math.inf
+                if math.isinf(p2):
+                    want = math.nan if mag == 0 else math.copysign(math.inf, mag)
+                else:
+                    want = float(np.float16(mag * p2))
+                if math.isnan(want):
+                    assert math.isnan(got), (s, c, got)
+                    continue
+            else:
+                want = exact if abs(exact) <= FLT_MAX else math.copysign(math.inf, exact)
+            assert got == want and math.copysign(1, got) == math.copysign(1, want), (name, s, c, got, want)
+
+
+@pytest.mark.parametrize("name", list(DTYPES))
+def test_dequant_c_matches_torch_restatement(name):
+    dt = DTYPES[name]
+    g = torch.Generator().manual_seed(11)
+    blocks = torch.randint(0, 256, (3, 40, 5, 16), generator=g, dtype=torch.uint8)
+    scales = torch.randint(0, 256, (3, 40, 5), generator=g, dtype=torch.uint8)
+    a = oracle.dequant_c(blocks, scales, dt)
+    b = oracle.dequant_torch(blocks, scales, dt)
+    assert a.shape == (3, 160, 40)
+    view = torch.int32 if dt == torch.float32 else torch.int16
+    ok = oracle.bits_equal_or_both_nan(a.view(view).numpy(), b.view(view).numpy(), dt)
+    assert ok.all()
+
+
+def _exhaustive():
+    from tests.golden.make_golden import exhaustive_inputs
+    return exhaustive_inputs()
+
+
+@pytest.mark.parametrize("name", list(DTYPES))
+def test_dequant_oracle_matches_golden_table(name):
+    """Golden vectors written by transformers' convert_moe_packed_tensors."""
+    dt = DTYPES[name]
+    want = np.load(GOLDEN / "dequant_table.npz")[name]
+    blocks, scales = _exhaustive()
+    got = oracle.dequant_c(blocks, scales, dt)[0]
+    view = torch.int32 if dt == torch.float32 else torch.int16
+    ok = oracle.bits_equal_or_both_nan(got.view(view).numpy(), want, dt)
+    assert ok.all(), np.argwhere(~ok)[:5]
+    # nibble order: low nibble -> even column (mxfp4.py:296-304)
+    assert _decode(int(np.uint16(want[0, 127 * 0 + 127]) if name != "f32" else want[0, 127]), name) == 0.0
+
+
+def test_dequantize_expert_ref_contract():
+    """tests/test_offload.py:405-414 restated on the oracle."""
+    g = torch.Generator().manual_seed(0)
+    blocks = torch.randint(0, 255, (64, 4, 16), generator=g, dtype=torch.uint8)
+    scales = torch.randint(120, 134, (64, 4), generator=g, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="packed blocks"):
+        oracle.dequantize_expert_ref(blocks, scales)
+    out = oracle.dequantize_expert_ref(blocks.unsqueeze(0), scales.unsqueeze(0), torch.float32)
+    assert out.shape == (128, 64)
+    # element check against the definition for one byte
+    b = int(blocks[5, 2, 7])
+    s = int(scales[5, 2])
+    assert out[32 * 2 + 14, 5].item() == math.ldexp(oracle.FP4_VALUES[b & 15], s - 127)
+    assert out[32 * 2 + 15, 5].item() == math.ldexp(oracle.FP4_VALUES[b >> 4], s - 127)
+
+
+def test_dequant_matches_transformers_random():
+    tf = pytest.importorskip("transformers.integrations.mxfp4")
+    g = torch.Generator().manual_seed(5)
+    blocks = torch.randint(0, 256, (2, 24, 3, 16), generator=g, dtype=torch.uint8)
+    scales = torch.randint(100, 160, (2, 24, 3), generator=g, dtype=torch.uint8)
+    for dt in DTYPES.values():
+        want = tf.convert_moe_packed_tensors(blocks, scales, dtype=dt)
+        got = oracle.dequant_c(blocks, scales, dt)
+        view = torch.int32 if dt == torch.float32 else torch.int16
+        assert oracle.bits_equal_or_both_nan(got.view(view).numpy(), want.view(view).numpy(), dt).all()
+
+
+# ----------------------------------------------------------------------------- router
+
+def test_topk_softmax_invariants():
+    """Selected set dominates the rest, descending order, softmax ratios."""
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randn(50, 16, generator=g)
+    vals, scores, idx = oracle.topk_softmax_ref(logits, 4)
+    for t in range(50):
+        sel = set(idx[t].tolist())
+        assert len(sel) == 4
+        rest = [logits[t, e].item() for e in range(16) if e not in sel]
+        assert min(logits[t, list(sel)]).item() > max(rest)
+        assert all(vals[t, i] >= vals[t, i + 1] for i in range(3))
+        assert torch.allclose(vals[t], logits[t, idx[t]])
+    assert torch.allclose(scores.sum(-1), torch.ones(50), atol=1e-6)
+    r = scores[:, 0] / scores[:, 1]
+    assert torch.allclose(r, torch.exp(vals[:, 0] - vals[:, 1]), rtol=1e-5)
+
+
+def test_topk_ties_lower_index_first():
+    logits = torch.tensor([[1.0, 3.0, 3.0, 0.5, 3.0]])
+    _, _, idx = oracle.topk_softmax_ref(logits, 2)
+    assert idx.tolist() == [[1, 2]]
+
+
+def test_router_matches_transformers():
+    gpt_oss = pytest.importorskip("transformers.models.gpt_oss.modeling_gpt_oss")
+    from transformers.models.gpt_oss.configuration_gpt_oss import GptOssConfig
+    cfg = GptOssConfig(num_local_experts=32, hidden_size=128, intermediate_size=128,
+                       num_experts_per_tok=4, num_hidden_layers=1)
+    r = gpt_oss.GptOssTopKRouter(cfg)
+    g = torch.Generator().manual_seed(9)
+    with torch.no_grad():
+        r.weight.copy_(torch.randn(32, 128, generator=g) * 0.1)
+        r.bias.copy_(torch.randn(32, generator=g) * 0.1)
+        h = torch.randn(40, 128, generator=g)
+        want = r(h)
+    got = oracle.router_ref(h, r.weight.detach(), r.bias.detach(), 4)
+    assert torch.equal(got[0], want[0])
+    assert torch.equal(got[2], want[2])
+    assert torch.equal(got[1], want[1])
+
+
+# ----------------------------------------------------------------------------- experts
+
+def _tiny():
+    from tests.golden.make_golden import tiny_layer
+    return tiny_layer()
+
+
+def _expert_args(t):
+    return (t["gate_up_proj_blocks"], t["gate_up_proj_scales"], t["gate_up_proj_bias"],
+            t["down_proj_blocks"], t["down_proj_scales"], t["down_proj_bias"])
+
+
+def test_tiny_inputs_regenerate_bit_identically():
+    gold = np.load(GOLDEN / "tiny_layer.npz")
+    from tests.golden.make_golden import digest
+    for k, v in _tiny().items():
+        assert str(gold[f"sha256_{k}"]) == digest(v), k
+
+
+def test_experts_oracle_matches_golden():
+    gold = np.load(GOLDEN / "tiny_layer.npz")
+    t = _tiny()
+    logits, scores, idx = oracle.router_ref(t["hidden"], t["router_weight"], t["router_bias"], 2)
+    assert np.array_equal(idx.numpy(), gold["router_indices"])
+    assert np.array_equal(logits.numpy(), gold["router_logits"])
+    assert np.allclose(scores.numpy(), gold["router_scores"], rtol=0, atol=1e-7)
+    out = oracle.experts_ref(t["hidden"], torch.from_numpy(gold["router_indices"]),
+                             torch.from_numpy(gold["router_scores"]), *_expert_args(t))
+    want = torch.from_numpy(gold["experts_out"])
+    assert torch.equal(out, want)
+
+
+def test_experts_oracle_matches_transformers_dense_twin():
+    gpt_oss = pytest.importorskip("transformers.models.gpt_oss.modeling_gpt_oss")
+    from transformers.models.gpt_oss.configuration_gpt_oss import GptOssConfig
+    from transformers.integrations.mxfp4 import convert_moe_packed_tensors
+    shape = synthetic.MoEShape(6, 3, 96, 64, 20)
+    t = synthetic.moe_layer(shape, seed=21, scale_lo=118, scale_hi=126)
+    idx, w = synthetic.random_routing(20, 6, 3, seed=22, dtype=torch.float32)
+    cfg = GptOssConfig(num_local_experts=6, hidden_size=96, intermediate_size=64,
+                       num_experts_per_tok=3, num_hidden_layers=1)
+    ex = gpt_oss.GptOssExperts(cfg)
+    with torch.no_grad():
+        ex.gate_up_proj.copy_(convert_moe_packed_tensors(t["gate_up_proj_blocks"], t["gate_up_proj_scales"], dtype=torch.float32))
+        ex.gate_up_proj_bias.copy_(t["gate_up_proj_bias"].float())
+        ex.down_proj.copy_(convert_moe_packed_tensors(t["down_proj_blocks"], t["down_proj_scales"], dtype=torch.float32))
+        ex.down_proj_bias.copy_(t["down_proj_bias"].float())
+        want = ex(t["hidden"].float(), idx, w)
+    got = oracle.experts_ref(t["hidden"], idx, w, *_expert_args(t))
+    assert torch.equal(got, want)
+
+
+def test_experts_invariants():
+    shape = synthetic.MoEShape(5, 2, 64, 64, 12)
+    t = synthetic.moe_layer(shape, seed=31, scale_lo=119, scale_hi=125)
+    idx, w = synthetic.random_routing(12, 5, 2, seed=32, dtype=torch.float32)
+    args = _expert_args(t)
+    h = t["hidden"]
+    full = oracle.experts_ref(h, idx, w, *args)
+    # a zero routing weight removes that slot's contribution
+    w0 = w.clone()
+    w0[:, 1] = 0
+    only0 = oracle.experts_ref(h, idx[:, :1], w[:, :1], *args)
+    assert torch.allclose(oracle.experts_ref(h, idx, w0, *args), only0, rtol=1e-6, atol=1e-3)
+    # permuting tokens permutes the output
+    perm = torch.randperm(12, generator=torch.Generator().manual_seed(1))
+    permuted = oracle.experts_ref(h[perm], idx[perm], w[perm], *args)
+    assert torch.allclose(permuted, full[perm], rtol=1e-5, atol=1e-2)
+    # linearity in the routing weights
+    twice = oracle.experts_ref(h, idx, 2 * w, *args)
+    assert torch.allclose(twice, 2 * full, rtol=1e-6, atol=1e-2)
+    # a different bias changes the output by exactly w * bias for that expert's tokens
+    args2 = list(args)
+    args2[5] = args[5] + 1.0
+    shifted = oracle.experts_ref(h, idx, w, *args2)
+    assert torch.allclose(shifted - full, w.sum(-1, keepdim=True).expand_as(full), atol=5e-2)
+
+
+def test_apply_gate_ref_clamps():
+    gu = torch.tensor([[10.0, 10.0, -3.0, -9.0, 0.5, 0.25]])
+    got = oracle.apply_gate_ref(gu)
+    # gate clamps only from above, up on both sides
+    assert torch.allclose(got[0, 0], torch.tensor(7.0 * torch.sigmoid(torch.tensor(7 * 1.702)) * 8.0))
+    g = torch.tensor(-3.0)
+    assert torch.allclose(got[0, 1], g * torch.sigmoid(g * 1.702) * (-6.0))
+    g = torch.tensor(0.5)
+    assert torch.allclose(got[0, 2], g * torch.sigmoid(g * 1.702) * 1.25)
