@@ -28,6 +28,14 @@ _SIGNATURES = {
     "bsa_version": [],
     "bsa_dequant_mxfp4": [_ptr, _ptr, _ptr, _int, _i64, _i64, _i64, _ptr],
     "bsa_dequant_mxfp4_mode": [_ptr, _ptr, _ptr, _int, _i64, _i64, _i64, _int, _ptr],
+    "bsa_moe_workspace_bytes": [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_i64)],
+    "bsa_moe_experts_fwd": [
+        _ptr, _i64, _i64, _i64, _i64, _i64,      # hidden, T, H, I, E, k
+        _ptr, _ptr, _int,                        # indices, weights, weight dtype
+        _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _int,  # gate_up b/s/bias, down b/s/bias, bias dtype
+        _f32, _f32,                              # alpha, limit
+        _ptr, _int, _ptr, _i64, _ptr, _int, _ptr,  # out, out dtype, ws, ws bytes, save, path, stream
+    ],
 }
 _RESTYPE = {"bsa_last_error": ctypes.c_char_p}
 

@@ -1,0 +1,231 @@
+// Token -> expert dispatch and the weighted combine.
+//
+// Dispatch replaces block_streamer/gptoss.py:143-154 (one_hot, permute, sum,
+// nonzero, where, and the gather of hidden rows), which costs three host
+// synchronisations per call.  Here one workgroup builds, on the device, the
+// expert-sorted order of the T*k (token, slot) pairs:
+//   counts[e], offsets[e] (exclusive scan), row_pair[pos] = t*k + p for the
+//   pos-th sorted row, pair_pos[t*k + p] = pos (or -1 for a dropped pair), and
+//   the grouped-GEMM tile list (expert, first row) for tiles of BM rows.
+// Rows of one expert are ordered by pair index (token, then slot), so the
+// layout is deterministic.  Indices outside [0, E) are dropped, like the
+// masking index skipped at gptoss.py:151.
+//
+// Combine replaces gptoss.py:175-176 (scale by the routing weight, then
+// index_add_ into the output): each token gathers its k rows and adds them in
+// ascending expert order (the reference's loop order) in float32, rounding
+// once to the output type.  No atomics, so the result is reproducible.
+#include "bsa_common.h"
+
+namespace bsa {
+
+constexpr int DISPATCH_THREADS = 1024;
+constexpr int DISPATCH_WAVES = DISPATCH_THREADS / 64;
+constexpr int DISPATCH_MAX_E = 1024;
+
+__global__ __launch_bounds__(DISPATCH_THREADS) void moe_dispatch_kernel(
+    const int64_t* __restrict__ idx, int P, int E, int BM, int* __restrict__ counts,
+    int* __restrict__ offsets, int* __restrict__ row_pair, int* __restrict__ pair_pos,
+    int2* __restrict__ tiles, int* __restrict__ num_tiles) {
+  __shared__ int s_cnt[DISPATCH_MAX_E];
+  __shared__ int s_off[DISPATCH_MAX_E];
+  __shared__ int s_run[DISPATCH_MAX_E];
+  __shared__ int s_tile[DISPATCH_MAX_E];
+  __shared__ int s_scan[DISPATCH_THREADS];
+  __shared__ uint8_t s_wc[DISPATCH_WAVES][DISPATCH_MAX_E];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  for (int e = tid; e < E; e += DISPATCH_THREADS) {
+    s_cnt[e] = 0;
+    s_run[e] = 0;
+  }
+  __syncthreads();
+
+  // 1. histogram
+  for (int i = tid; i < P; i += DISPATCH_THREADS) {
+    const int64_t e = idx[i];
+    if (e >= 0 && e < E) atomicAdd(&s_cnt[(int)e], 1);
+  }
+  __syncthreads();
+
+  // 2. exclusive scans of counts and of tile counts (E <= 1024 = one entry per thread)
+  const int my_cnt = tid < E ? s_cnt[tid] : 0;
+  const int my_tiles = (my_cnt + BM - 1) / BM;
+  s_scan[tid] = my_cnt;
+  __syncthreads();
+  for (int off = 1; off < DISPATCH_THREADS; off <<= 1) {
+    const int v = tid >= off ? s_scan[tid - off] : 0;
+    __syncthreads();
+    s_scan[tid] += v;
+    __syncthreads();
+  }
+  const int incl_rows = s_scan[tid];
+  __syncthreads();
+  s_scan[tid] = my_tiles;
+  __syncthreads();
+  for (int off = 1; off < DISPATCH_THREADS; off <<= 1) {
+    const int v = tid >= off ? s_scan[tid - off] : 0;
+    __syncthreads();
+    s_scan[tid] += v;
+    __syncthreads();
+  }
+  const int incl_tiles = s_scan[tid];
+  if (tid < E) {
+    const int start = incl_rows - my_cnt;
+    s_off[tid] = start;
+    s_tile[tid] = incl_tiles - my_tiles;
+    counts[tid] = my_cnt;
+    offsets[tid] = start;
+    if (tid == E - 1) {
+      offsets[E] = incl_rows;
+      *num_tiles = incl_tiles;
+    }
+    for (int j = 0; j < my_tiles; ++j) tiles[incl_tiles - my_tiles + j] = make_int2(tid, start + j * BM);
+  }
+  __syncthreads();
+
+  // 3. stable placement, DISPATCH_THREADS pairs per round
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int base = 0; base < P; base += DISPATCH_THREADS) {
+    const int i = base + tid;
+    int e = -1;
+    if (i < P) {
+      const int64_t v = idx[i];
+      e = (v >= 0 && v < E) ? (int)v : -1;
+    }
+    // lanes of this wave holding the same expert id (ids < 1024: 10 bits + valid bit)
+    uint64_t same = __ballot(e >= 0);
+    if (e < 0) same = ~same;
+#pragma unroll
+    for (int b = 0; b < 10; ++b) {
+      const uint64_t m = __ballot((e >> b) & 1);
+      same &= ((e >> b) & 1) ? m : ~m;
+    }
+    const int local_rank = __popcll(same & lt_mask);
+    const int wave_cnt = __popcll(same);
+    for (int j = tid; j < DISPATCH_WAVES * E; j += DISPATCH_THREADS)
+      s_wc[j / E][j % E] = 0;
+    __syncthreads();
+    if (e >= 0 && local_rank == 0) s_wc[wave][e] = (uint8_t)wave_cnt;
+    __syncthreads();
+    if (i < P) {
+      if (e >= 0) {
+        int prefix = 0;
+        for (int w = 0; w < wave; ++w) prefix += s_wc[w][e];
+        const int pos = s_off[e] + s_run[e] + prefix + local_rank;
+        row_pair[pos] = i;
+        pair_pos[i] = pos;
+      } else {
+        pair_pos[i] = -1;
+      }
+    }
+    __syncthreads();
+    for (int ee = tid; ee < E; ee += DISPATCH_THREADS) {
+      int add = 0;
+      for (int w = 0; w < DISPATCH_WAVES; ++w) add += s_wc[w][ee];
+      s_run[ee] += add;
+    }
+    __syncthreads();
+  }
+}
+
+__device__ __forceinline__ float load_f32(const void* p, int64_t i, int dtype) {
+  if (dtype == DT_F32) return static_cast<const float*>(p)[i];
+  const uint32_t b = static_cast<const uint16_t*>(p)[i];
+  if (dtype == DT_BF16) return __uint_as_float(b << 16);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+}
+
+__device__ __forceinline__ void store_f32_as(void* p, int64_t i, float v, int dtype) {
+  if (dtype == DT_F32) {
+    static_cast<float*>(p)[i] = v;
+  } else if (dtype == DT_BF16) {
+    static_cast<uint16_t*>(p)[i] = (uint16_t)f32_to_bf16_bits(v);
+  } else {
+    static_cast<uint16_t*>(p)[i] = (uint16_t)f32_to_f16_bits(v);
+  }
+}
+
+constexpr int COMBINE_MAX_K = 16;
+
+// out[t][h] = sum over valid slots p of w[t,p] * Y[pair_pos[t*k+p]][h], slots
+// taken in ascending expert order.  Y is float32 [P, H].  One workgroup per
+// token; each thread handles 4 adjacent columns.
+__global__ __launch_bounds__(256) void moe_combine_kernel(
+    const float* __restrict__ Y, const int64_t* __restrict__ idx, const void* __restrict__ w,
+    int w_dtype, const int* __restrict__ pair_pos, int T, int k, int H, void* __restrict__ out,
+    int out_dtype) {
+  const int t = blockIdx.x;
+  int pos[COMBINE_MAX_K];
+  float wt[COMBINE_MAX_K];
+  int64_t ex[COMBINE_MAX_K];
+  int n = 0;
+  for (int p = 0; p < k; ++p) {
+    const int ps = pair_pos[(int64_t)t * k + p];
+    if (ps < 0) continue;
+    const int64_t e = idx[(int64_t)t * k + p];
+    const float wv = load_f32(w, (int64_t)t * k + p, w_dtype);
+    // insertion by expert id (ties keep slot order)
+    int j = n;
+    while (j > 0 && ex[j - 1] > e) {
+      ex[j] = ex[j - 1];
+      pos[j] = pos[j - 1];
+      wt[j] = wt[j - 1];
+      --j;
+    }
+    ex[j] = e;
+    pos[j] = ps;
+    wt[j] = wv;
+    ++n;
+  }
+  const int64_t obase = (int64_t)t * H;
+  if ((H & 3) == 0) {
+    for (int h = threadIdx.x * 4; h < H; h += blockDim.x * 4) {
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int j = 0; j < n; ++j) {
+        const float4 y = *reinterpret_cast<const float4*>(Y + (int64_t)pos[j] * H + h);
+        acc.x += wt[j] * y.x;
+        acc.y += wt[j] * y.y;
+        acc.z += wt[j] * y.z;
+        acc.w += wt[j] * y.w;
+      }
+      if (out_dtype == DT_BF16) {
+        uint2 v = make_uint2(pack_bf16x2(acc.x, acc.y), pack_bf16x2(acc.z, acc.w));
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + obase + h) = v;
+      } else {
+        store_f32_as(out, obase + h, acc.x, out_dtype);
+        store_f32_as(out, obase + h + 1, acc.y, out_dtype);
+        store_f32_as(out, obase + h + 2, acc.z, out_dtype);
+        store_f32_as(out, obase + h + 3, acc.w, out_dtype);
+      }
+    }
+  } else {
+    for (int h = threadIdx.x; h < H; h += blockDim.x) {
+      float acc = 0.f;
+      for (int j = 0; j < n; ++j) acc += wt[j] * Y[(int64_t)pos[j] * H + h];
+      store_f32_as(out, obase + h, acc, out_dtype);
+    }
+  }
+}
+
+int launch_dispatch(const int64_t* idx, int P, int E, int BM, int* counts, int* offsets,
+                    int* row_pair, int* pair_pos, int2* tiles, int* num_tiles, hipStream_t st) {
+  hipLaunchKernelGGL(moe_dispatch_kernel, dim3(1), dim3(DISPATCH_THREADS), 0, st, idx, P, E, BM,
+                     counts, offsets, row_pair, pair_pos, tiles, num_tiles);
+  BSA_LAUNCH_CHECK("dispatch launch");
+  return BSA_OK;
+}
+
+int launch_combine(const float* Y, const int64_t* idx, const void* w, int w_dtype,
+                   const int* pair_pos, int T, int k, int H, void* out, int out_dtype,
+                   hipStream_t st) {
+  if (T == 0) return BSA_OK;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3(T), dim3(256), 0, st, Y, idx, w, w_dtype, pair_pos,
+                     T, k, H, out, out_dtype);
+  BSA_LAUNCH_CHECK("combine launch");
+  return BSA_OK;
+}
+
+}  // namespace bsa

@@ -4,13 +4,21 @@ Same public names, signatures, parameter names and error behaviour as
 block_streamer/gptoss.py:1-189, so ``StreamedModel``'s ``functional_call``
 binding (streamer.py:151-180), the LoRA recompute backward
 (_autograd.py:125-175) and ``install_mxfp4_experts`` callers work unchanged.
-The arithmetic runs in hand-written gfx950 HIP kernels (``libbsamd.so``).
+The arithmetic runs in hand-written gfx950 HIP kernels (``libbsamd.so``):
+
+* ``MXFP4Experts.forward`` is one device-side dispatch, two grouped GEMMs
+  that decode MXFP4 on the fly (bias and clamped SwiGLU fused), and a
+  combine -- no host synchronisation and no dense weight in memory;
+* ``dequantize_expert`` is the dequant kernel, bit-exact with the reference.
+
+The module reads its parameters at every call and never caches device
+pointers or mutates them (the StreamedModel contract, streamer.py:159-174).
 """
 
 from __future__ import annotations
 
 import torch
-from torch import Tensor
+from torch import Tensor, nn
 
 from . import kernels
 
@@ -31,3 +39,152 @@ def dequantize_expert(
         )
     dense = kernels.dequantize_mxfp4(blocks, scales, dtype)
     return dense.squeeze(0)
+
+
+class _MXFP4Matmul(torch.autograd.Function):
+    """x @ dequantize(blocks, scales), re-dequantizing in backward.
+
+    block_streamer/gptoss.py:45-71.  Only the packed tensors are saved, so the
+    dense weight is a temporary in both directions; backward returns dX only.
+    """
+
+    @staticmethod
+    def forward(ctx, x: Tensor, blocks: Tensor, scales: Tensor) -> Tensor:
+        weight = dequantize_expert(blocks, scales, x.dtype)
+        ctx.save_for_backward(x, blocks, scales)
+        return x @ weight
+
+    @staticmethod
+    def backward(ctx, grad: Tensor) -> tuple[Tensor | None, None, None]:
+        x, blocks, scales = ctx.saved_tensors
+        grad_x = None
+        if ctx.needs_input_grad[0]:
+            weight = dequantize_expert(blocks, scales, x.dtype)
+            grad_x = grad @ weight.transpose(-2, -1)
+        return grad_x, None, None
+
+
+def mxfp4_matmul(x: Tensor, blocks: Tensor, scales: Tensor) -> Tensor:
+    """block_streamer/gptoss.py:74-75."""
+    return _MXFP4Matmul.apply(x, blocks, scales)
+
+
+class _MoEExperts(torch.autograd.Function):
+    """Fused expert forward; backward gives d(hidden) and d(routing weights).
+
+    Saves the packed weights (already resident as the block's staged state),
+    the inputs, the device-side dispatch and the gate_up pre-activations --
+    never a dense weight (the rationale of block_streamer/gptoss.py:46-56).
+    """
+
+    @staticmethod
+    def forward(ctx, hidden, router_indices, routing_weights, gu_blocks, gu_scales, gu_bias,
+                dn_blocks, dn_scales, dn_bias, alpha, limit):
+        needs = ctx.needs_input_grad[0] or ctx.needs_input_grad[2]
+        if needs:
+            out, ws, pre = kernels.moe_experts_forward(
+                hidden, router_indices, routing_weights, gu_blocks, gu_scales, gu_bias,
+                dn_blocks, dn_scales, dn_bias, alpha, limit, save=True)
+            ctx.save_for_backward(hidden, router_indices, routing_weights, gu_blocks, gu_scales,
+                                  gu_bias, dn_blocks, dn_scales, dn_bias, ws, pre)
+            ctx.alpha, ctx.limit = alpha, limit
+        else:
+            out = kernels.moe_experts_forward(
+                hidden, router_indices, routing_weights, gu_blocks, gu_scales, gu_bias,
+                dn_blocks, dn_scales, dn_bias, alpha, limit)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        (hidden, idx, w, gu_b, gu_s, gu_bias, dn_b, dn_s, dn_bias, ws,
+         pre) = ctx.saved_tensors
+        grad_h, grad_w = kernels.moe_experts_backward(
+            grad_out, hidden, idx, w, gu_b, gu_s, dn_b, dn_s, ws, pre, ctx.alpha, ctx.limit,
+            need_hidden=ctx.needs_input_grad[0], need_weights=ctx.needs_input_grad[2])
+        return grad_h, None, grad_w, None, None, None, None, None, None, None, None
+
+
+class MXFP4Experts(nn.Module):
+    """Drop-in for ``GptOssExperts`` whose weights stay packed until used.
+
+    block_streamer/gptoss.py:78-177.  Parameter names match the checkpoint
+    exactly, so the shard manifest needs no renaming and the streamed state
+    binds straight through.  As in the reference, the meta shapes use
+    ``hidden_size // 32`` groups for both projections (gptoss.py:92); the
+    kernels take their shapes from the bound tensors.
+    """
+
+    def __init__(self, config, dtype: torch.dtype = torch.bfloat16) -> None:
+        super().__init__()
+        self.num_experts = config.num_local_experts
+        self.hidden_size = config.hidden_size
+        self.expert_dim = config.intermediate_size
+        self.alpha = 1.702
+        self.limit = getattr(config, "swiglu_limit", 7.0)
+        groups = self.hidden_size // 32
+
+        def packed(rows: int) -> nn.Parameter:
+            return nn.Parameter(
+                torch.empty(self.num_experts, rows, groups, 16, dtype=torch.uint8, device="meta"),
+                requires_grad=False,
+            )
+
+        def scale(rows: int) -> nn.Parameter:
+            return nn.Parameter(
+                torch.empty(self.num_experts, rows, groups, dtype=torch.uint8, device="meta"),
+                requires_grad=False,
+            )
+
+        self.gate_up_proj_blocks = packed(2 * self.expert_dim)
+        self.gate_up_proj_scales = scale(2 * self.expert_dim)
+        self.gate_up_proj_bias = nn.Parameter(
+            torch.empty(self.num_experts, 2 * self.expert_dim, dtype=dtype, device="meta"),
+            requires_grad=False,
+        )
+        self.down_proj_blocks = packed(self.hidden_size)
+        self.down_proj_scales = scale(self.hidden_size)
+        self.down_proj_bias = nn.Parameter(
+            torch.empty(self.num_experts, self.hidden_size, dtype=dtype, device="meta"),
+            requires_grad=False,
+        )
+
+    def _apply_gate(self, gate_up: Tensor) -> Tensor:
+        """block_streamer/gptoss.py:130-135 (the fused kernels apply it in-register)."""
+        gate, up = gate_up[..., ::2], gate_up[..., 1::2]
+        gate = gate.clamp(max=self.limit)
+        up = up.clamp(min=-self.limit, max=self.limit)
+        glu = gate * torch.sigmoid(gate * self.alpha)
+        return (up + 1) * glu
+
+    def forward(
+        self,
+        hidden_states: Tensor,
+        router_indices: Tensor | None = None,
+        routing_weights: Tensor | None = None,
+    ) -> Tensor:
+        if router_indices is None or routing_weights is None:
+            raise ValueError("MXFP4Experts.forward needs router_indices and routing_weights")
+        shape = hidden_states.shape
+        flat = hidden_states.reshape(-1, shape[-1])
+        out = _MoEExperts.apply(
+            flat, router_indices, routing_weights,
+            self.gate_up_proj_blocks, self.gate_up_proj_scales, self.gate_up_proj_bias,
+            self.down_proj_blocks, self.down_proj_scales, self.down_proj_bias,
+            float(self.alpha), float(self.limit),
+        )
+        return out.reshape(shape)
+
+
+def install_mxfp4_experts(model: nn.Module, config, dtype=torch.bfloat16) -> int:
+    """Swap every dense GptOssExperts for the packed, fused version.
+
+    block_streamer/gptoss.py:180-189; returns the number of layers replaced.
+    """
+    from transformers.models.gpt_oss import modeling_gpt_oss as gpt_oss
+
+    replaced = 0
+    for layer in model.model.layers:
+        if isinstance(layer.mlp.experts, gpt_oss.GptOssExperts):
+            layer.mlp.experts = MXFP4Experts(config, dtype)
+            replaced += 1
+    return replaced

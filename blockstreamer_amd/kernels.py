@@ -46,3 +46,85 @@ def dequantize_mxfp4(blocks: Tensor, scales: Tensor, dtype: torch.dtype = torch.
         _lib.call("bsa_dequant_mxfp4_mode", blocks.data_ptr(), scales.data_ptr(), out.data_ptr(),
                   code, E, R, G, mode, _lib.stream_handle(dev))
     return out
+
+
+PATHS = {"auto": 0, "stream": 1, "tiled": 2}
+
+
+def moe_workspace_bytes(T: int, H: int, I: int, E: int, k: int) -> int:
+    import ctypes
+    out = ctypes.c_int64(0)
+    _lib.call("bsa_moe_workspace_bytes", T, H, I, E, k, ctypes.byref(out))
+    return out.value
+
+
+def _aligned_bytes(nbytes: int, device, align: int = 256) -> Tensor:
+    buf = torch.empty(nbytes + align, dtype=torch.uint8, device=device)
+    off = (-buf.data_ptr()) % align
+    return buf[off:off + nbytes]
+
+
+def _check_packed(blocks: Tensor, scales: Tensor, E: int, rows: int, K: int, what: str) -> None:
+    want = (E, rows, K // 32, 16)
+    if tuple(blocks.shape) != want:
+        raise ValueError(f"{what}_blocks must be {list(want)}, got {list(blocks.shape)}")
+    if tuple(scales.shape) != want[:3]:
+        raise ValueError(f"{what}_scales must be {list(want[:3])}, got {list(scales.shape)}")
+
+
+def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights: Tensor,
+                        gate_up_blocks: Tensor, gate_up_scales: Tensor, gate_up_bias: Tensor | None,
+                        down_blocks: Tensor, down_scales: Tensor, down_bias: Tensor | None,
+                        alpha: float = 1.702, limit: float = 7.0, *, save: bool = False,
+                        path: str = "auto"):
+    """Fused MoE experts forward (block_streamer/gptoss.py:137-177).
+
+    ``hidden [T, H]``, ``router_indices [T, k]``, ``routing_weights [T, k]``;
+    packed experts in the checkpoint layout.  Returns ``out [T, H]`` in the
+    dtype of ``hidden``; with ``save=True`` also ``(workspace, gate_up_pre)``
+    for the input-gradient backward.  Activations enter the MFMA as bfloat16.
+    """
+    if hidden.dim() != 2:
+        raise ValueError(f"hidden_states must be [tokens, hidden], got {tuple(hidden.shape)}")
+    if router_indices.dim() != 2 or router_indices.shape[0] != hidden.shape[0]:
+        raise ValueError("router_indices must be [tokens, top_k]")
+    if tuple(routing_weights.shape) != tuple(router_indices.shape):
+        raise ValueError("routing_weights must match router_indices in shape")
+    T, H = hidden.shape
+    k = router_indices.shape[1]
+    E = gate_up_blocks.shape[0]
+    I = gate_up_blocks.shape[1] // 2
+    _check_packed(gate_up_blocks, gate_up_scales, E, 2 * I, H, "gate_up_proj")
+    _check_packed(down_blocks, down_scales, E, H, I, "down_proj")
+    dev = _lib.require_gpu(hidden, router_indices, routing_weights, gate_up_blocks,
+                           gate_up_scales, down_blocks, down_scales, gate_up_bias, down_bias)
+    out_dtype = hidden.dtype
+    out_code = _lib.dtype_code(out_dtype)
+    x = hidden if hidden.dtype == torch.bfloat16 else hidden.to(torch.bfloat16)
+    x = x.contiguous()
+    idx = router_indices.to(torch.int64).contiguous()
+    w = routing_weights.contiguous()
+    w_code = _lib.dtype_code(w.dtype)
+    bias_dtype = (gate_up_bias if gate_up_bias is not None else down_bias)
+    bias_code = _lib.dtype_code(bias_dtype.dtype) if bias_dtype is not None else 0
+    gub = gate_up_bias.to(bias_dtype.dtype).contiguous() if gate_up_bias is not None else None
+    dnb = down_bias.to(bias_dtype.dtype).contiguous() if down_bias is not None else None
+    gu_b, gu_s = _as_u8(gate_up_blocks), _as_u8(gate_up_scales)
+    dn_b, dn_s = _as_u8(down_blocks), _as_u8(down_scales)
+    out = torch.empty((T, H), dtype=out_dtype, device=dev)
+    ws_bytes = moe_workspace_bytes(T, H, I, E, k)
+    ws = _aligned_bytes(ws_bytes, dev)
+    save_pre = torch.empty((T * k, 2 * I), dtype=torch.float32, device=dev) if save else None
+
+    def ptr(t):
+        return t.data_ptr() if t is not None else None
+
+    with torch.cuda.device(dev):
+        _lib.call("bsa_moe_experts_fwd", x.data_ptr(), T, H, I, E, k, idx.data_ptr(),
+                  w.data_ptr(), w_code, gu_b.data_ptr(), gu_s.data_ptr(), ptr(gub),
+                  dn_b.data_ptr(), dn_s.data_ptr(), ptr(dnb), bias_code, float(alpha),
+                  float(limit), out.data_ptr(), out_code, ws.data_ptr(), ws_bytes,
+                  ptr(save_pre), PATHS[path], _lib.stream_handle(dev))
+    if save:
+        return out, ws, save_pre
+    return out

@@ -71,6 +71,49 @@ int bsa_dequant_mxfp4_mode(const void *blocks, const void *scales, void *out,
                            int out_dtype, int64_t E, int64_t R, int64_t G,
                            int mode, void *stream);
 
+/*
+ * Bytes of workspace bsa_moe_experts_fwd needs for T tokens, hidden H,
+ * intermediate I, E experts and top-k k (written to *bytes).  No reference
+ * counterpart: the reference allocates per expert inside its loop.
+ */
+int bsa_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
+                            int64_t k, int64_t *bytes);
+
+/*
+ * Fused MoE expert forward.
+ *
+ * Replaces block_streamer/gptoss.py:137-177 (MXFP4Experts.forward: dispatch
+ * :143-154, per-expert mxfp4_matmul + bias :158-165 and :167-174, clamped
+ * SwiGLU :130-135 / :166, routing-weight scale and index_add_ :175-176).
+ *
+ *   hidden          bf16 [T, H] (16-byte aligned)
+ *   router_indices  int64 [T, k]; entries outside [0, E) are dropped
+ *   routing_weights weight_dtype [T, k]
+ *   gate_up_blocks  uint8 [E, 2I, H/32, 16], gate_up_scales uint8 [E, 2I, H/32]
+ *   gate_up_bias    bias_dtype [E, 2I] (may be NULL)
+ *   down_blocks     uint8 [E, H, I/32, 16],  down_scales uint8 [E, H, I/32]
+ *   down_bias       bias_dtype [E, H] (may be NULL)
+ *   out             out_dtype [T, H]
+ *   workspace       >= bsa_moe_workspace_bytes(...) bytes, 256-byte aligned;
+ *                   holds the expert-sorted dispatch and intermediates, and is
+ *                   what a later backward reads
+ *   save_gate_up    optional float32 [T*k, 2I]: gate_up pre-activations in
+ *                   expert-sorted row order, for the backward
+ *   path            0 = automatic, 1 = weight-streaming kernel, 2 = tiled kernel
+ *
+ * Gate and up columns are interleaved (gate = even, up = odd), alpha and
+ * limit parameterise the clamped SwiGLU.  Each token's k contributions are
+ * summed in ascending expert order in float32 and rounded once.
+ */
+int bsa_moe_experts_fwd(
+    const void *hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+    const int64_t *router_indices, const void *routing_weights,
+    int weight_dtype, const void *gate_up_blocks, const void *gate_up_scales,
+    const void *gate_up_bias, const void *down_blocks, const void *down_scales,
+    const void *down_bias, int bias_dtype, float alpha, float limit, void *out,
+    int out_dtype, void *workspace, int64_t workspace_bytes,
+    void *save_gate_up, int path, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
