@@ -143,13 +143,176 @@ def bench_dequant(args) -> dict:
     }
 
 
+# ----------------------------------------------------------------------------- MoE layer
+
+GPTOSS_120B = dict(E=128, k=4, H=2880, I=2880)
+BF16_PEAK_TFLOPS = 2500.0
+MXFP4_PEAK_TFLOPS = 10100.0
+
+
+def expert_bytes(H: int, I: int) -> int:
+    """Packed weights, scales and bf16 biases of one expert (both projections)."""
+    gu = 2 * I * (H // 32) * 17 + 2 * I * 2
+    dn = H * (I // 32) * 17 + H * 2
+    return gu + dn
+
+
+def moe_flops(T: int, k: int, H: int, I: int) -> int:
+    return 2 * T * k * (H * 2 * I + I * H)
+
+
+def _median_ms(pairs):
+    return statistics.median([a.elapsed_time(b) for a, b in pairs])
+
+
+def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int) -> dict:
+    import torch.nn.functional as F
+
+    from blockstreamer_amd import kernels, synthetic
+
+    dev = torch.device("cuda", 0)
+    E, k, H, I = (GPTOSS_120B[x] for x in ("E", "k", "H", "I"))
+    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=seed, scale_lo=115,
+                            scale_hi=131, router_bias_std=router_bias_std, device=dev)
+    x = t["hidden"]
+    args = tuple(t[n] for n in ("gate_up_proj_blocks", "gate_up_proj_scales", "gate_up_proj_bias",
+                                "down_proj_blocks", "down_proj_scales", "down_proj_bias"))
+
+    def route():
+        # the reference router (TF modeling_gpt_oss.py:126-131) as torch ops
+        logits = F.linear(x, t["router_weight"], t["router_bias"])
+        vals, idx = torch.topk(logits, k, dim=-1)
+        return idx, torch.softmax(vals, dim=1, dtype=vals.dtype)
+
+    def step():
+        idx, w = route()
+        return kernels.moe_experts_forward(x, idx, w, *args)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    # per-stage HIP events on the launch stream (a separate pass, so the
+    # events do not sit inside the timed layer steps above)
+    idx, w = route()
+    hit = int(torch.unique(idx).numel())
+    st = kernels.MoEStages(x, idx, w, *args)
+    names = ("route", "dispatch", "gate_up", "down", "combine")
+    ev = {n: [] for n in names}
+    for _ in range(max(steps, 5)):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+        e[0].record()
+        route()
+        e[1].record()
+        st.dispatch()
+        e[2].record()
+        st.gate_up()
+        e[3].record()
+        st.down()
+        e[4].record()
+        st.combine()
+        e[5].record()
+        for i, n in enumerate(names):
+            ev[n].append((e[i], e[i + 1]))
+    torch.cuda.synchronize()
+    ms = {n: round(_median_ms(ev[n]), 4) for n in names}
+    gemm_ms = ms["gate_up"] + ms["down"]
+    flops = moe_flops(T, k, H, I)
+    wbytes = hit * expert_bytes(H, I)
+    res = {
+        "tokens": T,
+        "tokens_per_s": round(T * steps / wall, 1),
+        "ms_per_layer": round(wall / steps * 1e3, 4),
+        "stage_ms": ms,
+        "hit_experts": hit,
+    }
+    hbm = wbytes / (gemm_ms / 1e3) / 1e9
+    tfl = flops / (gemm_ms / 1e3) / 1e12
+    if T * k <= 16 * E:
+        res["roofline"] = {"bound": "hbm", "achieved": round(hbm, 1), "peak": HBM_PEAK_GBS,
+                           "unit": "GB/s", "frac": round(hbm / HBM_PEAK_GBS, 4),
+                           "kernel": "moe_stream_kernel gate_up + down",
+                           "algorithmic_bytes": wbytes}
+    else:
+        res["roofline"] = {"bound": "mfma", "achieved": round(tfl, 1), "peak": BF16_PEAK_TFLOPS,
+                           "unit": "TFLOP/s", "frac": round(tfl / BF16_PEAK_TFLOPS, 4),
+                           "frac_of_mxfp4_peak": round(tfl / MXFP4_PEAK_TFLOPS, 4),
+                           "kernel": "moe_tiled_kernel gate_up + down",
+                           "algorithmic_flops": flops}
+    return res
+
+
+def cpu_baseline_moe(T: int = 64, sample: int = 4) -> dict:
+    """Oracle (fp32 torch restatement of the reference) on a few decode tokens."""
+    import oracle
+    from blockstreamer_amd import synthetic
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    E, k, H, I = (GPTOSS_120B[x] for x in ("E", "k", "H", "I"))
+    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=4, scale_lo=115,
+                            scale_hi=131, router_bias_std=0.5)
+    h = t["hidden"][:sample]
+    args = tuple(t[n] for n in ("gate_up_proj_blocks", "gate_up_proj_scales", "gate_up_proj_bias",
+                                "down_proj_blocks", "down_proj_scales", "down_proj_bias"))
+    times = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        _, scores, idx = oracle.router_ref(h, t["router_weight"], t["router_bias"], k)
+        oracle.experts_ref(h, idx, scores, *args)
+        times.append(time.perf_counter() - t0)
+    tm = min(times)
+    return {"value": round(sample / tm, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{sample} tokens of the 64-token gpt-oss-120b decode batch, router + "
+                      f"experts in float32 (per-expert dequant + GEMMs), best of 2 ({tm:.2f} s)"}
+
+
+def bench_copy(steps: int, warmup: int) -> dict:
+    """torch device-to-device copy of 2 GiB: 4 GiB of HBM traffic per step."""
+    dev = torch.device("cuda", 0)
+    src = torch.empty(2 << 30, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return {"bytes_per_step": 2 * src.numel(), "GB_per_s": round(2 * src.numel() * steps / wall / 1e9, 1),
+            "ms_per_step": round(wall / steps * 1e3, 4)}
+
+
+def focused(args) -> int:
+    if args.workload == "copy":
+        res = bench_copy(args.steps, args.warmup)
+    elif args.workload == "moe_decode":
+        res = bench_moe(64, args.steps, args.warmup, 0.5, seed=4)
+    else:
+        res = bench_moe(8192, args.steps, args.warmup, 0.0, seed=5)
+    print(json.dumps({"workload": args.workload, "steps": args.steps, "warmup": args.warmup, **res}),
+          flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="dequant", choices=["dequant"])
+    ap.add_argument("--workload", default="dequant",
+                    choices=["dequant", "moe_decode", "moe_prefill", "copy"],
+                    help="dequant: the headline line (plus MoE layer results); moe_decode / "
+                         "moe_prefill: one MoE workload alone; copy: a plain 2 GiB device copy "
+                         "that calibrates the HBM byte counters")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-moe", action="store_true", help="skip the MoE layer measurements")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs the MoE expert path on a "
@@ -158,6 +321,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
+    if args.workload != "dequant":
+        return focused(args)
     res = bench_dequant(args)
     line = {
         "metric": res["metric"],
@@ -176,6 +341,14 @@ def main() -> int:
         "roofline": res["roofline"],
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_dequant(),
     }
+    if not args.no_moe:
+        moe = {
+            "decode_t64": bench_moe(64, max(args.steps, 20), args.warmup, 0.5, seed=4),
+            "prefill_t8192": bench_moe(8192, max(args.steps // 4, 5), args.warmup, 0.0, seed=5),
+        }
+        if not args.no_cpu_baseline:
+            moe["decode_t64"]["cpu_baseline"] = cpu_baseline_moe()
+        line["moe_layer"] = moe
     print(json.dumps(line), flush=True)
     return 0
 

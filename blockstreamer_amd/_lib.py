@@ -36,6 +36,12 @@ _SIGNATURES = {
         _f32, _f32,                              # alpha, limit
         _ptr, _int, _ptr, _i64, _ptr, _int, _ptr,  # out, out dtype, ws, ws bytes, save, path, stream
     ],
+    "bsa_moe_dispatch": [_ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr],
+    "bsa_moe_gate_up": [_ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr, _int, _f32, _f32,
+                        _ptr, _i64, _ptr, _int, _ptr],
+    "bsa_moe_down": [_i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr, _int, _ptr, _i64, _int, _ptr],
+    "bsa_moe_combine": [_ptr, _ptr, _int, _i64, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _int,
+                        _ptr],
 }
 _RESTYPE = {"bsa_last_error": ctypes.c_char_p}
 

@@ -77,12 +77,37 @@ __device__ __forceinline__ f32x16_t mfma32(s16x8_t a, s16x8_t b, f32x16_t c) {
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-// 8 MXFP4 codes (4 packed bytes) -> 8 bf16 in code order.
+// 8 MXFP4 codes (4 packed bytes) -> 8 bf16 in code order.  HW: the gfx950
+// converter, valid when no scale byte in play is 255 (callers make that
+// decision uniform across the wave); otherwise the integer decoder.
+template <bool HW>
 __device__ __forceinline__ s16x8_t decode8(uint32_t q, uint32_t s) {
   uint32_t d[4];
-  mx_dword_to_bf16x8(q, s, mx_scale_hw_ok(s), d);
+  if constexpr (HW) {
+    const float sf = mx_scale_f32(s);
+    d[0] = mx_byte_to_bf16x2_hw<0>(q, sf);
+    d[1] = mx_byte_to_bf16x2_hw<1>(q, sf);
+    d[2] = mx_byte_to_bf16x2_hw<2>(q, sf);
+    d[3] = mx_byte_to_bf16x2_hw<3>(q, sf);
+  } else {
+    mx_dword_to_bf16x8(q, s, false, d);
+  }
   u32x4_t v = {d[0], d[1], d[2], d[3]};
   return __builtin_bit_cast(s16x8_t, v);
+}
+
+// 8 codes with the converter, redone by the integer decoder in the rare
+// lanes whose scale byte is 255 (the converter's NaN code).
+__device__ __forceinline__ s16x8_t decode8_fix(uint32_t q, uint32_t s) {
+  s16x8_t v = decode8<true>(q, s);
+  if (__builtin_expect(s == 0xFFu, 0)) v = decode8<false>(q, s);
+  return v;
+}
+
+// true if any byte of w is 0xFF
+__device__ __forceinline__ bool has_ff_byte(uint32_t w) {
+  return ((w & 0xFFu) == 0xFFu) | ((w & 0xFF00u) == 0xFF00u) | ((w & 0xFF0000u) == 0xFF0000u) |
+         ((w & 0xFF000000u) == 0xFF000000u);
 }
 
 __device__ __forceinline__ float bias_at(const void* bias, int dtype, int64_t i) {
@@ -126,11 +151,13 @@ __device__ __forceinline__ u32x4_t load16(const uint8_t* p) {
 // Epilogue shared by both kernels: one output element pair (SwiGLU) or one
 // element, for sorted row pos and weight-row index n.
 // ---------------------------------------------------------------------------
+// Bias values are loaded once per lane before the K loop (each lane owns
+// fixed columns) and passed in, so the epilogue issues no dependent loads.
 template <int EPI>
-__device__ __forceinline__ void epilogue_swiglu(const GemmArgs& a, int e, int64_t pos, int n_gate,
-                                                float accg, float accu) {
-  const float g = accg + bias_at(a.bias, a.bias_dtype, (int64_t)e * a.N + n_gate);
-  const float u = accu + bias_at(a.bias, a.bias_dtype, (int64_t)e * a.N + n_gate + 1);
+__device__ __forceinline__ void epilogue_swiglu(const GemmArgs& a, int64_t pos, int n_gate,
+                                                float accg, float accu, float bg, float bu) {
+  const float g = accg + bg;
+  const float u = accu + bu;
   if (a.save_pre) {
     float2* sp = reinterpret_cast<float2*>(a.save_pre + pos * a.N + n_gate);
     *sp = make_float2(g, u);
@@ -140,8 +167,9 @@ __device__ __forceinline__ void epilogue_swiglu(const GemmArgs& a, int e, int64_
 }
 
 template <int EPI>
-__device__ __forceinline__ void epilogue_one(const GemmArgs& a, int e, int64_t pos, int n, float acc) {
-  const float v = acc + bias_at(a.bias, a.bias_dtype, (int64_t)e * a.N + n);
+__device__ __forceinline__ void epilogue_one(const GemmArgs& a, int64_t pos, int n, float acc,
+                                             float b) {
+  const float v = acc + b;
   if constexpr (EPI == EPI_BIAS_F32)
     static_cast<float*>(a.out)[pos * a.ldo + n] = v;
   else
@@ -150,19 +178,113 @@ __device__ __forceinline__ void epilogue_one(const GemmArgs& a, int e, int64_t p
 
 // ---------------------------------------------------------------------------
 // Weight-streaming kernel (decode).
+//
+// One workgroup per (expert, 32 consecutive weight rows).  The slice is one
+// contiguous 32*K/2-byte span, copied to LDS at once.  K is walked in steps
+// of 4 scale groups (128 k); in a step, the lane with column col = lane%16
+// and quarter c = lane/16 decodes all 32 codes of group 4*step + c of its
+// weight row (one 16-byte LDS read, one scale byte) and feeds them to four
+// v_mfma_f32_16x16x32_bf16, whose k slots it fills with that group's codes
+// [8m, 8m+8) for m = 0..3; the A lanes of quarter c read the same k.  The
+// four waves take alternate steps and are summed through LDS.  Gate/up
+// columns of the gate_up projection are adjacent lanes; the SwiGLU pairs
+// them with one lane exchange.
 // ---------------------------------------------------------------------------
-constexpr int ST_BN = 32;     // weight rows (output columns) per workgroup
-constexpr int ST_MAXRB = 2;   // 16-row blocks per pass
-constexpr int ST_PF = 8;      // A prefetch distance (k-steps)
+constexpr int ST_BN = 32;  // weight rows (output columns) per workgroup
 
-__host__ __device__ inline int st_lds_row(int K) { return K / 2 + 16; }
 inline size_t st_smem_bytes(int K) {
-  const size_t b = (size_t)ST_BN * st_lds_row(K) + (size_t)ST_BN * (K / 32);
-  const size_t red = (size_t)4 * ST_MAXRB * 2 * 64 * sizeof(f32x4_t);
+  const size_t b = (size_t)ST_BN * (K / 2) + (size_t)ST_BN * (K / 32);
+  const size_t red = (size_t)4 * 2 * 64 * sizeof(f32x4_t);
   return (b > red ? b : red) + 16;
 }
 
-template <int EPI, bool ALIGN16>
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Copy `bytes` (a multiple of 16) from global to LDS.  DMA: gfx950
+// global_load_lds_dwordx4, each wave moving 1 KiB per instruction with every
+// load of the workgroup in flight at once (16-byte aligned source).
+// Otherwise a register copy with 8-byte loads, 8 in flight per thread.
+template <bool DMA>
+__device__ __forceinline__ void copy_to_lds(uint8_t* dst, const uint8_t* src, int bytes, int tid) {
+  if constexpr (DMA) {
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int chunks = (bytes + 1023) >> 10;
+    for (int c = wave; c < chunks; c += 4) {
+      const int off = (c << 10) + lane * 16;
+      if (off < bytes)
+        __builtin_amdgcn_global_load_lds(src + off, (lds_void*)(dst + (c << 10)), 16, 0, 0);
+    }
+  } else {
+    const int units = bytes >> 4;
+    for (int u0 = 0; u0 < units; u0 += 8 * 256) {
+      u32x4_t r[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int u = u0 + tid + 256 * i;
+        if (u < units) r[i] = load16<false>(src + u * 16);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int u = u0 + tid + 256 * i;
+        if (u < units) *reinterpret_cast<u32x4_t*>(dst + u * 16) = r[i];
+      }
+    }
+  }
+}
+
+// All 32 codes of one packed group (16 bytes) -> four 8-element bf16 operands.
+template <bool HW>
+__device__ __forceinline__ void decode32(const u32x4_t& q, uint32_t s, s16x8_t (&op)[4]) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) op[m] = decode8<HW>(q[m], s);
+}
+
+template <int EPI, bool HW>
+__device__ __forceinline__ void st_kloop(const GemmArgs& a, const uint8_t* sB, const uint8_t* sS,
+                                         const uint16_t* arow, bool aval, int wave, int col, int c,
+                                         f32x4_t (&acc)[2]) {
+  const int G = a.K / 32;
+  const int nsteps = (G + 3) >> 2;
+  // A for this lane: 64 contiguous bytes (k = 32*g .. 32*g+31) per step
+  u32x4_t an[4];
+  auto loadA = [&](int step, u32x4_t (&dst)[4]) {
+    const int g = 4 * step + c;
+    const bool ok = aval && g < G;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      dst[m] = ok ? *reinterpret_cast<const u32x4_t*>(arow + g * 32 + m * 8)
+                  : u32x4_t{0u, 0u, 0u, 0u};
+  };
+  if (wave < nsteps) loadA(wave, an);
+  for (int step = wave; step < nsteps; step += 4) {
+    u32x4_t ac[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) ac[m] = an[m];
+    if (step + 4 < nsteps) loadA(step + 4, an);
+    const int g = 4 * step + c;
+    s16x8_t bop[2][4];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int row = 16 * b + col;
+      u32x4_t q = u32x4_t{0u, 0u, 0u, 0u};
+      uint32_t sc = 127u;
+      if (g < G) {
+        q = *reinterpret_cast<const u32x4_t*>(sB + ((int64_t)row * G + g) * 16);
+        sc = sS[row * G + g];
+      }
+      decode32<HW>(q, sc, bop[b]);
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const s16x8_t av = __builtin_bit_cast(s16x8_t, ac[m]);
+      acc[0] = mfma16(av, bop[0][m], acc[0]);
+      acc[1] = mfma16(av, bop[1][m], acc[1]);
+    }
+  }
+}
+
+template <int EPI, bool DMA>
 __global__ __launch_bounds__(256) void moe_stream_kernel(GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int slices = (a.N + ST_BN - 1) / ST_BN;
@@ -175,129 +297,76 @@ __global__ __launch_bounds__(256) void moe_stream_kernel(GemmArgs a) {
   const int nvalid = min(ST_BN, a.N - n0);
   const int G = a.K / 32;
   const int rowbytes = a.K / 2;
-  const int ldsrow = st_lds_row(a.K);
   uint8_t* sB = smem;
-  uint8_t* sS = smem + ST_BN * ldsrow;
+  uint8_t* sS = smem + ST_BN * rowbytes;
   f32x4_t* sRed = reinterpret_cast<f32x4_t*>(smem);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int lr = lane & 15;
-  const int lk = lane >> 4;
+  const int col = lane & 15;  // MFMA column (B) / row (A) within the block
+  const int c = lane >> 4;    // quarter: group 4*step + c / C rows 4c..4c+3
 
   const uint8_t* gB = a.Bq + ((int64_t)e * a.N + n0) * rowbytes;
   const uint8_t* gS = a.Bs + ((int64_t)e * a.N + n0) * G;
+  const float bias0 = col < nvalid ? bias_at(a.bias, a.bias_dtype, (int64_t)e * a.N + n0 + col) : 0.f;
+  const float bias1 =
+      16 + col < nvalid ? bias_at(a.bias, a.bias_dtype, (int64_t)e * a.N + n0 + 16 + col) : 0.f;
 
-  // weight rows of this lane's two 16-column blocks
-  const int bc0 = (EPI == EPI_SWIGLU) ? 2 * lr : lr;
-  const int bc1 = (EPI == EPI_SWIGLU) ? 2 * lr + 1 : 16 + lr;
-
-  for (int pass0 = 0; pass0 < cnt; pass0 += 16 * ST_MAXRB) {
-    // (re)load the packed slice; the LDS also serves the cross-wave reduction
-    const int units = nvalid * rowbytes / 16;
-    for (int u = tid; u < units; u += 256) {
-      const int byte = u * 16;
-      const int r = byte / rowbytes;
-      const int c = byte - r * rowbytes;
-      *reinterpret_cast<u32x4_t*>(sB + r * ldsrow + c) = load16<ALIGN16>(gB + byte);
+  for (int pass0 = 0; pass0 < cnt; pass0 += 16) {
+    // (re)load the slice: its LDS also holds the cross-wave reduction
+    copy_to_lds<DMA>(sB, gB, nvalid * rowbytes, tid);
+    if (DMA && nvalid == ST_BN) {
+      copy_to_lds<true>(sS, gS, ST_BN * G, tid);
+    } else {
+      for (int u = tid; u < ST_BN * G; u += 256) sS[u] = u < nvalid * G ? gS[u] : 0;
     }
-    for (int u = tid; u < (ST_BN - nvalid) * ldsrow / 16; u += 256)
-      reinterpret_cast<u32x4_t*>(sB + nvalid * ldsrow)[u] = u32x4_t{0u, 0u, 0u, 0u};
-    for (int u = tid; u < ST_BN * G; u += 256) sS[u] = u < nvalid * G ? gS[u] : 0;
+    for (int u = tid; u < (ST_BN - nvalid) * rowbytes / 16; u += 256)
+      reinterpret_cast<u32x4_t*>(sB + nvalid * rowbytes)[u] = u32x4_t{0u, 0u, 0u, 0u};
+    if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    // decoder for the whole slice: the converter unless a scale byte is 255
+    int ff = 0;
+    for (int u = tid; u < ST_BN * G; u += 256) ff |= (sS[u] == 0xFF);
+    const bool hw = !__syncthreads_or(ff);
 
-    const int nrb = min(ST_MAXRB, (cnt - pass0 + 15) / 16);
-    const uint16_t* arow[ST_MAXRB];
-    bool aval[ST_MAXRB];
-#pragma unroll
-    for (int rb = 0; rb < ST_MAXRB; ++rb) {
-      const int r = pass0 + rb * 16 + lr;
-      aval[rb] = rb < nrb && r < cnt;
-      const int64_t pos = row0 + (aval[rb] ? r : 0);
-      const int64_t src = a.row_pair ? (int64_t)(a.row_pair[pos] / a.topk) : pos;
-      arow[rb] = a.A + src * a.lda + lk * 8;
-    }
-    f32x4_t acc[ST_MAXRB][2];
-#pragma unroll
-    for (int rb = 0; rb < ST_MAXRB; ++rb) {
-      acc[rb][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      acc[rb][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
-    const uint8_t* b0p = sB + bc0 * ldsrow + lk * 4;
-    const uint8_t* b1p = sB + bc1 * ldsrow + lk * 4;
-    const uint8_t* s0p = sS + bc0 * G;
-    const uint8_t* s1p = sS + bc1 * G;
-    // this wave's k-steps: ks = wave + 4 * it
-    const int nit = (G - wave + 3) / 4;
-    s16x8_t abuf[ST_PF][ST_MAXRB];
-#pragma unroll
-    for (int p = 0; p < ST_PF; ++p) {
-#pragma unroll
-      for (int rb = 0; rb < ST_MAXRB; ++rb) {
-        const int ks = wave + 4 * p;
-        abuf[p][rb] = (p < nit && aval[rb])
-                          ? *reinterpret_cast<const s16x8_t*>(arow[rb] + ks * 32)
-                          : s16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
-      }
-    }
-    for (int it0 = 0; it0 < nit; it0 += ST_PF) {
-#pragma unroll
-      for (int p = 0; p < ST_PF; ++p) {
-        const int it = it0 + p;
-        if (it < nit) {
-          const int ks = wave + 4 * it;
-          s16x8_t acur[ST_MAXRB];
-#pragma unroll
-          for (int rb = 0; rb < ST_MAXRB; ++rb) {
-            acur[rb] = abuf[p][rb];
-            const int itn = it + ST_PF;
-            if (itn < nit && aval[rb])
-              abuf[p][rb] = *reinterpret_cast<const s16x8_t*>(arow[rb] + (wave + 4 * itn) * 32);
-          }
-          const uint32_t q0 = *reinterpret_cast<const uint32_t*>(b0p + ks * 16);
-          const uint32_t q1 = *reinterpret_cast<const uint32_t*>(b1p + ks * 16);
-          const s16x8_t bf0 = decode8(q0, s0p[ks]);
-          const s16x8_t bf1 = decode8(q1, s1p[ks]);
-#pragma unroll
-          for (int rb = 0; rb < ST_MAXRB; ++rb) {
-            if (rb < nrb) {
-              acc[rb][0] = mfma16(acur[rb], bf0, acc[rb][0]);
-              acc[rb][1] = mfma16(acur[rb], bf1, acc[rb][1]);
-            }
-          }
-        }
-      }
-    }
+    const int r = pass0 + col;
+    const bool aval = r < cnt;
+    const int64_t pos = row0 + (aval ? r : 0);
+    const int64_t src = a.row_pair ? (int64_t)(a.row_pair[pos] / a.topk) : pos;
+    const uint16_t* arow = a.A + src * a.lda;
+    f32x4_t acc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+    if (hw)
+      st_kloop<EPI, true>(a, sB, sS, arow, aval, wave, col, c, acc);
+    else
+      st_kloop<EPI, false>(a, sB, sS, arow, aval, wave, col, c, acc);
+
     __syncthreads();  // all waves done with sB: reuse it for the reduction
-#pragma unroll
-    for (int rb = 0; rb < ST_MAXRB; ++rb) {
-      sRed[((wave * ST_MAXRB + rb) * 2 + 0) * 64 + lane] = acc[rb][0];
-      sRed[((wave * ST_MAXRB + rb) * 2 + 1) * 64 + lane] = acc[rb][1];
-    }
+    sRed[(wave * 2 + 0) * 64 + lane] = acc[0];
+    sRed[(wave * 2 + 1) * 64 + lane] = acc[1];
     __syncthreads();
-    if (wave < nrb) {
-      const int rb = wave;
-      f32x4_t c0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, c1 = c0;
+    if (wave < 2) {
+      // wave b finishes column block b
+      const int b = wave;
+      f32x4_t v = sRed[(0 * 2 + b) * 64 + lane];
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        c0 += sRed[((w * ST_MAXRB + rb) * 2 + 0) * 64 + lane];
-        c1 += sRed[((w * ST_MAXRB + rb) * 2 + 1) * 64 + lane];
-      }
+      for (int w = 1; w < 4; ++w) v += sRed[(w * 2 + b) * 64 + lane];
+      const int n = n0 + 16 * b + col;
+      const float bias = b ? bias1 : bias0;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int r = pass0 + rb * 16 + lk * 4 + j;
-        if (r >= cnt) continue;
-        const int64_t pos = row0 + r;
+        const int rr = pass0 + 4 * c + j;
+        const float val = v[j] + bias;
         if constexpr (EPI == EPI_SWIGLU) {
-          const int ng = n0 + 2 * lr;
-          if (2 * lr + 1 < nvalid) epilogue_swiglu<EPI>(a, e, pos, ng, c0[j], c1[j]);
+          // even column = gate, odd column = up of the same output index
+          const float up = __shfl_xor(val, 1);
+          if (rr < cnt && (col & 1) == 0 && 16 * b + col + 1 < nvalid)
+            epilogue_swiglu<EPI>(a, row0 + rr, n, val, up, 0.f, 0.f);
         } else {
-          if (lr < nvalid) epilogue_one<EPI>(a, e, pos, n0 + lr, c0[j]);
-          if (16 + lr < nvalid) epilogue_one<EPI>(a, e, pos, n0 + 16 + lr, c1[j]);
+          if (rr < cnt && 16 * b + col < nvalid) epilogue_one<EPI>(a, row0 + rr, n, val, 0.f);
         }
       }
     }
-    __syncthreads();  // reduction buffer is the next pass's weight slice
+    __syncthreads();  // the reduction buffer is the next pass's weight slice
   }
 }
 
@@ -394,6 +463,19 @@ __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
   const int cb1 = (EPI == EPI_SWIGLU) ? 64 + 32 * wn : 64 * wn + 32;
   const int l32 = lane & 31;
   const int lh = lane >> 5;
+  // this lane's output columns and their biases
+  const int ng_sw = n0 + 2 * (32 * wn + l32);
+  const int n_a = n0 + cb0 + l32;
+  const int n_b = n0 + cb1 + l32;
+  const int64_t eb = (int64_t)e * a.N;
+  float bias0, bias1;
+  if constexpr (EPI == EPI_SWIGLU) {
+    bias0 = ng_sw < a.N ? bias_at(a.bias, a.bias_dtype, eb + ng_sw) : 0.f;
+    bias1 = ng_sw < a.N ? bias_at(a.bias, a.bias_dtype, eb + ng_sw + 1) : 0.f;
+  } else {
+    bias0 = n_a < a.N ? bias_at(a.bias, a.bias_dtype, eb + n_a) : 0.f;
+    bias1 = n_b < a.N ? bias_at(a.bias, a.bias_dtype, eb + n_b) : 0.f;
+  }
 
   gload(0);
   lstore(0);
@@ -428,13 +510,198 @@ __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
       if (r >= rows) continue;
       const int64_t pos = m0 + r;
       if constexpr (EPI == EPI_SWIGLU) {
-        const int ng = n0 + 2 * (32 * wn + l32);
-        if (ng < a.N) epilogue_swiglu<EPI>(a, e, pos, ng, acc[mb][0][v], acc[mb][1][v]);
+        if (ng_sw < a.N) epilogue_swiglu<EPI>(a, pos, ng_sw, acc[mb][0][v], acc[mb][1][v], bias0, bias1);
       } else {
-        const int n_a = n0 + cb0 + l32;
-        const int n_b = n0 + cb1 + l32;
-        if (n_a < a.N) epilogue_one<EPI>(a, e, pos, n_a, acc[mb][0][v]);
-        if (n_b < a.N) epilogue_one<EPI>(a, e, pos, n_b, acc[mb][1][v]);
+        if (n_a < a.N) epilogue_one<EPI>(a, pos, n_a, acc[mb][0][v], bias0);
+        if (n_b < a.N) epilogue_one<EPI>(a, pos, n_b, acc[mb][1][v], bias1);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pipelined LDS-tiled kernel (prefill), 16-byte aligned operands.
+//
+// Tile 128 rows x 256 weight rows, BK = 64 (two scale groups), 3 LDS stages
+// filled only by global_load_lds DMA (no register staging):
+//  * A stage [128][64] bf16; row r's 16-byte chunk c is stored at chunk
+//    c ^ (r & 7), so fragment reads are bank-conflict free;
+//  * B stage kept packed, [2 groups][256 rows][16 bytes], natural row order,
+//    plus per row the 4-byte-aligned dword holding its two scale bytes
+//    (dword DMA writes 4 bytes per lane; G is even, so the pair sits at byte
+//    0 or 2 of that dword).
+// The four waves split N: each computes 128 x 64 (4 x 2 blocks of
+// v_mfma_f32_32x32x16_bf16), so every B fragment is decoded by one wave
+// only.  k order inside a group: MFMA m (0, 1) takes, in lane half lh,
+// k = 16*lh + 8*m .. +8, for both A and B; a lane reads its row's whole
+// 16-byte group once (rows consecutive: conflict free) and decodes its half.
+// Bound: MFMA.
+// ---------------------------------------------------------------------------
+constexpr int T2_BM = 128;
+constexpr int T2_BN = 256;
+constexpr int T2_BK = 64;
+constexpr int T2_NS = 3;
+constexpr int T2_A_BYTES = T2_BM * T2_BK * 2;          // 16 KiB
+constexpr int T2_B_BYTES = 2 * T2_BN * 16;             // 8 KiB
+constexpr int T2_S_BYTES = T2_BN * 4;                  // 1 KiB: one dword per row
+constexpr int T2_STAGE = T2_A_BYTES + T2_B_BYTES + T2_S_BYTES;
+constexpr int T2_DMA_PER_TILE = 4 + 2 + 1;             // per wave: A, B, scales
+
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
+  __shared__ __align__(1024) uint8_t smem[T2_NS * T2_STAGE];
+  const int nblk = gridDim.x;  // multiple of 8
+  const int L = (blockIdx.x & 7) * (nblk >> 3) + (blockIdx.x >> 3);
+  const int tile = L / a.n_tiles_n;
+  const int nt = L - tile * a.n_tiles_n;
+  if (tile >= *a.num_tiles) return;
+  const int2 te = a.tiles[tile];
+  const int e = te.x;
+  const int m0 = te.y;
+  const int rows = min(T2_BM, a.offsets[e] + a.counts[e] - m0);
+  const int n0 = nt * T2_BN;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;  // column quarter: weight rows 64*wave .. +64
+  const int G = a.K / 32;
+  const int KT = a.K / T2_BK;
+  const int l32 = lane & 31;
+  const int lh = lane >> 5;
+
+  // --- per-lane DMA sources (every lane always issues all of them, so the
+  //     per-wave vmcnt arithmetic below is exact; rows/columns past the tile
+  //     read a clamped valid address and are never stored) ----------------
+  const uint16_t* asrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 8 * (4 * wave + i) + (lane >> 3);
+    const int ch = (lane & 7) ^ (r & 7);
+    const int64_t pos = m0 + (r < rows ? r : 0);
+    const int64_t src = a.row_pair ? (int64_t)(a.row_pair[pos] / a.topk) : pos;
+    asrc[i] = a.A + src * a.lda + ch * 8;
+  }
+  // B: instruction i = 2*wave + h2 (0..7): group h = i / 4, row q = 64*(i%4) + lane
+  const uint8_t* bsrc[2];
+#pragma unroll
+  for (int h2 = 0; h2 < 2; ++h2) {
+    const int i = 2 * wave + h2;
+    const int q = 64 * (i & 3) + lane;
+    const bool ok = n0 + q < a.N;
+    bsrc[h2] = a.Bq + ((int64_t)e * a.N + (ok ? n0 + q : 0)) * G * 16 + (i >> 2) * 16;
+  }
+  // scales: row q = 64*wave + lane; with a 4-byte aligned base and E*N*G a
+  // multiple of 4 (N % 32 == 0) the aligned dword never leaves the tensor
+  const int sq = 64 * wave + lane;
+  const uint8_t* ssrc = a.Bs + ((int64_t)e * a.N + (n0 + sq < a.N ? n0 + sq : 0)) * G;
+
+  auto issue = [&](int kt) {
+    uint8_t* st = smem + (kt % T2_NS) * T2_STAGE;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds(asrc[i] + kt * T2_BK,
+                                       (lds_void*)(st + (4 * wave + i) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+      __builtin_amdgcn_global_load_lds(bsrc[h2] + kt * 32,
+                                       (lds_void*)(st + T2_A_BYTES + (2 * wave + h2) * 1024), 16, 0, 0);
+    const uint8_t* sp = ssrc + kt * 2;
+    __builtin_amdgcn_global_load_lds(
+        reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(sp) & ~uintptr_t(3)),
+        (lds_void*)(st + T2_A_BYTES + T2_B_BYTES + wave * 256), 4, 0, 0);
+  };
+
+  // this lane's two B rows (weight rows n0 + bq[nb]), scale-pair position, bias
+  int bq[2];
+  uint32_t spar[2];
+  float bias[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    bq[nb] = wave * 64 + nb * 32 + l32;
+    const bool ok = n0 + bq[nb] < a.N;
+    const int64_t row = (int64_t)e * a.N + (ok ? n0 + bq[nb] : 0);
+    spar[nb] = (uint32_t)(reinterpret_cast<uintptr_t>(a.Bs + row * G) & 3u);
+    bias[nb] = ok ? bias_at(a.bias, a.bias_dtype, row) : 0.f;
+  }
+  // A fragment chunk positions: chunk 4h + 2lh + m of row r sits at chunk ^ (r & 7)
+  const int rsw = l32 & 7;
+
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  issue(0);
+  if (KT > 1) issue(1);
+  for (int kt = 0; kt < KT; ++kt) {
+    // this wave's DMA for tile kt has landed once at most one tile's worth
+    // (the next tile's) is outstanding; the barrier then covers every wave.
+    // A bare s_barrier: __syncthreads' release fence would wait for the
+    // next tiles' loads too and serialise the pipeline.  The previous use of
+    // the stage refilled below ended before this barrier (its LDS reads fed
+    // MFMAs that have issued).
+    if (kt + 1 < KT)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (T2_DMA_PER_TILE & 15) | ((T2_DMA_PER_TILE >> 4) << 14));
+    else
+      __builtin_amdgcn_s_waitcnt(0x0070);
+    asm volatile("s_barrier" ::: "memory");
+    if (kt + 2 < KT) issue(kt + 2);
+    const uint8_t* st = smem + (kt % T2_NS) * T2_STAGE;
+    const uint8_t* sa = st;
+    const uint8_t* sb = st + T2_A_BYTES;
+    const uint8_t* ss = st + T2_A_BYTES + T2_B_BYTES;
+    uint32_t sc[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const uint32_t d = *reinterpret_cast<const uint32_t*>(ss + bq[nb] * 4);
+      sc[nb] = (d >> (((spar[nb] + 2u * (uint32_t)kt) & 3u) * 8u)) & 0xFFFFu;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      // B: whole 16-byte group of each of this lane's two rows, decode its half
+      s16x8_t bop[2][2];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const u32x4_t q = *reinterpret_cast<const u32x4_t*>(sb + h * (T2_BN * 16) + bq[nb] * 16);
+        const uint32_t s = (sc[nb] >> (8 * h)) & 0xFFu;
+        const uint32_t q0 = lh ? q[2] : q[0];
+        const uint32_t q1 = lh ? q[3] : q[1];
+        bop[nb][0] = decode8_fix(q0, s);
+        bop[nb][1] = decode8_fix(q1, s);
+      }
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const int pos = ((4 * h + 2 * lh + m) ^ rsw) * 16;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          const s16x8_t af = *reinterpret_cast<const s16x8_t*>(sa + (mb * 32 + l32) * 128 + pos);
+          acc[mb][0] = mfma32(af, bop[0][m], acc[mb][0]);
+          acc[mb][1] = mfma32(af, bop[1][m], acc[mb][1]);
+        }
+      }
+    }
+  }
+
+  // epilogue: lane holds column l32 of each 32x32 block, rows 8*(v/4) + 4*lh + v%4
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int r = mb * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+      const int64_t pos = m0 + r;
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const int n = n0 + bq[nb];
+        const float val = acc[mb][nb][v] + bias[nb];
+        if constexpr (EPI == EPI_SWIGLU) {
+          const float up = __shfl_xor(val, 1);  // odd weight row = up of the pair
+          if (r < rows && (l32 & 1) == 0 && n + 1 < a.N)
+            epilogue_swiglu<EPI>(a, pos, n, val, up, 0.f, 0.f);
+        } else {
+          if (r < rows && n < a.N) epilogue_one<EPI>(a, pos, n, val, 0.f);
+        }
       }
     }
   }
@@ -493,10 +760,22 @@ static int launch_gemm(const GemmArgs& a, int path, int64_t P, hipStream_t st) {
       set_error("stream GEMM: K=%d needs %zu bytes of LDS", a.K, smem);
       return BSA_EINVAL;
     }
-    if (align16)
+    const bool dma = align16 && (reinterpret_cast<uintptr_t>(a.Bs) % 16) == 0;
+    if (dma)
       hipLaunchKernelGGL((moe_stream_kernel<EPI, true>), dim3((unsigned)grid), dim3(256), smem, st, a);
     else
       hipLaunchKernelGGL((moe_stream_kernel<EPI, false>), dim3((unsigned)grid), dim3(256), smem, st, a);
+  } else if (align16 && (reinterpret_cast<uintptr_t>(a.Bs) % 4) == 0 &&
+             (reinterpret_cast<uintptr_t>(a.A) % 16) == 0 && (a.lda % 8) == 0) {
+    const int64_t max_tiles = (P + T2_BM - 1) / T2_BM + a.E;
+    GemmArgs b = a;
+    b.n_tiles_n = (a.N + T2_BN - 1) / T2_BN;
+    int64_t grid = align_up(max_tiles * b.n_tiles_n, 8);
+    if (grid > INT32_MAX) {
+      set_error("tiled GEMM: grid too large");
+      return BSA_EINVAL;
+    }
+    hipLaunchKernelGGL((moe_tiled2_kernel<EPI>), dim3((unsigned)grid), dim3(256), 0, st, b);
   } else {
     const int64_t max_tiles = (P + TL_BM - 1) / TL_BM + a.E;
     int64_t grid = max_tiles * a.n_tiles_n;
@@ -535,6 +814,161 @@ extern "C" int bsa_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t 
   return BSA_OK;
 }
 
+namespace bsa {
+
+struct MoeShape {
+  int64_t T, H, I, E, k;
+};
+
+static int check_shape(const MoeShape& m, const char* what) {
+  BSA_REQUIRE(m.T >= 0 && m.H > 0 && m.I > 0 && m.E > 0 && m.k > 0,
+              "%s: bad shape T=%lld H=%lld I=%lld E=%lld k=%lld", what, (long long)m.T,
+              (long long)m.H, (long long)m.I, (long long)m.E, (long long)m.k);
+  BSA_REQUIRE(m.H % 32 == 0 && m.I % 32 == 0, "%s: hidden and intermediate must be multiples of 32", what);
+  BSA_REQUIRE(m.E <= 1024, "%s: at most 1024 experts (got %lld)", what, (long long)m.E);
+  BSA_REQUIRE(m.k <= 16, "%s: top-k at most 16 (got %lld)", what, (long long)m.k);
+  BSA_REQUIRE(m.T * m.k < INT32_MAX / 2 && (m.T * m.k) * (2 * m.I) < INT64_MAX / 4,
+              "%s: too many tokens", what);
+  return BSA_OK;
+}
+
+static int check_ws(const MoeShape& m, void* workspace, int64_t bytes, Workspace* w, const char* what) {
+  BSA_REQUIRE(workspace, "%s: null workspace", what);
+  *w = carve(workspace, m.T, m.H, m.I, m.E, m.k);
+  BSA_REQUIRE(bytes >= w->bytes, "%s: workspace of %lld bytes, need %lld", what, (long long)bytes,
+              (long long)w->bytes);
+  BSA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "%s: workspace must be 256-byte aligned", what);
+  return BSA_OK;
+}
+
+static int stage_dispatch(const MoeShape& m, const int64_t* idx, const Workspace& w, hipStream_t st) {
+  return launch_dispatch(idx, (int)(m.T * m.k), (int)m.E, TL_BM, w.counts, w.offsets, w.row_pair,
+                         w.pair_pos, w.tiles, w.num_tiles, st);
+}
+
+static int stage_gate_up(const MoeShape& m, const void* hidden, const void* blocks, const void* scales,
+                         const void* bias, int bias_dtype, float alpha, float limit, const Workspace& w,
+                         void* save_gate_up, int path, hipStream_t st) {
+  GemmArgs g{};
+  g.A = static_cast<const uint16_t*>(hidden);
+  g.lda = m.H;
+  g.row_pair = w.row_pair;
+  g.topk = (int)m.k;
+  g.Bq = static_cast<const uint8_t*>(blocks);
+  g.Bs = static_cast<const uint8_t*>(scales);
+  g.bias = bias;
+  g.bias_dtype = bias_dtype;
+  g.counts = w.counts;
+  g.offsets = w.offsets;
+  g.E = (int)m.E;
+  g.N = (int)(2 * m.I);
+  g.K = (int)m.H;
+  g.out = w.act;
+  g.ldo = m.I;
+  g.out_dtype = DT_BF16;
+  g.save_pre = static_cast<float*>(save_gate_up);
+  g.alpha = alpha;
+  g.limit = limit;
+  g.tiles = w.tiles;
+  g.num_tiles = w.num_tiles;
+  g.n_tiles_n = (int)((2 * m.I + TL_BN - 1) / TL_BN);
+  const int64_t P = m.T * m.k;
+  return launch_gemm<EPI_SWIGLU>(g, pick_path(path, P, m.E, m.H), P, st);
+}
+
+static int stage_down(const MoeShape& m, const void* blocks, const void* scales, const void* bias,
+                      int bias_dtype, const Workspace& w, int path, hipStream_t st) {
+  GemmArgs g{};
+  g.A = w.act;
+  g.lda = m.I;
+  g.row_pair = nullptr;
+  g.topk = (int)m.k;
+  g.Bq = static_cast<const uint8_t*>(blocks);
+  g.Bs = static_cast<const uint8_t*>(scales);
+  g.bias = bias;
+  g.bias_dtype = bias_dtype;
+  g.counts = w.counts;
+  g.offsets = w.offsets;
+  g.E = (int)m.E;
+  g.N = (int)m.H;
+  g.K = (int)m.I;
+  g.out = w.y;
+  g.ldo = m.H;
+  g.out_dtype = DT_F32;
+  g.tiles = w.tiles;
+  g.num_tiles = w.num_tiles;
+  g.n_tiles_n = (int)((m.H + TL_BN - 1) / TL_BN);
+  const int64_t P = m.T * m.k;
+  return launch_gemm<EPI_BIAS_F32>(g, pick_path(path, P, m.E, m.I), P, st);
+}
+
+static bool dtype_ok(int d) { return d >= 0 && d <= 2; }
+
+}  // namespace bsa
+
+extern "C" int bsa_moe_dispatch(const int64_t* router_indices, int64_t T, int64_t H, int64_t I,
+                                int64_t E, int64_t k, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  clear_error();
+  const MoeShape m{T, H, I, E, k};
+  int rc = check_shape(m, "dispatch");
+  if (rc || T == 0) return rc;
+  BSA_REQUIRE(router_indices, "dispatch: null router_indices");
+  Workspace w;
+  if ((rc = check_ws(m, workspace, workspace_bytes, &w, "dispatch"))) return rc;
+  return stage_dispatch(m, router_indices, w, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int bsa_moe_gate_up(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E,
+                               int64_t k, const void* blocks, const void* scales, const void* bias,
+                               int bias_dtype, float alpha, float limit, void* workspace,
+                               int64_t workspace_bytes, void* save_gate_up, int path, void* stream) {
+  clear_error();
+  const MoeShape m{T, H, I, E, k};
+  int rc = check_shape(m, "gate_up");
+  if (rc || T == 0) return rc;
+  BSA_REQUIRE(hidden && blocks && scales, "gate_up: null pointer");
+  BSA_REQUIRE(dtype_ok(bias_dtype) && path >= 0 && path <= 2, "gate_up: bad dtype or path");
+  BSA_REQUIRE(reinterpret_cast<uintptr_t>(hidden) % 16 == 0 && reinterpret_cast<uintptr_t>(blocks) % 8 == 0,
+              "gate_up: hidden must be 16-byte and blocks 8-byte aligned");
+  Workspace w;
+  if ((rc = check_ws(m, workspace, workspace_bytes, &w, "gate_up"))) return rc;
+  return stage_gate_up(m, hidden, blocks, scales, bias, bias_dtype, alpha, limit, w, save_gate_up,
+                       path, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int bsa_moe_down(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                            const void* blocks, const void* scales, const void* bias,
+                            int bias_dtype, void* workspace, int64_t workspace_bytes, int path,
+                            void* stream) {
+  clear_error();
+  const MoeShape m{T, H, I, E, k};
+  int rc = check_shape(m, "down");
+  if (rc || T == 0) return rc;
+  BSA_REQUIRE(blocks && scales, "down: null pointer");
+  BSA_REQUIRE(dtype_ok(bias_dtype) && path >= 0 && path <= 2, "down: bad dtype or path");
+  BSA_REQUIRE(reinterpret_cast<uintptr_t>(blocks) % 8 == 0, "down: blocks must be 8-byte aligned");
+  Workspace w;
+  if ((rc = check_ws(m, workspace, workspace_bytes, &w, "down"))) return rc;
+  return stage_down(m, blocks, scales, bias, bias_dtype, w, path, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int bsa_moe_combine(const int64_t* router_indices, const void* routing_weights,
+                               int weight_dtype, int64_t T, int64_t H, int64_t I, int64_t E,
+                               int64_t k, void* workspace, int64_t workspace_bytes, void* out,
+                               int out_dtype, void* stream) {
+  clear_error();
+  const MoeShape m{T, H, I, E, k};
+  int rc = check_shape(m, "combine");
+  if (rc || T == 0) return rc;
+  BSA_REQUIRE(router_indices && routing_weights && out, "combine: null pointer");
+  BSA_REQUIRE(dtype_ok(weight_dtype) && dtype_ok(out_dtype), "combine: bad dtype");
+  Workspace w;
+  if ((rc = check_ws(m, workspace, workspace_bytes, &w, "combine"))) return rc;
+  return launch_combine(w.y, router_indices, routing_weights, weight_dtype, w.pair_pos, (int)T,
+                        (int)k, (int)H, out, out_dtype, static_cast<hipStream_t>(stream));
+}
+
 extern "C" int bsa_moe_experts_fwd(
     const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
     const int64_t* router_indices, const void* routing_weights, int weight_dtype,
@@ -543,78 +977,27 @@ extern "C" int bsa_moe_experts_fwd(
     float alpha, float limit, void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
     void* save_gate_up, int path, void* stream) {
   clear_error();
-  BSA_REQUIRE(T >= 0 && H > 0 && I > 0 && E > 0 && k > 0, "experts fwd: bad shape T=%lld H=%lld I=%lld E=%lld k=%lld",
-              (long long)T, (long long)H, (long long)I, (long long)E, (long long)k);
-  BSA_REQUIRE(H % 32 == 0 && I % 32 == 0, "experts fwd: hidden and intermediate must be multiples of 32");
-  BSA_REQUIRE(E <= 1024, "experts fwd: at most 1024 experts (got %lld)", (long long)E);
-  BSA_REQUIRE(k <= 16, "experts fwd: top-k at most 16 (got %lld)", (long long)k);
-  BSA_REQUIRE(T * k < INT32_MAX / 2 && (T * k) * (2 * I) < INT64_MAX / 4, "experts fwd: too many tokens");
-  BSA_REQUIRE(weight_dtype >= 0 && weight_dtype <= 2 && bias_dtype >= 0 && bias_dtype <= 2 &&
-                  out_dtype >= 0 && out_dtype <= 2, "experts fwd: bad dtype code");
+  const MoeShape m{T, H, I, E, k};
+  int rc = check_shape(m, "experts fwd");
+  if (rc || T == 0) return rc;
+  BSA_REQUIRE(dtype_ok(weight_dtype) && dtype_ok(bias_dtype) && dtype_ok(out_dtype),
+              "experts fwd: bad dtype code");
   BSA_REQUIRE(path >= 0 && path <= 2, "experts fwd: path must be 0, 1 or 2");
-  if (T == 0) return BSA_OK;
   BSA_REQUIRE(hidden && router_indices && routing_weights && gate_up_blocks && gate_up_scales &&
-                  down_blocks && down_scales && out && workspace,
+                  down_blocks && down_scales && out,
               "experts fwd: null pointer");
   BSA_REQUIRE(reinterpret_cast<uintptr_t>(hidden) % 16 == 0, "experts fwd: hidden must be 16-byte aligned");
-  BSA_REQUIRE(reinterpret_cast<uintptr_t>(gate_up_blocks) % 8 == 0 && reinterpret_cast<uintptr_t>(down_blocks) % 8 == 0,
+  BSA_REQUIRE(reinterpret_cast<uintptr_t>(gate_up_blocks) % 8 == 0 &&
+                  reinterpret_cast<uintptr_t>(down_blocks) % 8 == 0,
               "experts fwd: packed blocks must be 8-byte aligned");
-  const Workspace w = carve(workspace, T, H, I, E, k);
-  BSA_REQUIRE(workspace_bytes >= w.bytes, "experts fwd: workspace of %lld bytes, need %lld",
-              (long long)workspace_bytes, (long long)w.bytes);
-  BSA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "experts fwd: workspace must be 256-byte aligned");
+  Workspace w;
+  if ((rc = check_ws(m, workspace, workspace_bytes, &w, "experts fwd"))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t P = T * k;
-
-  int rc = launch_dispatch(router_indices, (int)P, (int)E, TL_BM, w.counts, w.offsets, w.row_pair,
-                           w.pair_pos, w.tiles, w.num_tiles, st);
-  if (rc) return rc;
-
-  // gate_up: [P, H] x [2I, H]^T -> SwiGLU -> act [P, I] bf16
-  GemmArgs g1{};
-  g1.A = static_cast<const uint16_t*>(hidden);
-  g1.lda = H;
-  g1.row_pair = w.row_pair;
-  g1.topk = (int)k;
-  g1.Bq = static_cast<const uint8_t*>(gate_up_blocks);
-  g1.Bs = static_cast<const uint8_t*>(gate_up_scales);
-  g1.bias = gate_up_bias;
-  g1.bias_dtype = bias_dtype;
-  g1.counts = w.counts;
-  g1.offsets = w.offsets;
-  g1.E = (int)E;
-  g1.N = (int)(2 * I);
-  g1.K = (int)H;
-  g1.out = w.act;
-  g1.ldo = I;
-  g1.out_dtype = DT_BF16;
-  g1.save_pre = static_cast<float*>(save_gate_up);
-  g1.alpha = alpha;
-  g1.limit = limit;
-  g1.tiles = w.tiles;
-  g1.num_tiles = w.num_tiles;
-  g1.n_tiles_n = (int)((2 * I + TL_BN - 1) / TL_BN);
-  rc = launch_gemm<EPI_SWIGLU>(g1, pick_path(path, P, E, H), P, st);
-  if (rc) return rc;
-
-  // down: [P, I] x [H, I]^T + bias -> y [P, H] f32
-  GemmArgs g2 = g1;
-  g2.A = w.act;
-  g2.lda = I;
-  g2.row_pair = nullptr;
-  g2.Bq = static_cast<const uint8_t*>(down_blocks);
-  g2.Bs = static_cast<const uint8_t*>(down_scales);
-  g2.bias = down_bias;
-  g2.N = (int)H;
-  g2.K = (int)I;
-  g2.out = w.y;
-  g2.ldo = H;
-  g2.out_dtype = DT_F32;
-  g2.save_pre = nullptr;
-  g2.n_tiles_n = (int)((H + TL_BN - 1) / TL_BN);
-  rc = launch_gemm<EPI_BIAS_F32>(g2, pick_path(path, P, E, I), P, st);
-  if (rc) return rc;
-
+  if ((rc = stage_dispatch(m, router_indices, w, st))) return rc;
+  if ((rc = stage_gate_up(m, hidden, gate_up_blocks, gate_up_scales, gate_up_bias, bias_dtype, alpha,
+                          limit, w, save_gate_up, path, st)))
+    return rc;
+  if ((rc = stage_down(m, down_blocks, down_scales, down_bias, bias_dtype, w, path, st))) return rc;
   return launch_combine(w.y, router_indices, routing_weights, weight_dtype, w.pair_pos, (int)T,
                         (int)k, (int)H, out, out_dtype, st);
 }

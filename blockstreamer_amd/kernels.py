@@ -128,3 +128,68 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
     if save:
         return out, ws, save_pre
     return out
+
+
+class MoEStages:
+    """The four forward stages of one MoE layer call, launched one by one.
+
+    Used where the stages must be timed or reused separately (the benchmark
+    brackets each with HIP events); ``moe_experts_forward`` runs the same
+    four launches through one C call.
+    """
+
+    def __init__(self, hidden: Tensor, router_indices: Tensor, routing_weights: Tensor,
+                 gate_up_blocks, gate_up_scales, gate_up_bias, down_blocks, down_scales,
+                 down_bias, alpha: float = 1.702, limit: float = 7.0, path: str = "auto"):
+        self.T, self.H = hidden.shape
+        self.k = router_indices.shape[1]
+        self.E = gate_up_blocks.shape[0]
+        self.I = gate_up_blocks.shape[1] // 2
+        _check_packed(gate_up_blocks, gate_up_scales, self.E, 2 * self.I, self.H, "gate_up_proj")
+        _check_packed(down_blocks, down_scales, self.E, self.H, self.I, "down_proj")
+        self.dev = _lib.require_gpu(hidden, router_indices, routing_weights, gate_up_blocks)
+        if hidden.dtype != torch.bfloat16 or not hidden.is_contiguous():
+            raise ValueError("MoEStages takes contiguous bfloat16 hidden states")
+        self.hidden = hidden
+        self.idx = router_indices.to(torch.int64).contiguous()
+        self.w = routing_weights.contiguous()
+        self.gu = (_as_u8(gate_up_blocks), _as_u8(gate_up_scales), gate_up_bias)
+        self.dn = (_as_u8(down_blocks), _as_u8(down_scales), down_bias)
+        self.bias_code = _lib.dtype_code(gate_up_bias.dtype) if gate_up_bias is not None else 0
+        self.alpha, self.limit, self.path = float(alpha), float(limit), PATHS[path]
+        self.ws_bytes = moe_workspace_bytes(self.T, self.H, self.I, self.E, self.k)
+        self.ws = _aligned_bytes(self.ws_bytes, self.dev)
+        self.out = torch.empty((self.T, self.H), dtype=torch.bfloat16, device=self.dev)
+        self.shape = (self.T, self.H, self.I, self.E, self.k)
+
+    def _stream(self):
+        return _lib.stream_handle(self.dev)
+
+    def dispatch(self):
+        _lib.call("bsa_moe_dispatch", self.idx.data_ptr(), *self.shape, self.ws.data_ptr(),
+                  self.ws_bytes, self._stream())
+
+    def gate_up(self):
+        b, s, bias = self.gu
+        _lib.call("bsa_moe_gate_up", self.hidden.data_ptr(), *self.shape, b.data_ptr(),
+                  s.data_ptr(), bias.data_ptr() if bias is not None else None, self.bias_code,
+                  self.alpha, self.limit, self.ws.data_ptr(), self.ws_bytes, None, self.path,
+                  self._stream())
+
+    def down(self):
+        b, s, bias = self.dn
+        _lib.call("bsa_moe_down", *self.shape, b.data_ptr(), s.data_ptr(),
+                  bias.data_ptr() if bias is not None else None, self.bias_code,
+                  self.ws.data_ptr(), self.ws_bytes, self.path, self._stream())
+
+    def combine(self):
+        _lib.call("bsa_moe_combine", self.idx.data_ptr(), self.w.data_ptr(),
+                  _lib.dtype_code(self.w.dtype), *self.shape, self.ws.data_ptr(), self.ws_bytes,
+                  self.out.data_ptr(), 0, self._stream())
+
+    def run(self) -> Tensor:
+        self.dispatch()
+        self.gate_up()
+        self.down()
+        self.combine()
+        return self.out

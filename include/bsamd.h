@@ -114,6 +114,39 @@ int bsa_moe_experts_fwd(
     int out_dtype, void *workspace, int64_t workspace_bytes,
     void *save_gate_up, int path, void *stream);
 
+/*
+ * The four stages bsa_moe_experts_fwd runs, callable one by one (same
+ * arguments and workspace; run in this order on one stream).
+ *
+ * bsa_moe_dispatch   replaces gptoss.py:143-154 (one_hot / nonzero / where):
+ *                    expert-sorted rows, per-expert offsets and the tile list,
+ *                    built on the device.
+ * bsa_moe_gate_up    replaces gptoss.py:158-166: gate_up GEMM + bias + clamped
+ *                    SwiGLU into the workspace's [T*k, I] activations.
+ * bsa_moe_down       replaces gptoss.py:167-174: down GEMM + bias into the
+ *                    workspace's float32 [T*k, H] rows.
+ * bsa_moe_combine    replaces gptoss.py:175-176: routing-weight scale and the
+ *                    per-token sum (ascending expert order) into out.
+ */
+int bsa_moe_dispatch(const int64_t *router_indices, int64_t T, int64_t H,
+                     int64_t I, int64_t E, int64_t k, void *workspace,
+                     int64_t workspace_bytes, void *stream);
+int bsa_moe_gate_up(const void *hidden, int64_t T, int64_t H, int64_t I,
+                    int64_t E, int64_t k, const void *blocks,
+                    const void *scales, const void *bias, int bias_dtype,
+                    float alpha, float limit, void *workspace,
+                    int64_t workspace_bytes, void *save_gate_up, int path,
+                    void *stream);
+int bsa_moe_down(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                 const void *blocks, const void *scales, const void *bias,
+                 int bias_dtype, void *workspace, int64_t workspace_bytes,
+                 int path, void *stream);
+int bsa_moe_combine(const int64_t *router_indices, const void *routing_weights,
+                    int weight_dtype, int64_t T, int64_t H, int64_t I,
+                    int64_t E, int64_t k, void *workspace,
+                    int64_t workspace_bytes, void *out, int out_dtype,
+                    void *stream);
+
 #ifdef __cplusplus
 }
 #endif

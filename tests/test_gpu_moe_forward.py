@@ -186,3 +186,24 @@ def test_edge_cases(device):
     # no tokens
     empty = kernels.moe_experts_forward(t["hidden"][:0], idx[:0], w[:0], *args)
     assert empty.shape == (0, 256)
+
+
+@pytest.mark.parametrize("path", PATHS)
+def test_shard_blob_views_8_byte_aligned(device, path):
+    """Packed weights as 8-byte-aligned views into one byte blob (the NVMe
+    staging layout) take the register-copy kernels; results match the oracle."""
+    shape = synthetic.MoEShape(8, 2, 256, 256, 150)
+    t = synthetic.moe_layer(shape, seed=12, scale_lo=119, scale_hi=127, device=device)
+    idx, w = synthetic.random_routing(150, 8, 2, seed=13, device=device)
+    views = dict(t)
+    for name in ("gate_up_proj_blocks", "gate_up_proj_scales", "down_proj_blocks", "down_proj_scales"):
+        src = t[name]
+        blob = torch.zeros(src.numel() + 64, dtype=torch.uint8, device=device)
+        blob[8:8 + src.numel()] = src.reshape(-1)
+        views[name] = blob[8:8 + src.numel()].view(src.shape)
+        assert views[name].data_ptr() % 16 == 8
+    announce(f"moe 8-byte aligned views path={path}")
+    got = kernels.moe_experts_forward(t["hidden"], idx, w, *expert_args(views), path=path)
+    want = oracle.experts_ref(t["hidden"].cpu(), idx.cpu(), w.cpu().float(),
+                              *[a.cpu() for a in expert_args(t)])
+    assert_layer_close(got, want, f"8-byte views {path}")
