@@ -25,6 +25,13 @@
 //    v_mfma_f32_32x32x16_bf16.  The B tile is decoded into LDS as bf16.
 //    Bound: MFMA.
 //
+// Weights are decoded with the gfx950 converter (v_cvt_scalef32_pk_bf16_fp4),
+// which follows OCP MX: a block whose E8M0 scale byte is 255 (the NaN code)
+// decodes to NaN, so the outputs it touches are NaN.  The reference's
+// float32 ldexp gives +-inf there instead (and NaN for zero codes), which
+// mixed-sign products also turn into NaN; the standalone dequant kernel
+// reproduces the reference bit for bit, this case included.
+//
 // For the gate_up projection the weight rows interleave gate (even) and up
 // (odd) columns (gptoss.py:131).  Both kernels place gate column j and up
 // column j in the same lane, so the clamped SwiGLU runs in registers.
@@ -94,20 +101,6 @@ __device__ __forceinline__ s16x8_t decode8(uint32_t q, uint32_t s) {
   }
   u32x4_t v = {d[0], d[1], d[2], d[3]};
   return __builtin_bit_cast(s16x8_t, v);
-}
-
-// 8 codes with the converter, redone by the integer decoder in the rare
-// lanes whose scale byte is 255 (the converter's NaN code).
-__device__ __forceinline__ s16x8_t decode8_fix(uint32_t q, uint32_t s) {
-  s16x8_t v = decode8<true>(q, s);
-  if (__builtin_expect(s == 0xFFu, 0)) v = decode8<false>(q, s);
-  return v;
-}
-
-// true if any byte of w is 0xFF
-__device__ __forceinline__ bool has_ff_byte(uint32_t w) {
-  return ((w & 0xFFu) == 0xFFu) | ((w & 0xFF00u) == 0xFF00u) | ((w & 0xFF0000u) == 0xFF0000u) |
-         ((w & 0xFF000000u) == 0xFF000000u);
 }
 
 __device__ __forceinline__ float bias_at(const void* bias, int dtype, int64_t i) {
@@ -242,39 +235,46 @@ __device__ __forceinline__ void decode32(const u32x4_t& q, uint32_t s, s16x8_t (
 
 template <int EPI, bool HW>
 __device__ __forceinline__ void st_kloop(const GemmArgs& a, const uint8_t* sB, const uint8_t* sS,
-                                         const uint16_t* arow, bool aval, int wave, int col, int c,
+                                         const uint16_t* arow, int wave, int col, int c,
                                          f32x4_t (&acc)[2]) {
   const int G = a.K / 32;
   const int nsteps = (G + 3) >> 2;
-  // A for this lane: 64 contiguous bytes (k = 32*g .. 32*g+31) per step
+  const bool full_last = (G & 3) == 0;
+  // A for this lane: the 64 contiguous bytes of group 4*step + c.  Rows past
+  // the expert's count and groups past K read a clamped valid address: the
+  // former are never stored, the latter meet zero B codes.
   u32x4_t an[4];
   auto loadA = [&](int step, u32x4_t (&dst)[4]) {
-    const int g = 4 * step + c;
-    const bool ok = aval && g < G;
+    const int g = min(4 * step + c, G - 1);
+    const u32x4_t* p = reinterpret_cast<const u32x4_t*>(arow + g * 32);
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
-      dst[m] = ok ? *reinterpret_cast<const u32x4_t*>(arow + g * 32 + m * 8)
-                  : u32x4_t{0u, 0u, 0u, 0u};
+    for (int m = 0; m < 4; ++m) dst[m] = p[m];
   };
+  // LDS byte offsets of this lane's two weight rows, group c
+  const uint32_t boff0 = (uint32_t)((col * G + c) * 16);
+  const uint32_t boff1 = (uint32_t)(((16 + col) * G + c) * 16);
+  const uint32_t soff0 = (uint32_t)(col * G + c);
+  const uint32_t soff1 = (uint32_t)((16 + col) * G + c);
   if (wave < nsteps) loadA(wave, an);
   for (int step = wave; step < nsteps; step += 4) {
     u32x4_t ac[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) ac[m] = an[m];
     if (step + 4 < nsteps) loadA(step + 4, an);
-    const int g = 4 * step + c;
-    s16x8_t bop[2][4];
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int row = 16 * b + col;
-      u32x4_t q = u32x4_t{0u, 0u, 0u, 0u};
-      uint32_t sc = 127u;
-      if (g < G) {
-        q = *reinterpret_cast<const u32x4_t*>(sB + ((int64_t)row * G + g) * 16);
-        sc = sS[row * G + g];
-      }
-      decode32<HW>(q, sc, bop[b]);
+    const uint32_t gofs = (uint32_t)(step * 4);
+    u32x4_t q0 = *reinterpret_cast<const u32x4_t*>(sB + boff0 + gofs * 16);
+    u32x4_t q1 = *reinterpret_cast<const u32x4_t*>(sB + boff1 + gofs * 16);
+    uint32_t s0 = sS[soff0 + gofs];
+    uint32_t s1 = sS[soff1 + gofs];
+    if (!full_last && step == nsteps - 1 && 4 * step + c >= G) {
+      // past the last group: zero codes (their LDS bytes may be another row's)
+      q0 = u32x4_t{0u, 0u, 0u, 0u};
+      q1 = q0;
+      s0 = s1 = 127u;
     }
+    s16x8_t bop[2][4];
+    decode32<HW>(q0, s0, bop[0]);
+    decode32<HW>(q1, s1, bop[1]);
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const s16x8_t av = __builtin_bit_cast(s16x8_t, ac[m]);
@@ -324,21 +324,13 @@ __global__ __launch_bounds__(256) void moe_stream_kernel(GemmArgs a) {
       reinterpret_cast<u32x4_t*>(sB + nvalid * rowbytes)[u] = u32x4_t{0u, 0u, 0u, 0u};
     if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    // decoder for the whole slice: the converter unless a scale byte is 255
-    int ff = 0;
-    for (int u = tid; u < ST_BN * G; u += 256) ff |= (sS[u] == 0xFF);
-    const bool hw = !__syncthreads_or(ff);
 
     const int r = pass0 + col;
-    const bool aval = r < cnt;
-    const int64_t pos = row0 + (aval ? r : 0);
+    const int64_t pos = row0 + (r < cnt ? r : 0);
     const int64_t src = a.row_pair ? (int64_t)(a.row_pair[pos] / a.topk) : pos;
     const uint16_t* arow = a.A + src * a.lda;
     f32x4_t acc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
-    if (hw)
-      st_kloop<EPI, true>(a, sB, sS, arow, aval, wave, col, c, acc);
-    else
-      st_kloop<EPI, false>(a, sB, sS, arow, aval, wave, col, c, acc);
+    st_kloop<EPI, true>(a, sB, sS, arow, wave, col, c, acc);
 
     __syncthreads();  // all waves done with sB: reuse it for the reduction
     sRed[(wave * 2 + 0) * 64 + lane] = acc[0];
@@ -442,7 +434,7 @@ __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
       *reinterpret_cast<u32x4_t*>(&sA[buf][r * TL_LDK + akc * 8]) = ra[i];
     }
     uint16_t* dst = &sB[buf][bcol * TL_LDK + bgs * 32];
-    const bool hw = mx_scale_hw_ok(rs);
+    const bool hw = true;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       uint32_t d[4];
@@ -540,14 +532,63 @@ __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
 constexpr int T2_BM = 128;
 constexpr int T2_BN = 256;
 constexpr int T2_BK = 64;
-constexpr int T2_NS = 3;
 constexpr int T2_A_BYTES = T2_BM * T2_BK * 2;          // 16 KiB
 constexpr int T2_B_BYTES = 2 * T2_BN * 16;             // 8 KiB
 constexpr int T2_S_BYTES = T2_BN * 4;                  // 1 KiB: one dword per row
 constexpr int T2_STAGE = T2_A_BYTES + T2_B_BYTES + T2_S_BYTES;
 constexpr int T2_DMA_PER_TILE = 4 + 2 + 1;             // per wave: A, B, scales
 
-template <int EPI>
+// One BK = 64 step of a wave's 128 x 64 block from LDS stage st, software
+// pipelined by hand: the LDS reads for step s+1 are issued before the eight
+// MFMAs of step s, and sched_barrier fences keep the compiler from sinking
+// them back next to their uses, so each wait covers reads issued a full step
+// (8 x 32 MFMA cycles) earlier.  Branch free.
+template <int SCHED>
+__device__ __forceinline__ void t2_ktile(f32x16_t (&acc)[4][2], const uint8_t* st,
+                                         const uint32_t (&sc)[2], const uint32_t (&aoff)[4],
+                                         const uint32_t (&boff)[2], int lh) {
+  s16x8_t afr[2][4];
+  u32x4_t bq[2][2];  // [h][nb] packed group of each B row
+  auto loadA = [&](int step, s16x8_t (&dst)[4]) {
+    const uint8_t* p = st + aoff[step];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) dst[mb] = *reinterpret_cast<const s16x8_t*>(p + mb * 4096);
+  };
+  auto loadB = [&](int h) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+      bq[h][nb] = *reinterpret_cast<const u32x4_t*>(st + T2_A_BYTES + h * (T2_BN * 16) + boff[nb]);
+  };
+  loadB(0);
+  loadA(0, afr[0]);
+  loadB(1);
+  s16x8_t bop[2][2];
+#pragma unroll
+  for (int step = 0; step < 4; ++step) {
+    const int h = step >> 1;
+    const int m = step & 1;
+    if (step + 1 < 4) loadA(step + 1, afr[(step + 1) & 1]);
+    if constexpr (SCHED) __builtin_amdgcn_sched_barrier(0);
+    if (m == 0) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const uint32_t sv = (sc[nb] >> (8 * h)) & 0xFFu;
+        const uint32_t q0 = lh ? bq[h][nb][2] : bq[h][nb][0];
+        const uint32_t q1 = lh ? bq[h][nb][3] : bq[h][nb][1];
+        bop[nb][0] = decode8<true>(q0, sv);
+        bop[nb][1] = decode8<true>(q1, sv);
+      }
+    }
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      acc[mb][0] = mfma32(afr[step & 1][mb], bop[0][m], acc[mb][0]);
+      acc[mb][1] = mfma32(afr[step & 1][mb], bop[1][m], acc[mb][1]);
+    }
+    if constexpr (SCHED) __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <int EPI, int T2_NS, int SCHED>
 __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
   __shared__ __align__(1024) uint8_t smem[T2_NS * T2_STAGE];
   const int nblk = gridDim.x;  // multiple of 8
@@ -622,8 +663,17 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
     spar[nb] = (uint32_t)(reinterpret_cast<uintptr_t>(a.Bs + row * G) & 3u);
     bias[nb] = ok ? bias_at(a.bias, a.bias_dtype, row) : 0.f;
   }
-  // A fragment chunk positions: chunk 4h + 2lh + m of row r sits at chunk ^ (r & 7)
+  // LDS byte offsets (within a stage) of this lane's A fragments for step
+  // (h, m): chunk 4h + 2lh + m of row l32 sits at chunk ^ (row & 7); rows
+  // mb*32 + l32 add mb * 4096.  And of its two B rows.
   const int rsw = l32 & 7;
+  uint32_t aoff[4];
+#pragma unroll
+  for (int step = 0; step < 4; ++step) {
+    const int h = step >> 1, m = step & 1;
+    aoff[step] = (uint32_t)(l32 * 128 + (((4 * h + 2 * lh + m) ^ rsw) * 16));
+  }
+  uint32_t boff[2] = {(uint32_t)(bq[0] * 16), (uint32_t)(bq[1] * 16)};
 
   f32x16_t acc[4][2];
 #pragma unroll
@@ -633,8 +683,8 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  issue(0);
-  if (KT > 1) issue(1);
+  for (int i = 0; i < T2_NS - 1; ++i)
+    if (i < KT) issue(i);
   for (int kt = 0; kt < KT; ++kt) {
     // this wave's DMA for tile kt has landed once at most one tile's worth
     // (the next tile's) is outstanding; the barrier then covers every wave.
@@ -642,46 +692,26 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
     // next tiles' loads too and serialise the pipeline.  The previous use of
     // the stage refilled below ended before this barrier (its LDS reads fed
     // MFMAs that have issued).
-    if (kt + 1 < KT)
-      __builtin_amdgcn_s_waitcnt(0x0F70 | (T2_DMA_PER_TILE & 15) | ((T2_DMA_PER_TILE >> 4) << 14));
-    else
-      __builtin_amdgcn_s_waitcnt(0x0070);
+    {
+      // tiles issued after kt and still allowed in flight
+      const int ahead = min(T2_NS - 2, KT - 1 - kt);
+      if (ahead >= 2)
+        __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * T2_DMA_PER_TILE) & 15) | (((2 * T2_DMA_PER_TILE) >> 4) << 14));
+      else if (ahead == 1)
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (T2_DMA_PER_TILE & 15) | ((T2_DMA_PER_TILE >> 4) << 14));
+      else
+        __builtin_amdgcn_s_waitcnt(0x0070);
+    }
     asm volatile("s_barrier" ::: "memory");
-    if (kt + 2 < KT) issue(kt + 2);
+    if (kt + T2_NS - 1 < KT) issue(kt + T2_NS - 1);
     const uint8_t* st = smem + (kt % T2_NS) * T2_STAGE;
-    const uint8_t* sa = st;
-    const uint8_t* sb = st + T2_A_BYTES;
-    const uint8_t* ss = st + T2_A_BYTES + T2_B_BYTES;
     uint32_t sc[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-      const uint32_t d = *reinterpret_cast<const uint32_t*>(ss + bq[nb] * 4);
+      const uint32_t d = *reinterpret_cast<const uint32_t*>(st + T2_A_BYTES + T2_B_BYTES + bq[nb] * 4);
       sc[nb] = (d >> (((spar[nb] + 2u * (uint32_t)kt) & 3u) * 8u)) & 0xFFFFu;
     }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      // B: whole 16-byte group of each of this lane's two rows, decode its half
-      s16x8_t bop[2][2];
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        const u32x4_t q = *reinterpret_cast<const u32x4_t*>(sb + h * (T2_BN * 16) + bq[nb] * 16);
-        const uint32_t s = (sc[nb] >> (8 * h)) & 0xFFu;
-        const uint32_t q0 = lh ? q[2] : q[0];
-        const uint32_t q1 = lh ? q[3] : q[1];
-        bop[nb][0] = decode8_fix(q0, s);
-        bop[nb][1] = decode8_fix(q1, s);
-      }
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const int pos = ((4 * h + 2 * lh + m) ^ rsw) * 16;
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          const s16x8_t af = *reinterpret_cast<const s16x8_t*>(sa + (mb * 32 + l32) * 128 + pos);
-          acc[mb][0] = mfma32(af, bop[0][m], acc[mb][0]);
-          acc[mb][1] = mfma32(af, bop[1][m], acc[mb][1]);
-        }
-      }
-    }
+    t2_ktile<SCHED>(acc, st, sc, aoff, boff, lh);
   }
 
   // epilogue: lane holds column l32 of each 32x32 block, rows 8*(v/4) + 4*lh + v%4
@@ -775,7 +805,7 @@ static int launch_gemm(const GemmArgs& a, int path, int64_t P, hipStream_t st) {
       set_error("tiled GEMM: grid too large");
       return BSA_EINVAL;
     }
-    hipLaunchKernelGGL((moe_tiled2_kernel<EPI>), dim3((unsigned)grid), dim3(256), 0, st, b);
+    hipLaunchKernelGGL((moe_tiled2_kernel<EPI, 3, 0>), dim3((unsigned)grid), dim3(256), 0, st, b);
   } else {
     const int64_t max_tiles = (P + TL_BM - 1) / TL_BM + a.E;
     int64_t grid = max_tiles * a.n_tiles_n;
