@@ -42,6 +42,15 @@ _SIGNATURES = {
     "bsa_moe_down": [_i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr, _int, _ptr, _i64, _int, _ptr],
     "bsa_moe_combine": [_ptr, _ptr, _int, _i64, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _int,
                         _ptr],
+    "bsa_moe_bwd_workspace_bytes": [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_i64)],
+    "bsa_moe_experts_bwd": [
+        _ptr, _int, _i64, _i64, _i64, _i64, _i64,  # grad_out, dtype, T, H, I, E, k
+        _ptr, _ptr, _int,                          # indices, weights, weight dtype
+        _ptr, _ptr, _ptr, _ptr,                    # gate_up b/s, down b/s
+        _f32, _f32,                                # alpha, limit
+        _ptr, _i64, _ptr, _ptr, _i64,              # ws, ws bytes, save, bwd ws, bwd bytes
+        _ptr, _int, _ptr, _ptr,                    # grad_hidden, dtype, grad_weights, stream
+    ],
 }
 _RESTYPE = {"bsa_last_error": ctypes.c_char_p}
 

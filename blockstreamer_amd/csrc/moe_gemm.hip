@@ -44,11 +44,19 @@ int launch_dispatch(const int64_t* idx, int P, int E, int BM, int* counts, int* 
 int launch_combine(const float* Y, const int64_t* idx, const void* w, int w_dtype,
                    const int* pair_pos, int T, int k, int H, void* out, int out_dtype,
                    hipStream_t st);
+int launch_bwd_prep(const void* dout, int dout_dtype, const float* y, const void* w, int w_dtype,
+                    const int* pair_pos, int P, int k, int H, uint16_t* dy, float* grad_w,
+                    hipStream_t st);
+int launch_dequant_bf16_routed(const uint8_t* blocks, const uint8_t* scales, uint16_t* out,
+                               int64_t E, int64_t R, int64_t G, const int* expert_rows,
+                               hipStream_t stream);
 
 enum Epi : int {
   EPI_SWIGLU = 0,    // out bf16 [P][N/2] = swiglu(acc + bias), optional f32 pre-activation save
   EPI_BIAS_F32 = 1,  // out f32 [P][N] = acc + bias
   EPI_STORE = 2,     // out (out_dtype) [P][N] = acc (+ bias if given)
+  EPI_SWIGLU_BWD = 3,  // out bf16 [P][2N] = d(gate_up) from acc = d(act) and the saved
+                       // f32 pre-activations in save_pre [P][2N]
 };
 
 struct GemmArgs {
@@ -58,6 +66,7 @@ struct GemmArgs {
   int topk;
   const uint8_t* Bq;     // packed [E][N][K/32][16]
   const uint8_t* Bs;     // scales [E][N][K/32]
+  const uint16_t* Bd;    // dense bf16 [E][N][K] (backward GEMMs) instead of Bq/Bs
   const void* bias;      // [E][N] or null
   int bias_dtype;
   const int* counts;     // rows per expert
@@ -119,6 +128,21 @@ __device__ __forceinline__ float swiglu(float g, float u, float alpha, float lim
   return (u + 1.0f) * (g * sig);
 }
 
+// Backward of swiglu() w.r.t. the raw gate and up pre-activations, as torch
+// autograd differentiates gptoss.py:130-135: clamp(max=limit) passes the
+// gradient where g <= limit, clamp(-limit, limit) where -limit <= u <= limit,
+// and d(x * sigmoid(a x))/dx = s + a x s (1 - s).
+__device__ __forceinline__ void swiglu_bwd(float g, float u, float dout, float alpha, float limit,
+                                           float* dg, float* du) {
+  const float gc = fminf(g, limit);
+  const float uc = fminf(fmaxf(u, -limit), limit);
+  const float sg = 1.0f / (1.0f + __expf(-alpha * gc));
+  const float glu = gc * sg;
+  *du = (u >= -limit && u <= limit) ? dout * glu : 0.0f;
+  const float dglu = dout * (uc + 1.0f);
+  *dg = (g <= limit) ? dglu * (sg + alpha * gc * sg * (1.0f - sg)) : 0.0f;
+}
+
 __device__ __forceinline__ void store_out(void* out, int dtype, int64_t i, float v) {
   if (dtype == DT_F32) {
     static_cast<float*>(out)[i] = v;
@@ -163,10 +187,17 @@ template <int EPI>
 __device__ __forceinline__ void epilogue_one(const GemmArgs& a, int64_t pos, int n, float acc,
                                              float b) {
   const float v = acc + b;
-  if constexpr (EPI == EPI_BIAS_F32)
+  if constexpr (EPI == EPI_BIAS_F32) {
     static_cast<float*>(a.out)[pos * a.ldo + n] = v;
-  else
+  } else if constexpr (EPI == EPI_SWIGLU_BWD) {
+    const float2 pre = *reinterpret_cast<const float2*>(a.save_pre + pos * (2 * (int64_t)a.N) + 2 * n);
+    float dg, du;
+    swiglu_bwd(pre.x, pre.y, v, a.alpha, a.limit, &dg, &du);
+    *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.out) + pos * a.ldo + 2 * n) =
+        pack_bf16x2(dg, du);
+  } else {
     store_out(a.out, a.out_dtype, pos * a.ldo + n, v);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -370,7 +401,7 @@ constexpr int TL_BN = 128;
 constexpr int TL_BK = 64;
 constexpr int TL_LDK = TL_BK + 8;  // padded row, bf16 elements (144 bytes)
 
-template <int EPI, bool ALIGN16>
+template <int EPI, bool ALIGN16, bool BDENSE>
 __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
   __shared__ __align__(16) uint16_t sA[2][TL_BM * TL_LDK];
   __shared__ __align__(16) uint16_t sB[2][TL_BN * TL_LDK];
@@ -412,20 +443,40 @@ __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
   const int brr = tid >> 1;
   const int bgs = tid & 1;
   const bool bok = n0 + brr < a.N;
-  const uint8_t* bq = a.Bq + ((int64_t)e * a.N + (bok ? n0 + brr : 0)) * G * 16 + bgs * 16;
-  const uint8_t* bs = a.Bs + ((int64_t)e * a.N + (bok ? n0 + brr : 0)) * G + bgs;
+  const uint8_t* bq = BDENSE ? nullptr
+                             : a.Bq + ((int64_t)e * a.N + (bok ? n0 + brr : 0)) * G * 16 + bgs * 16;
+  const uint8_t* bs = BDENSE ? nullptr : a.Bs + ((int64_t)e * a.N + (bok ? n0 + brr : 0)) * G + bgs;
   const int bcol = (EPI == EPI_SWIGLU) ? ((brr & 1) ? 64 + (brr >> 1) : (brr >> 1)) : brr;
+  // dense B: 4 units of 16 bytes per thread per k-tile, like A
+  const uint16_t* bdp[4];
+  bool bdok[4];
+  if constexpr (BDENSE) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = (tid >> 3) + 32 * i;
+      bdok[i] = n0 + r < a.N;
+      bdp[i] = a.Bd + ((int64_t)e * a.N + (bdok[i] ? n0 + r : 0)) * a.K + akc * 8;
+    }
+  }
 
   u32x4_t ra[4];
   u32x4_t rb;
+  u32x4_t rbd[4];
   uint32_t rs;
   auto gload = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       ra[i] = aok[i] ? *reinterpret_cast<const u32x4_t*>(aptr[i] + kt * TL_BK)
                      : u32x4_t{0u, 0u, 0u, 0u};
-    rb = bok ? load16<ALIGN16>(bq + kt * 32) : u32x4_t{0u, 0u, 0u, 0u};
-    rs = bok ? (uint32_t)bs[kt * 2] : 127u;
+    if constexpr (BDENSE) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        rbd[i] = bdok[i] ? *reinterpret_cast<const u32x4_t*>(bdp[i] + kt * TL_BK)
+                         : u32x4_t{0u, 0u, 0u, 0u};
+    } else {
+      rb = bok ? load16<ALIGN16>(bq + kt * 32) : u32x4_t{0u, 0u, 0u, 0u};
+      rs = bok ? (uint32_t)bs[kt * 2] : 127u;
+    }
   };
   auto lstore = [&](int buf) {
 #pragma unroll
@@ -433,13 +484,20 @@ __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
       const int r = (tid >> 3) + 32 * i;
       *reinterpret_cast<u32x4_t*>(&sA[buf][r * TL_LDK + akc * 8]) = ra[i];
     }
-    uint16_t* dst = &sB[buf][bcol * TL_LDK + bgs * 32];
-    const bool hw = true;
+    if constexpr (BDENSE) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      uint32_t d[4];
-      mx_dword_to_bf16x8(rb[q], rs, hw, d);
-      *reinterpret_cast<u32x4_t*>(dst + q * 8) = u32x4_t{d[0], d[1], d[2], d[3]};
+      for (int i = 0; i < 4; ++i) {
+        const int r = (tid >> 3) + 32 * i;
+        *reinterpret_cast<u32x4_t*>(&sB[buf][r * TL_LDK + akc * 8]) = rbd[i];
+      }
+    } else {
+      uint16_t* dst = &sB[buf][bcol * TL_LDK + bgs * 32];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t d[4];
+        mx_dword_to_bf16x8(rb[q], rs, true, d);
+        *reinterpret_cast<u32x4_t*>(dst + q * 8) = u32x4_t{d[0], d[1], d[2], d[3]};
+      }
     }
   };
 
@@ -460,8 +518,9 @@ __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
   const int n_a = n0 + cb0 + l32;
   const int n_b = n0 + cb1 + l32;
   const int64_t eb = (int64_t)e * a.N;
-  float bias0, bias1;
-  if constexpr (EPI == EPI_SWIGLU) {
+  float bias0 = 0.f, bias1 = 0.f;
+  if constexpr (EPI == EPI_SWIGLU_BWD) {
+  } else if constexpr (EPI == EPI_SWIGLU) {
     bias0 = ng_sw < a.N ? bias_at(a.bias, a.bias_dtype, eb + ng_sw) : 0.f;
     bias1 = ng_sw < a.N ? bias_at(a.bias, a.bias_dtype, eb + ng_sw + 1) : 0.f;
   } else {
@@ -779,6 +838,21 @@ static Workspace carve(void* base, int64_t T, int64_t H, int64_t I, int64_t E, i
   return w;
 }
 
+// Grouped GEMM with a dense bf16 B [E][N][K] (K % 64 == 0): the backward
+// products with transposed weights, fed by the dequant kernel's [K, N] output.
+template <int EPI>
+static int launch_gemm_dense(const GemmArgs& a, int64_t P, hipStream_t st) {
+  const int64_t max_tiles = (P + TL_BM - 1) / TL_BM + a.E;
+  const int64_t grid = align_up(max_tiles * a.n_tiles_n, 8);
+  if (grid > INT32_MAX) {
+    set_error("dense grouped GEMM: grid too large");
+    return BSA_EINVAL;
+  }
+  hipLaunchKernelGGL((moe_tiled_kernel<EPI, true, true>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  BSA_LAUNCH_CHECK("dense grouped GEMM launch");
+  return BSA_OK;
+}
+
 template <int EPI>
 static int launch_gemm(const GemmArgs& a, int path, int64_t P, hipStream_t st) {
   const bool align16 = (reinterpret_cast<uintptr_t>(a.Bq) % 16) == 0;
@@ -815,9 +889,9 @@ static int launch_gemm(const GemmArgs& a, int path, int64_t P, hipStream_t st) {
       return BSA_EINVAL;
     }
     if (align16)
-      hipLaunchKernelGGL((moe_tiled_kernel<EPI, true>), dim3((unsigned)grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((moe_tiled_kernel<EPI, true, false>), dim3((unsigned)grid), dim3(256), 0, st, a);
     else
-      hipLaunchKernelGGL((moe_tiled_kernel<EPI, false>), dim3((unsigned)grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((moe_tiled_kernel<EPI, false, false>), dim3((unsigned)grid), dim3(256), 0, st, a);
   }
   BSA_LAUNCH_CHECK("grouped GEMM launch");
   return BSA_OK;
@@ -1030,4 +1104,133 @@ extern "C" int bsa_moe_experts_fwd(
   if ((rc = stage_down(m, down_blocks, down_scales, down_bias, bias_dtype, w, path, st))) return rc;
   return launch_combine(w.y, router_indices, routing_weights, weight_dtype, w.pair_pos, (int)T,
                         (int)k, (int)H, out, out_dtype, st);
+}
+
+namespace bsa {
+
+struct BwdWorkspace {
+  uint16_t* w_gate_up;  // dense bf16 [E][H][2I] (dequant of gate_up: [K=H, N=2I])
+  uint16_t* w_down;     // dense bf16 [E][I][H]  (dequant of down:    [K=I, N=H])
+  uint16_t* dy;         // [P][H] bf16: dOut rows scaled by the routing weight
+  uint16_t* dgu;        // [P][2I] bf16: gradient of the gate_up pre-activations
+  float* dx;            // [P][H] f32: per-row input gradients
+  float* dw;            // [P] f32: routing-weight gradients
+  int64_t bytes;
+};
+
+static BwdWorkspace carve_bwd(void* base, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k) {
+  const int64_t P = T * k;
+  char* p = static_cast<char*>(base);
+  int64_t off = 0;
+  BwdWorkspace w{};
+  auto take = [&](int64_t bytes) {
+    char* r = p ? p + off : nullptr;
+    off = align_up(off + bytes, 256);
+    return r;
+  };
+  w.w_gate_up = reinterpret_cast<uint16_t*>(take(E * H * 2 * I * 2));
+  w.w_down = reinterpret_cast<uint16_t*>(take(E * I * H * 2));
+  w.dy = reinterpret_cast<uint16_t*>(take(P * H * 2));
+  w.dgu = reinterpret_cast<uint16_t*>(take(P * 2 * I * 2));
+  w.dx = reinterpret_cast<float*>(take(P * H * 4));
+  w.dw = reinterpret_cast<float*>(take(P * 4));
+  w.bytes = off;
+  return w;
+}
+
+}  // namespace bsa
+
+extern "C" int bsa_moe_bwd_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                                           int64_t* bytes) {
+  clear_error();
+  BSA_REQUIRE(bytes, "backward workspace size: null output pointer");
+  BSA_REQUIRE(T >= 0 && H > 0 && I > 0 && E > 0 && k > 0, "backward workspace size: bad shape");
+  *bytes = carve_bwd(nullptr, T, H, I, E, k).bytes;
+  return BSA_OK;
+}
+
+extern "C" int bsa_moe_experts_bwd(
+    const void* grad_out, int grad_dtype, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+    const int64_t* router_indices, const void* routing_weights, int weight_dtype,
+    const void* gate_up_blocks, const void* gate_up_scales, const void* down_blocks,
+    const void* down_scales, float alpha, float limit, void* workspace, int64_t workspace_bytes,
+    const void* save_gate_up, void* bwd_workspace, int64_t bwd_workspace_bytes, void* grad_hidden,
+    int grad_hidden_dtype, float* grad_weights, void* stream) {
+  clear_error();
+  const MoeShape m{T, H, I, E, k};
+  int rc = check_shape(m, "experts bwd");
+  if (rc || T == 0) return rc;
+  BSA_REQUIRE(dtype_ok(grad_dtype) && dtype_ok(weight_dtype) && dtype_ok(grad_hidden_dtype),
+              "experts bwd: bad dtype code");
+  BSA_REQUIRE(H % 64 == 0 && I % 32 == 0, "experts bwd: needs hidden % 64 == 0 and intermediate % 32 == 0");
+  BSA_REQUIRE(grad_out && router_indices && routing_weights && gate_up_blocks && gate_up_scales &&
+                  down_blocks && down_scales && save_gate_up && bwd_workspace,
+              "experts bwd: null pointer");
+  Workspace w;
+  if ((rc = check_ws(m, workspace, workspace_bytes, &w, "experts bwd"))) return rc;
+  const BwdWorkspace b = carve_bwd(bwd_workspace, T, H, I, E, k);
+  BSA_REQUIRE(bwd_workspace_bytes >= b.bytes, "experts bwd: backward workspace of %lld bytes, need %lld",
+              (long long)bwd_workspace_bytes, (long long)b.bytes);
+  BSA_REQUIRE(reinterpret_cast<uintptr_t>(bwd_workspace) % 256 == 0,
+              "experts bwd: backward workspace must be 256-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t P = T * k;
+
+  // 1. routing-weight gradients and the weighted output gradient rows
+  if ((rc = launch_bwd_prep(grad_out, grad_dtype, w.y, routing_weights, weight_dtype, w.pair_pos,
+                            (int)P, (int)k, (int)H, b.dy, grad_weights ? grad_weights : b.dw, st)))
+    return rc;
+  if (!grad_hidden) return BSA_OK;
+
+  // 2. dense bf16 weights of the routed experts, in the [K, N] orientation
+  if ((rc = launch_dequant_bf16_routed(static_cast<const uint8_t*>(gate_up_blocks),
+                                       static_cast<const uint8_t*>(gate_up_scales), b.w_gate_up, E,
+                                       2 * I, H / 32, w.counts, st)))
+    return rc;
+  if ((rc = launch_dequant_bf16_routed(static_cast<const uint8_t*>(down_blocks),
+                                       static_cast<const uint8_t*>(down_scales), b.w_down, E, H,
+                                       I / 32, w.counts, st)))
+    return rc;
+
+  // 3. d(act) = dY @ W_down^T with the SwiGLU backward in the epilogue -> d(gate_up)
+  GemmArgs g{};
+  g.A = b.dy;
+  g.lda = H;
+  g.Bd = b.w_down;  // rows = intermediate index, K = hidden
+  g.counts = w.counts;
+  g.offsets = w.offsets;
+  g.E = (int)E;
+  g.N = (int)I;
+  g.K = (int)H;
+  g.out = b.dgu;
+  g.ldo = 2 * I;
+  g.save_pre = const_cast<float*>(static_cast<const float*>(save_gate_up));
+  g.alpha = alpha;
+  g.limit = limit;
+  g.tiles = w.tiles;
+  g.num_tiles = w.num_tiles;
+  g.n_tiles_n = (int)((I + TL_BN - 1) / TL_BN);
+  if ((rc = launch_gemm_dense<EPI_SWIGLU_BWD>(g, P, st))) return rc;
+
+  // 4. dX rows = d(gate_up) @ W_gate_up^T
+  GemmArgs g2{};
+  g2.A = b.dgu;
+  g2.lda = 2 * I;
+  g2.Bd = b.w_gate_up;  // rows = hidden index, K = 2I
+  g2.counts = w.counts;
+  g2.offsets = w.offsets;
+  g2.E = (int)E;
+  g2.N = (int)H;
+  g2.K = (int)(2 * I);
+  g2.out = b.dx;
+  g2.ldo = H;
+  g2.out_dtype = DT_F32;
+  g2.tiles = w.tiles;
+  g2.num_tiles = w.num_tiles;
+  g2.n_tiles_n = (int)((H + TL_BN - 1) / TL_BN);
+  if ((rc = launch_gemm_dense<EPI_STORE>(g2, P, st))) return rc;
+
+  // 5. per-token sum of its k rows (ascending expert order)
+  return launch_combine(b.dx, router_indices, nullptr, DT_F32, w.pair_pos, (int)T, (int)k, (int)H,
+                        grad_hidden, grad_hidden_dtype, st);
 }

@@ -166,7 +166,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
     const int ps = pair_pos[(int64_t)t * k + p];
     if (ps < 0) continue;
     const int64_t e = idx[(int64_t)t * k + p];
-    const float wv = load_f32(w, (int64_t)t * k + p, w_dtype);
+    const float wv = w ? load_f32(w, (int64_t)t * k + p, w_dtype) : 1.0f;
     // insertion by expert id (ties keep slot order)
     int j = n;
     while (j > 0 && ex[j - 1] > e) {
@@ -208,6 +208,44 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
       store_f32_as(out, obase + h, acc, out_dtype);
     }
   }
+}
+
+// Backward prep, one wave per (token, slot) pair (block_streamer/gptoss.py:175
+// differentiated): grad_w[t,p] = <dOut[t], y[pos]> (y = down output + bias,
+// before the routing weight) and dY[pos] = bf16(dOut[t] * w[t,p]).
+__global__ __launch_bounds__(256) void moe_bwd_prep_kernel(
+    const void* __restrict__ dout, int dout_dtype, const float* __restrict__ y,
+    const void* __restrict__ w, int w_dtype, const int* __restrict__ pair_pos, int P, int k,
+    int H, uint16_t* __restrict__ dy, float* __restrict__ grad_w) {
+  const int lane = threadIdx.x & 63;
+  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pair >= P) return;
+  const int pos = pair_pos[pair];
+  if (pos < 0) {
+    if (lane == 0) grad_w[pair] = 0.f;
+    return;
+  }
+  const int64_t t = pair / k;
+  const float wv = load_f32(w, pair, w_dtype);
+  float dot = 0.f;
+  for (int h = lane; h < H; h += 64) {
+    const float g = load_f32(dout, t * H + h, dout_dtype);
+    dot += g * y[(int64_t)pos * H + h];
+    dy[(int64_t)pos * H + h] = (uint16_t)f32_to_bf16_bits(g * wv);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) dot += __shfl_xor(dot, off);
+  if (lane == 0) grad_w[pair] = dot;
+}
+
+int launch_bwd_prep(const void* dout, int dout_dtype, const float* y, const void* w, int w_dtype,
+                    const int* pair_pos, int P, int k, int H, uint16_t* dy, float* grad_w,
+                    hipStream_t st) {
+  if (P == 0) return BSA_OK;
+  hipLaunchKernelGGL(moe_bwd_prep_kernel, dim3((P + 3) / 4), dim3(256), 0, st, dout, dout_dtype, y,
+                     w, w_dtype, pair_pos, P, k, H, dy, grad_w);
+  BSA_LAUNCH_CHECK("backward prep launch");
+  return BSA_OK;
 }
 
 int launch_dispatch(const int64_t* idx, int P, int E, int BM, int* counts, int* offsets,

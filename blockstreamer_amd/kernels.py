@@ -193,3 +193,51 @@ class MoEStages:
         self.down()
         self.combine()
         return self.out
+
+
+def moe_bwd_workspace_bytes(T: int, H: int, I: int, E: int, k: int) -> int:
+    import ctypes
+    out = ctypes.c_int64(0)
+    _lib.call("bsa_moe_bwd_workspace_bytes", T, H, I, E, k, ctypes.byref(out))
+    return out.value
+
+
+def moe_experts_backward(grad_out: Tensor, hidden: Tensor, router_indices: Tensor,
+                         routing_weights: Tensor, gate_up_blocks: Tensor, gate_up_scales: Tensor,
+                         down_blocks: Tensor, down_scales: Tensor, workspace: Tensor,
+                         gate_up_pre: Tensor, alpha: float = 1.702, limit: float = 7.0, *,
+                         need_hidden: bool = True, need_weights: bool = True):
+    """Input-gradient backward of ``moe_experts_forward(..., save=True)``.
+
+    Returns ``(grad_hidden or None, grad_routing_weights or None)`` in the
+    dtypes of ``hidden`` and ``routing_weights``.  Expert weights and biases
+    get no gradient (frozen under LoRA, block_streamer/lora.py:138-148).
+    """
+    T, H = hidden.shape
+    k = router_indices.shape[1]
+    E = gate_up_blocks.shape[0]
+    I = gate_up_blocks.shape[1] // 2
+    dev = _lib.require_gpu(grad_out, hidden, router_indices, routing_weights, workspace)
+    if T == 0:
+        return (torch.zeros_like(hidden) if need_hidden else None,
+                torch.zeros_like(routing_weights) if need_weights else None)
+    g = grad_out.contiguous()
+    g_code = _lib.dtype_code(g.dtype)
+    idx = router_indices.to(torch.int64).contiguous()
+    w = routing_weights.contiguous()
+    bwd_bytes = moe_bwd_workspace_bytes(T, H, I, E, k)
+    bws = _aligned_bytes(bwd_bytes, dev)
+    grad_h = torch.empty((T, H), dtype=hidden.dtype, device=dev) if need_hidden else None
+    grad_w = torch.empty((T, k), dtype=torch.float32, device=dev) if need_weights else None
+    with torch.cuda.device(dev):
+        _lib.call("bsa_moe_experts_bwd", g.data_ptr(), g_code, T, H, I, E, k, idx.data_ptr(),
+                  w.data_ptr(), _lib.dtype_code(w.dtype), _as_u8(gate_up_blocks).data_ptr(),
+                  _as_u8(gate_up_scales).data_ptr(), _as_u8(down_blocks).data_ptr(),
+                  _as_u8(down_scales).data_ptr(), float(alpha), float(limit),
+                  workspace.data_ptr(), workspace.numel(), gate_up_pre.data_ptr(), bws.data_ptr(),
+                  bwd_bytes, grad_h.data_ptr() if grad_h is not None else None,
+                  _lib.dtype_code(hidden.dtype),
+                  grad_w.data_ptr() if grad_w is not None else None, _lib.stream_handle(dev))
+    if grad_w is not None:
+        grad_w = grad_w.to(routing_weights.dtype)
+    return grad_h, grad_w

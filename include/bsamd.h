@@ -147,6 +147,42 @@ int bsa_moe_combine(const int64_t *router_indices, const void *routing_weights,
                     int64_t workspace_bytes, void *out, int out_dtype,
                     void *stream);
 
+/*
+ * Bytes of the extra workspace bsa_moe_experts_bwd needs (dense bf16 copies
+ * of the routed experts' weights and the per-row gradients).
+ */
+int bsa_moe_bwd_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
+                                int64_t k, int64_t *bytes);
+
+/*
+ * Input-gradient backward of bsa_moe_experts_fwd (the LoRA training path,
+ * where expert weights and biases are frozen).
+ *
+ * Replaces the autograd of block_streamer/gptoss.py:137-177:
+ * _MXFP4Matmul.backward (:64-71, grad @ W^T re-dequantising from the packed
+ * tensors) for both projections, the backward of the clamped SwiGLU
+ * (:130-135) and of the routing-weight product and index_add_ (:175-176).
+ *
+ *   grad_out        grad_dtype [T, H]
+ *   workspace       the forward's workspace, unchanged since that call
+ *   save_gate_up    the forward's float32 [T*k, 2I] pre-activations
+ *   bwd_workspace   >= bsa_moe_bwd_workspace_bytes(...) bytes, 256-aligned
+ *   grad_hidden     grad_hidden_dtype [T, H], or NULL to skip
+ *   grad_weights    float32 [T, k] gradient of routing_weights, or NULL
+ *
+ * H must be a multiple of 64.  Dropped (token, slot) pairs get a zero
+ * routing-weight gradient.
+ */
+int bsa_moe_experts_bwd(
+    const void *grad_out, int grad_dtype, int64_t T, int64_t H, int64_t I,
+    int64_t E, int64_t k, const int64_t *router_indices,
+    const void *routing_weights, int weight_dtype, const void *gate_up_blocks,
+    const void *gate_up_scales, const void *down_blocks,
+    const void *down_scales, float alpha, float limit, void *workspace,
+    int64_t workspace_bytes, const void *save_gate_up, void *bwd_workspace,
+    int64_t bwd_workspace_bytes, void *grad_hidden, int grad_hidden_dtype,
+    float *grad_weights, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,168 @@
+"""Input-gradient backward parity on the GPU (the LoRA training path).
+
+Reference gradients come from torch autograd of the float32 oracle (CPU) or,
+at the gpt-oss-20b shape, of a float32 torch reference on the GPU.
+Tolerance for gradients: relative L2 <= 1e-2 and max-abs <= 5e-2 * max|ref|
+-- the backward rounds twice more to bfloat16 than the forward (the weighted
+output gradient and the gate_up gradient feed bf16 MFMAs).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from blockstreamer_amd import gptoss, kernels, synthetic
+from tests.conftest import announce
+from tests.moe_util import errors, expert_args
+
+pytestmark = pytest.mark.gpu
+
+GRAD_REL_L2 = 1e-2
+GRAD_MAX_ABS = 5e-2
+
+
+def assert_grad_close(got, want, what):
+    rel_l2, max_abs, scale = errors(got, want)
+    msg = f"{what}: rel_l2={rel_l2:.3e} max_abs={max_abs:.3e} (|ref|max={scale:.3e})"
+    print(msg)
+    assert rel_l2 <= GRAD_REL_L2, msg
+    assert max_abs <= GRAD_MAX_ABS * max(scale, 1e-30), msg
+
+
+def _oracle_grads(t, idx, w, g):
+    h = t["hidden"].cpu().float().requires_grad_(True)
+    wr = w.cpu().float().requires_grad_(True)
+    out = oracle.experts_ref(h, idx.cpu(), wr, *[a.cpu() for a in expert_args(t)])
+    out.backward(g.cpu().float())
+    return out.detach(), h.grad, wr.grad
+
+
+def _gpu_grads(t, idx, w, g):
+    h = t["hidden"].detach().clone().requires_grad_(True)
+    wr = w.detach().clone().requires_grad_(True)
+    args = expert_args(t)
+    out = gptoss._MoEExperts.apply(h, idx, wr, *args, 1.702, 7.0)
+    out.backward(g)
+    return out.detach(), h.grad, wr.grad
+
+
+CASES = [
+    # (E, k, H, I, T, scale_lo, scale_hi)
+    (8, 2, 256, 256, 64, 119, 129),
+    (8, 2, 256, 256, 64, 116, 120),
+    (16, 4, 512, 256, 129, 116, 120),
+    (4, 1, 128, 192, 77, 117, 121),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"E{c[0]}k{c[1]}H{c[2]}I{c[3]}T{c[4]}s{c[5]}" for c in CASES])
+def test_backward_vs_oracle_autograd(device, case):
+    E, k, H, I, T, lo, hi = case
+    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=T + E, scale_lo=lo,
+                            scale_hi=hi, device=device)
+    idx, w = synthetic.random_routing(T, E, k, seed=T + 3, dtype=torch.float32, device=device)
+    g = torch.randn(T, H, generator=torch.Generator().manual_seed(T), dtype=torch.float32)
+    g = g.to(torch.bfloat16).to(device)
+    announce(f"moe backward {case}")
+    out, gh, gw = _gpu_grads(t, idx, w, g)
+    _, rh, rw = _oracle_grads(t, idx, w, g)
+    assert gh.dtype == torch.bfloat16 and gw.dtype == torch.float32
+    assert_grad_close(gh, rh, f"d hidden {case}")
+    assert_grad_close(gw, rw, f"d routing weights {case}")
+
+
+def test_backward_through_module_like_recompute(device):
+    """functional_call + autograd.grad on [hidden, weights], as _autograd.py:127-175 does."""
+    from torch.func import functional_call
+    from transformers.models.gpt_oss.configuration_gpt_oss import GptOssConfig
+
+    E, k, H, I, T = 8, 2, 256, 256, 48
+    cfg = GptOssConfig(num_local_experts=E, hidden_size=H, intermediate_size=I,
+                       num_experts_per_tok=k, num_hidden_layers=1)
+    mod = gptoss.MXFP4Experts(cfg, torch.bfloat16)
+    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=41, scale_lo=116,
+                            scale_hi=120, device=device)
+    state = {n: t[n] for n in ("gate_up_proj_blocks", "gate_up_proj_scales", "gate_up_proj_bias",
+                               "down_proj_blocks", "down_proj_scales", "down_proj_bias")}
+    idx, w = synthetic.random_routing(T, E, k, seed=42, dtype=torch.bfloat16, device=device)
+    h = t["hidden"].detach().clone().requires_grad_(True)
+    wr = w.detach().clone().requires_grad_(True)
+    announce("moe backward via functional_call")
+    with torch.enable_grad():
+        out = functional_call(mod, state, (h, idx, wr), strict=True)
+        g = torch.ones_like(out)
+        gh, gw = torch.autograd.grad(out, [h, wr], g)
+    _, rh, rw = _oracle_grads(t, idx, w.float(), g.float())
+    assert gw.dtype == torch.bfloat16
+    assert_grad_close(gh, rh, "module d hidden")
+    assert_grad_close(gw.float(), rw, "module d routing weights")
+
+
+def test_no_grad_forward_saves_nothing(device):
+    E, k, H, I, T = 8, 2, 256, 256, 16
+    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=5, scale_lo=119, scale_hi=125,
+                            device=device)
+    idx, w = synthetic.random_routing(T, E, k, seed=6, device=device)
+    with torch.no_grad():
+        out = gptoss._MoEExperts.apply(t["hidden"], idx, w, *expert_args(t), 1.702, 7.0)
+    assert out.grad_fn is None
+
+
+def _gpu_fp32_reference_grads(t, idx, w, g):
+    """float32 torch autograd on the GPU, dense weights from the dequant kernel."""
+    h = t["hidden"].float().requires_grad_(True)
+    wr = w.float().requires_grad_(True)
+    out = torch.zeros_like(h)
+    for e in torch.unique(idx).tolist():
+        tok, pos = torch.where(idx == e)
+        wgu = kernels.dequantize_mxfp4(t["gate_up_proj_blocks"][e:e + 1],
+                                       t["gate_up_proj_scales"][e:e + 1], torch.float32)[0]
+        wdn = kernels.dequantize_mxfp4(t["down_proj_blocks"][e:e + 1],
+                                       t["down_proj_scales"][e:e + 1], torch.float32)[0]
+        gu = h[tok] @ wgu + t["gate_up_proj_bias"][e].float()
+        o = oracle.apply_gate_ref(gu) @ wdn + t["down_proj_bias"][e].float()
+        out = out.index_add(0, tok, o * wr[tok, pos, None])
+    out.backward(g.float())
+    return h.grad, wr.grad
+
+
+def test_backward_gptoss_20b_shape(device):
+    E, k, H, I, T = 32, 4, 2880, 2880, 512
+    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=23, scale_lo=116, scale_hi=120,
+                            device=device)
+    idx, w = synthetic.random_routing(T, E, k, seed=24, dtype=torch.float32, device=device)
+    g = (torch.randn(T, H, device=device) * 0.1).to(torch.bfloat16)
+    announce("moe backward 20b shape")
+    _, gh, gw = _gpu_grads(t, idx, w, g)
+    rh, rw = _gpu_fp32_reference_grads(t, idx, w, g)
+    assert_grad_close(gh, rh, "20b d hidden")
+    assert_grad_close(gw, rw, "20b d routing weights")
+
+
+def test_mxfp4_matmul_gradient_and_memory(device):
+    """tests/test_offload.py:369-402 on this build: float32 mxfp4_matmul is
+    bit-equal to x @ dequantize_expert(...), gradients too, and the dense
+    weight is not retained across calls."""
+    torch.manual_seed(0)
+    blocks = torch.randint(0, 255, (1, 64, 4, 16), dtype=torch.uint8, device=device)
+    scales = torch.randint(120, 134, (1, 64, 4), dtype=torch.uint8, device=device)
+    weight = gptoss.dequantize_expert(blocks, scales, torch.float32)
+    x = torch.randn(8, 128, device=device, requires_grad=True)
+    reference_x = x.detach().clone().requires_grad_(True)
+    announce("mxfp4_matmul gradient and memory")
+    actual = gptoss.mxfp4_matmul(x, blocks, scales)
+    expected = reference_x @ weight
+    assert torch.equal(actual, expected)
+    grad = torch.randn_like(actual)
+    actual.backward(grad)
+    expected.backward(grad)
+    assert torch.equal(x.grad, reference_x.grad)
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    chained = [gptoss.mxfp4_matmul(x, blocks, scales) for _ in range(64)]
+    peak = torch.cuda.max_memory_allocated() - base
+    sum(y.sum() for y in chained).backward()
+    dense_bytes = weight.numel() * weight.element_size()
+    assert peak < dense_bytes * 16
