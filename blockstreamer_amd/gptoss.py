@@ -175,6 +175,99 @@ class MXFP4Experts(nn.Module):
         return out.reshape(shape)
 
 
+class _Router(torch.autograd.Function):
+    """Fused router forward; backward through the softmax over the top-k
+    values and the linear layer, as torch autograd differentiates
+    TF/models/gpt_oss/modeling_gpt_oss.py:127-129 (gradients flow only into the
+    k selected logits)."""
+
+    @staticmethod
+    def forward(ctx, hidden, weight, bias, top_k):
+        logits, scores, idx = kernels.router_forward(hidden, weight, bias, top_k)
+        ctx.save_for_backward(hidden, weight, scores, idx)
+        ctx.has_bias = bias is not None
+        ctx.mark_non_differentiable(idx)
+        return logits, scores, idx
+
+    @staticmethod
+    def backward(ctx, d_logits, d_scores, _d_idx):
+        hidden, weight, scores, idx = ctx.saved_tensors
+        T, E = hidden.shape[0], weight.shape[0]
+        dl = torch.zeros((T, E), dtype=torch.float32, device=hidden.device)
+        if d_logits is not None:
+            dl += d_logits.float()
+        if d_scores is not None:
+            s = scores.float()
+            ds = d_scores.float()
+            dvals = s * (ds - (s * ds).sum(dim=-1, keepdim=True))  # softmax backward
+            dl.scatter_add_(1, idx, dvals)
+        dl = dl.to(hidden.dtype)
+        dh = dl @ weight.to(hidden.dtype) if ctx.needs_input_grad[0] else None
+        dw = dl.t() @ hidden if ctx.needs_input_grad[1] else None
+        db = dl.sum(0) if (ctx.has_bias and ctx.needs_input_grad[2]) else None
+        return dh, dw, db, None
+
+
+class MXFP4TopKRouter(nn.Module):
+    """Drop-in for ``GptOssTopKRouter`` (TF/models/gpt_oss/modeling_gpt_oss.py:117-131)
+    with the logits, top-k and softmax in one HIP kernel.  Same parameter
+    names (``weight [E, H]``, ``bias [E]``) and return value
+    ``(logits, scores, indices)``."""
+
+    def __init__(self, config, dtype: torch.dtype = torch.bfloat16) -> None:
+        super().__init__()
+        self.top_k = config.num_experts_per_tok
+        self.num_experts = config.num_local_experts
+        self.hidden_dim = config.hidden_size
+        self.weight = nn.Parameter(torch.zeros(self.num_experts, self.hidden_dim, dtype=dtype))
+        self.bias = nn.Parameter(torch.zeros(self.num_experts, dtype=dtype))
+
+    def forward(self, hidden_states: Tensor):
+        flat = hidden_states.reshape(-1, self.hidden_dim)
+        return _Router.apply(flat, self.weight, self.bias, self.top_k)
+
+
+class MXFP4MLP(nn.Module):
+    """Drop-in for ``GptOssMLP`` (TF/models/gpt_oss/modeling_gpt_oss.py:133-146):
+    fused router plus packed experts; ``forward(h [B, S, H])`` returns
+    ``(out [B, S, H], router_scores [T, k])``."""
+
+    def __init__(self, config, dtype: torch.dtype = torch.bfloat16) -> None:
+        super().__init__()
+        self.router = MXFP4TopKRouter(config, dtype)
+        self.experts = MXFP4Experts(config, dtype)
+
+    def forward(self, hidden_states: Tensor):
+        batch_size, sequence_length, hidden_dim = hidden_states.shape
+        flat = hidden_states.reshape(-1, hidden_dim)
+        _, router_scores, router_indices = self.router(flat)
+        out = self.experts(flat, router_indices, router_scores)
+        return out.reshape(batch_size, sequence_length, hidden_dim), router_scores
+
+
+def install_mxfp4_router(model: nn.Module, config, dtype=torch.bfloat16) -> int:
+    """Swap every ``GptOssTopKRouter`` for the fused ``MXFP4TopKRouter``.
+
+    No counterpart in the reference, which keeps the transformers router;
+    parameter names are unchanged, so checkpoints and shards bind as before.
+    Returns the number of layers changed.
+    """
+    from transformers.models.gpt_oss import modeling_gpt_oss as gpt_oss
+
+    replaced = 0
+    for layer in model.model.layers:
+        if isinstance(layer.mlp.router, gpt_oss.GptOssTopKRouter):
+            old = layer.mlp.router
+            new = MXFP4TopKRouter(config, dtype)
+            if old.weight.device.type != "meta":
+                with torch.no_grad():
+                    new.weight.copy_(old.weight)
+                    new.bias.copy_(old.bias)
+            layer.mlp.router = new
+            replaced += 1
+    return replaced
+
+
 def install_mxfp4_experts(model: nn.Module, config, dtype=torch.bfloat16) -> int:
     """Swap every dense GptOssExperts for the packed, fused version.
 

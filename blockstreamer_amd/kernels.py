@@ -241,3 +241,46 @@ def moe_experts_backward(grad_out: Tensor, hidden: Tensor, router_indices: Tenso
     if grad_w is not None:
         grad_w = grad_w.to(routing_weights.dtype)
     return grad_h, grad_w
+
+
+def router_forward(hidden: Tensor, weight: Tensor, bias: Tensor | None, top_k: int):
+    """GptOssTopKRouter.forward (TF/models/gpt_oss/modeling_gpt_oss.py:126-131).
+
+    Returns ``(logits [T, E], scores [T, k], indices [T, k] int64)`` in the
+    dtype of ``hidden`` (the module dtype).
+    """
+    if hidden.dim() != 2:
+        raise ValueError(f"router input must be [tokens, hidden], got {tuple(hidden.shape)}")
+    T, H = hidden.shape
+    E = weight.shape[0]
+    if tuple(weight.shape) != (E, H):
+        raise ValueError(f"router weight must be [{E}, {H}], got {tuple(weight.shape)}")
+    dev = _lib.require_gpu(hidden, weight, bias)
+    dt = hidden.dtype
+    code = _lib.dtype_code(dt)
+    h = hidden.contiguous()
+    w = weight.to(dt).contiguous()
+    b = bias.to(dt).contiguous() if bias is not None else None
+    logits = torch.empty((T, E), dtype=dt, device=dev)
+    scores = torch.empty((T, top_k), dtype=dt, device=dev)
+    idx = torch.empty((T, top_k), dtype=torch.int64, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("bsa_router_fwd", h.data_ptr(), code, T, H, E, top_k, w.data_ptr(),
+                  b.data_ptr() if b is not None else None, logits.data_ptr(), scores.data_ptr(),
+                  idx.data_ptr(), _lib.stream_handle(dev))
+    return logits, scores, idx
+
+
+def router_topk(logits: Tensor, top_k: int):
+    """Top-k (descending, lower index first on ties) and softmax of given logits."""
+    if logits.dim() != 2:
+        raise ValueError("logits must be [tokens, experts]")
+    T, E = logits.shape
+    dev = _lib.require_gpu(logits)
+    lg = logits.contiguous()
+    scores = torch.empty((T, top_k), dtype=lg.dtype, device=dev)
+    idx = torch.empty((T, top_k), dtype=torch.int64, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("bsa_router_topk", lg.data_ptr(), _lib.dtype_code(lg.dtype), T, E, top_k,
+                  scores.data_ptr(), idx.data_ptr(), _lib.stream_handle(dev))
+    return scores, idx

@@ -148,6 +148,29 @@ int bsa_moe_combine(const int64_t *router_indices, const void *routing_weights,
                     void *stream);
 
 /*
+ * Router forward.
+ *
+ * Replaces transformers models/gpt_oss/modeling_gpt_oss.py:126-131
+ * (GptOssTopKRouter.forward, called at :143):
+ *   logits  dtype [T, E] = hidden [T, H] @ weight[E, H]^T + bias[E]
+ *   indices int64 [T, k] = top-k of logits, descending (equal logits: lower
+ *           index first; -0 == +0)
+ *   scores  dtype [T, k] = softmax of the k selected logits (float32, rounded)
+ * dtype is the module dtype of hidden, weight, bias (bias may be NULL).
+ * E <= 256, k <= 16.
+ */
+int bsa_router_fwd(const void *hidden, int dtype, int64_t T, int64_t H,
+                   int64_t E, int64_t k, const void *weight, const void *bias,
+                   void *logits, void *scores, int64_t *indices, void *stream);
+
+/*
+ * Top-k and softmax of given logits [T, E] (modeling_gpt_oss.py:128-129):
+ * the same selection and softmax as bsa_router_fwd.
+ */
+int bsa_router_topk(const void *logits, int dtype, int64_t T, int64_t E,
+                    int64_t k, void *scores, int64_t *indices, void *stream);
+
+/*
  * Bytes of the extra workspace bsa_moe_experts_bwd needs (dense bf16 copies
  * of the routed experts' weights and the per-row gradients).
  */
