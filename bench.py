@@ -9,10 +9,11 @@ resident in HBM.  A step is one dequantisation of the whole layer (both
 projections).  ``value`` is the whole-job algorithmic bandwidth (bytes read
 plus bytes written, 8,062,156,800 B per step) over the timed steps.
 
-``roofline`` covers the dequant kernel, timed per launch with HIP events on
-the launch stream; ``traffic`` is the measured HBM bytes per step from the
-rocprofv3 FETCH_SIZE/WRITE_SIZE runs recorded in profiles/traffic.json (null
-when absent).  ``cpu_baseline`` times the oracle's torch restatement of the
+``roofline`` covers the dominant launch, the gate_up dequantisation
+(5,374,771,200 algorithmic bytes per launch), timed per launch with HIP events
+on the launch stream; ``traffic`` is that launch's measured HBM bytes from the
+rocprofv3 FETCH_SIZE/WRITE_SIZE runs recorded in profiles/traffic.json, each
+counter scaled by its plain-copy calibration factor (null when absent).  ``cpu_baseline`` times the oracle's torch restatement of the
 reference dequant on the host cores over a bounded sample of the same
 workload.
 """
@@ -43,13 +44,14 @@ def dequant_bytes(E: int, R: int, G: int, out_elem: int = 2) -> int:
     return E * R * G * 16 + E * R * G + E * R * G * 32 * out_elem
 
 
-def traffic_record(key: str):
+def traffic_record(key: str, field: str):
+    """Measured HBM bytes (calibrated FETCH_SIZE + WRITE_SIZE) from profiles/traffic.json."""
     path = ROOT / "profiles" / "traffic.json"
     if not path.exists():
         return None
     try:
-        return json.loads(path.read_text()).get(key)
-    except (OSError, ValueError):
+        return json.loads(path.read_text()).get(key, {}).get(field)
+    except (OSError, ValueError, AttributeError):
         return None
 
 
@@ -114,9 +116,9 @@ def bench_dequant(args) -> dict:
     wall = time.perf_counter() - t0
     gu_ms = [e[0].elapsed_time(e[1]) for e in evs]
     dn_ms = [e[1].elapsed_time(e[2]) for e in evs]
-    kern_s = (sum(gu_ms) + sum(dn_ms)) / 1e3
-    achieved = step_bytes * args.steps / kern_s / 1e9
-    traffic = traffic_record("dequant_mxfp4_gptoss120b_layer")
+    gu_launch_ms = statistics.mean(gu_ms)
+    achieved = bytes_gu / (gu_launch_ms / 1e3) / 1e9
+    traffic = traffic_record("dequant_mxfp4_gptoss120b_layer", "gate_up_launch_bytes")
     return {
         "metric": "MoE layer tokens/s + MXFP4 dequant GB/s, gpt-oss-120b shape, 1xMI355X",
         "value": round(step_bytes * args.steps / wall / 1e9, 2),
@@ -138,7 +140,10 @@ def bench_dequant(args) -> dict:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "dequant_vec_kernel<bf16>",
+            "kernel": "dequant_vec_kernel<bf16>, gate_up launch [128,5760,90,16] -> [128,2880,5760]",
+            "algorithmic_bytes": bytes_gu,
+            "launch_ms": round(gu_launch_ms, 4),
+            "layer_kernel_GB_per_s": round(step_bytes * args.steps / ((sum(gu_ms) + sum(dn_ms)) / 1e3) / 1e9, 1),
         },
     }
 
@@ -166,8 +171,6 @@ def _median_ms(pairs):
 
 
 def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int) -> dict:
-    import torch.nn.functional as F
-
     from blockstreamer_amd import kernels, synthetic
 
     dev = torch.device("cuda", 0)
@@ -179,10 +182,9 @@ def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int
                                 "down_proj_blocks", "down_proj_scales", "down_proj_bias"))
 
     def route():
-        # the reference router (TF modeling_gpt_oss.py:126-131) as torch ops
-        logits = F.linear(x, t["router_weight"], t["router_bias"])
-        vals, idx = torch.topk(logits, k, dim=-1)
-        return idx, torch.softmax(vals, dim=1, dtype=vals.dtype)
+        # fused router kernel (logits, top-k, softmax over the top-k)
+        _, scores, idx = kernels.router_forward(x, t["router_weight"], t["router_bias"], k)
+        return idx, scores
 
     def step():
         idx, w = route()
@@ -238,6 +240,10 @@ def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int
                            "unit": "GB/s", "frac": round(hbm / HBM_PEAK_GBS, 4),
                            "kernel": "moe_stream_kernel gate_up + down",
                            "algorithmic_bytes": wbytes}
+        if T == 64:
+            gu_b = traffic_record("moe_layer_gptoss120b_decode_t64", "gate_up_hbm_bytes")
+            dn_b = traffic_record("moe_layer_gptoss120b_decode_t64", "down_hbm_bytes")
+            res["roofline"]["traffic"] = gu_b + dn_b if gu_b and dn_b else None
     else:
         res["roofline"] = {"bound": "mfma", "achieved": round(tfl, 1), "peak": BF16_PEAK_TFLOPS,
                            "unit": "TFLOP/s", "frac": round(tfl / BF16_PEAK_TFLOPS, 4),

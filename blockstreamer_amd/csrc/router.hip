@@ -6,19 +6,19 @@
 //   vals, idx = topk(logits, k)                sorted descending
 //   scores = softmax(vals, dim=1, dtype=vals.dtype)
 //
-// One workgroup per 16 tokens.  bf16 modules: logits by
-// v_mfma_f32_16x16x32_bf16 (float32 accumulation, bias added in float32, one
-// rounding to bf16, as a bf16 GEMM with a bias epilogue does); float32 and
-// float16 modules: float32 VALU dot products.  The rounded logits go to LDS;
-// each wave then selects the top-k of four tokens by k rounds of a wave-wide
-// arg-max on a 64-bit key (orderable value, then lower expert index first;
-// -0 and +0 compare equal), and takes the softmax of the k values in float32
-// rounded once to the module dtype.
+// bf16 modules (the gpt-oss case): a tiled logits kernel on
+// v_mfma_f32_16x16x32_bf16 (16x16 token x expert tiles, 32x32 once T >= 4096;
+// float32 accumulation, bias added in float32, one rounding to bf16, as a
+// bf16 GEMM with a bias epilogue does), then a top-k kernel over the bf16
+// logits.  float32 and float16 modules: one fused kernel of float32 VALU dot
+// products per 16 tokens.  Top-k: each wave selects one token's k largest by
+// k rounds of a wave-wide arg-max on a 64-bit key (orderable value, then
+// lower expert index first; -0 and +0 compare equal), and takes the softmax
+// of the k values in float32 rounded once to the module dtype.
 #include "bsa_common.h"
 
 namespace bsa {
 
-constexpr int RT_TOK = 16;      // tokens per workgroup
 constexpr int RT_MAX_E = 256;   // experts
 constexpr int RT_MAX_K = 16;
 
@@ -100,67 +100,136 @@ __device__ void topk_softmax_wave(const float* row, int E, int k, int lane, int 
   }
 }
 
-template <bool MFMA>
-__global__ __launch_bounds__(256) void router_kernel(const void* __restrict__ hidden, int dtype,
-                                                     int T, int H, int E, int k,
-                                                     const void* __restrict__ weight,
-                                                     const void* __restrict__ bias,
-                                                     void* __restrict__ logits,
-                                                     void* __restrict__ scores,
-                                                     int64_t* __restrict__ indices) {
-  __shared__ float s_log[RT_TOK][RT_MAX_E + 1];
+// bf16 logits tile: RT*16 tokens x RE*16 experts per workgroup.  The four
+// waves split the hidden dimension (wave w takes k-steps w, w+4, ...); their
+// float32 partial sums are added in wave order (deterministic), the bias is
+// added in float32 and the result rounded once to bf16.  Tiles are ordered
+// so that all expert tiles of one token tile run on one XCD (the token rows
+// are then fetched from HBM once into that XCD's L2).
+template <int RT, int RE>
+__global__ __launch_bounds__(256) void logits_bf16_kernel(const uint16_t* __restrict__ hidden,
+                                                          const uint16_t* __restrict__ weight,
+                                                          const uint16_t* __restrict__ bias,
+                                                          int T, int H, int E,
+                                                          uint16_t* __restrict__ logits) {
+  __shared__ float s_part[3][RT][RE][4][64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int t0 = blockIdx.x * RT_TOK;
+  const int lr = lane & 15;
+  const int lk = lane >> 4;
+  const int n_te = (E + 16 * RE - 1) / (16 * RE);
+  const int nblk = gridDim.x;
+  const int bid = blockIdx.x;
+  const int L = (nblk & 7) == 0 ? (bid & 7) * (nblk >> 3) + (bid >> 3) : bid;
+  const int t0 = (L / n_te) * 16 * RT;
+  const int e0 = (L % n_te) * 16 * RE;
+  const int nks = H / 32;
 
-  if constexpr (MFMA) {
-    // wave w: column blocks w, w+4, ... of 16 experts; A = 16 tokens
-    const int lr = lane & 15;
-    const int lk = lane >> 4;
-    const int nblk = (E + 15) / 16;
-    const uint16_t* hp = static_cast<const uint16_t*>(hidden);
-    const uint16_t* wp = static_cast<const uint16_t*>(weight);
-    const int tok = min(t0 + lr, T - 1);
-    const uint16_t* arow = hp + (int64_t)tok * H + lk * 8;
-    for (int b = wave; b < nblk; b += 4) {
-      const int e = b * 16 + lr;
-      const bool eok = e < E;
-      const uint16_t* brow = wp + (int64_t)(eok ? e : 0) * H + lk * 8;
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-      for (int ks = 0; ks < H / 32; ++ks) {
-        const rs16x8_t av = *reinterpret_cast<const rs16x8_t*>(arow + ks * 32);
-        rs16x8_t bv = *reinterpret_cast<const rs16x8_t*>(brow + ks * 32);
-        if (!eok) bv = rs16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av),
-                                                      __builtin_bit_cast(bf16x8_t, bv), acc, 0, 0,
-                                                      0);
-      }
-      // C: column (expert) lr, rows (tokens) 4*lk + j
-      const float bv = (eok && bias) ? ld_any(bias, e, dtype) : 0.f;
+  const uint16_t* arow[RT];
+  const uint16_t* brow[RE];
+  bool bok[RE];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (eok) s_log[4 * lk + j][e] = round_to(acc[j] + bv, dtype);
+  for (int r = 0; r < RT; ++r)
+    arow[r] = hidden + (int64_t)min(t0 + r * 16 + lr, T - 1) * H + lk * 8;
+#pragma unroll
+  for (int j = 0; j < RE; ++j) {
+    const int e = e0 + j * 16 + lr;
+    bok[j] = e < E;
+    brow[j] = weight + (int64_t)(bok[j] ? e : 0) * H + lk * 8;
+  }
+  f32x4_t acc[RT][RE];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int j = 0; j < RE; ++j) acc[r][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // D k-steps per round: all loads of a round are issued before its MFMAs
+  constexpr int D = RT * RE == 1 ? 8 : 4;
+  for (int base = wave; base < nks; base += 4 * D) {
+    rs16x8_t av[D][RT], bv[D][RE];
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+      const int ks = min(base + 4 * u, nks - 1);
+#pragma unroll
+      for (int r = 0; r < RT; ++r) av[u][r] = *reinterpret_cast<const rs16x8_t*>(arow[r] + ks * 32);
+#pragma unroll
+      for (int j = 0; j < RE; ++j) {
+        bv[u][j] = *reinterpret_cast<const rs16x8_t*>(brow[j] + ks * 32);
+        if (!bok[j]) bv[u][j] = rs16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
+      }
     }
-  } else {
-    for (int idx = tid; idx < RT_TOK * E; idx += 256) {
-      const int tt = idx / E;
-      const int e = idx - tt * E;
-      const int t = min(t0 + tt, T - 1);
-      float acc = 0.f;
-      for (int h = 0; h < H; ++h)
-        acc += ld_any(hidden, (int64_t)t * H + h, dtype) * ld_any(weight, (int64_t)e * H + h, dtype);
-      const float bv = bias ? ld_any(bias, e, dtype) : 0.f;
-      s_log[tt][e] = round_to(acc + bv, dtype);
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+      if (base + 4 * u >= nks) break;
+#pragma unroll
+      for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int j = 0; j < RE; ++j)
+          acc[r][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[u][r]),
+                                                              __builtin_bit_cast(bf16x8_t, bv[u][j]),
+                                                              acc[r][j], 0, 0, 0);
     }
   }
+  if (wave > 0) {
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int j = 0; j < RE; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s_part[wave - 1][r][j][i][lane] = acc[r][j][i];
+  }
   __syncthreads();
-  for (int idx = tid; idx < RT_TOK * E; idx += 256) {
+  if (wave != 0) return;
+  // C layout: lane (lr, lk) holds expert e0 + 16j + lr, tokens 16r + 4lk + i
+#pragma unroll
+  for (int j = 0; j < RE; ++j) {
+    const int e = e0 + j * 16 + lr;
+    if (e >= E) continue;
+    const float bv = bias ? __uint_as_float((uint32_t)bias[e] << 16) : 0.f;
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + r * 16 + 4 * lk + i;
+        float v = acc[r][j][i];
+        v += s_part[0][r][j][i][lane];
+        v += s_part[1][r][j][i][lane];
+        v += s_part[2][r][j][i][lane];
+        if (t < T) logits[(int64_t)t * E + e] = (uint16_t)f32_to_bf16_bits(v + bv);
+      }
+  }
+}
+
+// float32 / float16 modules: float32 VALU dot products, 16 tokens per workgroup.
+__global__ __launch_bounds__(256) void router_valu_kernel(const void* __restrict__ hidden, int dtype,
+                                                         int T, int H, int E, int k,
+                                                         const void* __restrict__ weight,
+                                                         const void* __restrict__ bias,
+                                                         void* __restrict__ logits,
+                                                         void* __restrict__ scores,
+                                                         int64_t* __restrict__ indices) {
+  __shared__ float s_log[16][RT_MAX_E + 1];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int t0 = blockIdx.x * 16;
+  for (int idx = tid; idx < 16 * E; idx += 256) {
+    const int tt = idx / E;
+    const int e = idx - tt * E;
+    const int t = min(t0 + tt, T - 1);
+    float acc = 0.f;
+    for (int h = 0; h < H; ++h)
+      acc += ld_any(hidden, (int64_t)t * H + h, dtype) * ld_any(weight, (int64_t)e * H + h, dtype);
+    const float bv = bias ? ld_any(bias, e, dtype) : 0.f;
+    s_log[tt][e] = round_to(acc + bv, dtype);
+  }
+  __syncthreads();
+  for (int idx = tid; idx < 16 * E; idx += 256) {
     const int tt = idx / E;
     const int e = idx - tt * E;
     if (t0 + tt < T) st_any(logits, (int64_t)(t0 + tt) * E + e, s_log[tt][e], dtype);
   }
-  for (int tt = wave; tt < RT_TOK; tt += 4)
+  for (int tt = wave; tt < 16; tt += 4)
     if (t0 + tt < T) topk_softmax_wave(s_log[tt], E, k, lane, dtype, scores, indices, t0 + tt);
 }
 
@@ -197,14 +266,30 @@ extern "C" int bsa_router_fwd(const void* hidden, int dtype, int64_t T, int64_t 
   BSA_REQUIRE(hidden && weight && logits && scores && indices, "router: null pointer");
   const bool mfma = dtype == DT_BF16 && H % 32 == 0 && reinterpret_cast<uintptr_t>(hidden) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(weight) % 16 == 0;
-  const dim3 grid((unsigned)((T + RT_TOK - 1) / RT_TOK)), block(256);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (mfma)
-    hipLaunchKernelGGL(router_kernel<true>, grid, block, 0, st, hidden, dtype, (int)T, (int)H,
-                       (int)E, (int)k, weight, bias, logits, scores, indices);
-  else
-    hipLaunchKernelGGL(router_kernel<false>, grid, block, 0, st, hidden, dtype, (int)T, (int)H,
-                       (int)E, (int)k, weight, bias, logits, scores, indices);
+  if (mfma) {
+    // logits tiles, then top-k + softmax from the (L2-resident) logits
+    if (T >= 4096) {
+      const int64_t nblk = ((T + 31) / 32) * ((E + 31) / 32);
+      hipLaunchKernelGGL((logits_bf16_kernel<2, 2>), dim3((unsigned)nblk), dim3(256), 0, st,
+                         static_cast<const uint16_t*>(hidden), static_cast<const uint16_t*>(weight),
+                         static_cast<const uint16_t*>(bias), (int)T, (int)H, (int)E,
+                         static_cast<uint16_t*>(logits));
+    } else {
+      const int64_t nblk = ((T + 15) / 16) * ((E + 15) / 16);
+      hipLaunchKernelGGL((logits_bf16_kernel<1, 1>), dim3((unsigned)nblk), dim3(256), 0, st,
+                         static_cast<const uint16_t*>(hidden), static_cast<const uint16_t*>(weight),
+                         static_cast<const uint16_t*>(bias), (int)T, (int)H, (int)E,
+                         static_cast<uint16_t*>(logits));
+    }
+    BSA_LAUNCH_CHECK("router logits launch");
+    hipLaunchKernelGGL(topk_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, logits, dtype,
+                       (int)T, (int)E, (int)k, scores, indices);
+  } else {
+    hipLaunchKernelGGL(router_valu_kernel, dim3((unsigned)((T + 15) / 16)), dim3(256), 0, st,
+                       hidden, dtype, (int)T, (int)H, (int)E, (int)k, weight, bias, logits, scores,
+                       indices);
+  }
   BSA_LAUNCH_CHECK("router launch");
   return BSA_OK;
 }
