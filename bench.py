@@ -9,11 +9,14 @@ resident in HBM.  A step is one dequantisation of the whole layer (both
 projections).  ``value`` is the whole-job algorithmic bandwidth (bytes read
 plus bytes written, 8,062,156,800 B per step) over the timed steps.
 
-``roofline`` covers the dominant launch, the gate_up dequantisation
-(5,374,771,200 algorithmic bytes per launch), timed per launch with HIP events
-on the launch stream; ``traffic`` is that launch's measured HBM bytes from the
-rocprofv3 FETCH_SIZE/WRITE_SIZE runs recorded in profiles/traffic.json, each
-counter scaled by its plain-copy calibration factor (null when absent).  ``cpu_baseline`` times the oracle's torch restatement of the
+``roofline`` covers the one kernel of the step, dequant_vec_kernel<bf16>,
+launched twice per step (gate_up: 5,374,771,200 algorithmic bytes; down:
+2,687,385,600): ``achieved`` is the mean algorithmic bytes per launch over the
+mean launch duration, timed with HIP events on the launch stream (the same
+average rocprofv3 --stats reports for the kernel); ``traffic`` is the mean
+measured HBM bytes per launch from the rocprofv3 FETCH_SIZE/WRITE_SIZE runs
+recorded in profiles/traffic.json, each counter scaled by its plain-copy
+calibration factor (null when absent).  ``cpu_baseline`` times the oracle's torch restatement of the
 reference dequant on the host cores over a bounded sample of the same
 workload.
 """
@@ -55,29 +58,38 @@ def traffic_record(key: str, field: str):
         return None
 
 
-def cpu_baseline_dequant(experts: int = 16) -> dict:
-    """Oracle torch restatement of the reference dequant on the host cores."""
+def cpu_baseline_dequant() -> dict:
+    """Oracle torch restatement of the reference dequant on the host cores.
+
+    The sample is the whole workload: both projections of one gpt-oss-120b
+    layer (all 128 experts), median of 3 runs (about 10 s of CPU work).
+    """
     import oracle
     from blockstreamer_amd import synthetic
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    E, R, G = GATE_UP
-    blocks, scales = synthetic.packed_weights(experts, R, G, seed=2, scale_lo=115, scale_hi=131)
-    oracle.dequant_torch(blocks[:1], scales[:1], torch.bfloat16)  # warm-up
+    packed = [synthetic.packed_weights(*GATE_UP, seed=2, scale_lo=115, scale_hi=131),
+              synthetic.packed_weights(*DOWN, seed=3, scale_lo=115, scale_hi=131)]
+    oracle.dequant_torch(packed[1][0][:1], packed[1][1][:1], torch.bfloat16)  # warm-up
     times = []
     for _ in range(3):
-        t0 = time.perf_counter()
-        oracle.dequant_torch(blocks, scales, torch.bfloat16)
-        times.append(time.perf_counter() - t0)
+        t = 0.0
+        for blocks, scales in packed:
+            t0 = time.perf_counter()
+            out = oracle.dequant_torch(blocks, scales, torch.bfloat16)
+            t += time.perf_counter() - t0
+            del out
+        times.append(t)
     t = statistics.median(times)
+    total = dequant_bytes(*GATE_UP) + dequant_bytes(*DOWN)
     return {
-        "value": round(dequant_bytes(experts, R, G) / t / 1e9, 3),
+        "value": round(total / t / 1e9, 3),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"{experts} of 128 gate_up experts [{experts},{R},{G},16] -> bf16, "
-                  f"median of 3 runs ({t:.2f} s each)",
+        "sample": f"the whole workload (gate_up [128,5760,90,16] + down [128,2880,90,16] -> "
+                  f"bf16), median of 3 runs ({t:.2f} s each)",
     }
 
 
@@ -116,9 +128,11 @@ def bench_dequant(args) -> dict:
     wall = time.perf_counter() - t0
     gu_ms = [e[0].elapsed_time(e[1]) for e in evs]
     dn_ms = [e[1].elapsed_time(e[2]) for e in evs]
-    gu_launch_ms = statistics.mean(gu_ms)
-    achieved = bytes_gu / (gu_launch_ms / 1e3) / 1e9
-    traffic = traffic_record("dequant_mxfp4_gptoss120b_layer", "gate_up_launch_bytes")
+    launch_ms = statistics.mean(gu_ms + dn_ms)
+    launch_bytes = step_bytes / 2
+    achieved = launch_bytes / (launch_ms / 1e3) / 1e9
+    step_traffic = traffic_record("dequant_mxfp4_gptoss120b_layer", "hbm_bytes_per_step")
+    traffic = round(step_traffic / 2) if step_traffic else None
     return {
         "metric": "MoE layer tokens/s + MXFP4 dequant GB/s, gpt-oss-120b shape, 1xMI355X",
         "value": round(step_bytes * args.steps / wall / 1e9, 2),
@@ -140,10 +154,9 @@ def bench_dequant(args) -> dict:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "dequant_vec_kernel<bf16>, gate_up launch [128,5760,90,16] -> [128,2880,5760]",
-            "algorithmic_bytes": bytes_gu,
-            "launch_ms": round(gu_launch_ms, 4),
-            "layer_kernel_GB_per_s": round(step_bytes * args.steps / ((sum(gu_ms) + sum(dn_ms)) / 1e3) / 1e9, 1),
+            "kernel": "dequant_vec_kernel<bf16> (gate_up and down launches)",
+            "algorithmic_bytes": launch_bytes,
+            "launch_ms": round(launch_ms, 4),
         },
     }
 
@@ -253,8 +266,8 @@ def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int
     return res
 
 
-def cpu_baseline_moe(T: int = 64, sample: int = 4) -> dict:
-    """Oracle (fp32 torch restatement of the reference) on a few decode tokens."""
+def cpu_baseline_moe(T: int = 64, sample: int = 64) -> dict:
+    """Oracle (fp32 torch restatement of the reference) on the 64-token decode batch."""
     import oracle
     from blockstreamer_amd import synthetic
 
@@ -267,15 +280,16 @@ def cpu_baseline_moe(T: int = 64, sample: int = 4) -> dict:
     args = tuple(t[n] for n in ("gate_up_proj_blocks", "gate_up_proj_scales", "gate_up_proj_bias",
                                 "down_proj_blocks", "down_proj_scales", "down_proj_bias"))
     times = []
-    for _ in range(2):
+    for _ in range(3):
         t0 = time.perf_counter()
         _, scores, idx = oracle.router_ref(h, t["router_weight"], t["router_bias"], k)
         oracle.experts_ref(h, idx, scores, *args)
         times.append(time.perf_counter() - t0)
-    tm = min(times)
+    tm = statistics.median(times)
     return {"value": round(sample / tm, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"{sample} tokens of the 64-token gpt-oss-120b decode batch, router + "
-                      f"experts in float32 (per-expert dequant + GEMMs), best of 2 ({tm:.2f} s)"}
+                      f"experts in float32 (per-expert dequant + GEMMs), median of 3 "
+                      f"({tm:.2f} s each)"}
 
 
 def bench_copy(steps: int, warmup: int) -> dict:

@@ -13,18 +13,20 @@
 // tensor holds output column n with K contiguous, which is exactly the
 // per-lane layout of an MFMA B operand, so no transpose is ever needed.
 //
-// Two kernels:
+// Three kernels:
 //  * moe_stream_kernel (decode, few rows per expert): one workgroup per
 //    (expert, 32-column slice).  The slice's packed bytes are one contiguous
 //    32*K/2-byte span; it is copied to LDS with 16-byte loads, then four
 //    waves split K and run v_mfma_f32_16x16x32_bf16 on 16-row blocks, with A
 //    rows prefetched 8 steps ahead.  Partial sums are reduced through LDS.
 //    Bound: HBM (each hit expert's weights are read exactly once).
-//  * moe_tiled_kernel (prefill): 128x128 output tiles of one expert, BK=64,
-//    LDS double buffering, 2x2 waves of 64x64 using
-//    v_mfma_f32_32x32x16_bf16.  The B tile is decoded into LDS as bf16.
-//    Bound: MFMA.
-//
+//  * moe_tiled2_kernel (prefill, 16-byte aligned operands): 128x256 output
+//    tiles of one expert, BK=64, three LDS stages filled by global_load_lds
+//    DMA, packed B decoded from LDS into MFMA operands by the one wave that
+//    uses them, v_mfma_f32_32x32x16_bf16.  Bound: MFMA.
+//  * moe_tiled_kernel (prefill for operands aligned to less than 16 bytes,
+//    and the backward products over dense bf16 weights): 128x128 tiles,
+//    BK=64, register-staged LDS double buffering, 2x2 waves of 64x64.
 // Weights are decoded with the gfx950 converter (v_cvt_scalef32_pk_bf16_fp4),
 // which follows OCP MX: a block whose E8M0 scale byte is 255 (the NaN code)
 // decodes to NaN, so the outputs it touches are NaN.  The reference's
