@@ -165,6 +165,7 @@ def bench_dequant(args) -> dict:
 
 GPTOSS_120B = dict(E=128, k=4, H=2880, I=2880)
 BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
 MXFP4_PEAK_TFLOPS = 10100.0
 
 
@@ -183,7 +184,8 @@ def _median_ms(pairs):
     return statistics.median([a.elapsed_time(b) for a, b in pairs])
 
 
-def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int) -> dict:
+def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int,
+              path: str = "auto") -> dict:
     from blockstreamer_amd import kernels, synthetic
 
     dev = torch.device("cuda", 0)
@@ -201,7 +203,7 @@ def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int
 
     def step():
         idx, w = route()
-        return kernels.moe_experts_forward(x, idx, w, *args)
+        return kernels.moe_experts_forward(x, idx, w, *args, path=path)
 
     for _ in range(warmup):
         step()
@@ -216,7 +218,7 @@ def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int
     # events do not sit inside the timed layer steps above)
     idx, w = route()
     hit = int(torch.unique(idx).numel())
-    st = kernels.MoEStages(x, idx, w, *args)
+    st = kernels.MoEStages(x, idx, w, *args, path=path)
     names = ("route", "dispatch", "gate_up", "down", "combine")
     ev = {n: [] for n in names}
     for _ in range(max(steps, 5)):
@@ -248,7 +250,18 @@ def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int
     }
     hbm = wbytes / (gemm_ms / 1e3) / 1e9
     tfl = flops / (gemm_ms / 1e3) / 1e12
-    if T * k <= 16 * E:
+    res["path"] = path
+    if path == "mx":
+        # MXFP8 x MXFP4 on the block-scaled MFMA runs at the FP8 rate
+        res["roofline"] = {"bound": "mfma", "achieved": round(tfl, 1), "peak": FP8_PEAK_TFLOPS,
+                           "unit": "TFLOP/s", "frac": round(tfl / FP8_PEAK_TFLOPS, 4),
+                           "frac_of_mxfp4_peak": round(tfl / MXFP4_PEAK_TFLOPS, 4),
+                           "kernel": "mx_quant + moe_mx_kernel gate_up + down",
+                           "algorithmic_flops": flops}
+        ref = kernels.moe_experts_forward(x, idx, w, *args, path="auto").float()
+        got = kernels.moe_experts_forward(x, idx, w, *args, path="mx").float()
+        res["rel_l2_vs_bf16_path"] = round(((got - ref).norm() / ref.norm()).item(), 5)
+    elif T * k <= 16 * E:
         res["roofline"] = {"bound": "hbm", "achieved": round(hbm, 1), "peak": HBM_PEAK_GBS,
                            "unit": "GB/s", "frac": round(hbm / HBM_PEAK_GBS, 4),
                            "kernel": "moe_stream_kernel gate_up + down",
@@ -313,9 +326,9 @@ def focused(args) -> int:
     if args.workload == "copy":
         res = bench_copy(args.steps, args.warmup)
     elif args.workload == "moe_decode":
-        res = bench_moe(64, args.steps, args.warmup, 0.5, seed=4)
+        res = bench_moe(64, args.steps, args.warmup, 0.5, seed=4, path=args.path)
     else:
-        res = bench_moe(8192, args.steps, args.warmup, 0.0, seed=5)
+        res = bench_moe(8192, args.steps, args.warmup, 0.0, seed=5, path=args.path)
     print(json.dumps({"workload": args.workload, "steps": args.steps, "warmup": args.warmup, **res}),
           flush=True)
     return 0
@@ -331,6 +344,8 @@ def main() -> int:
                     help="dequant: the headline line (plus MoE layer results); moe_decode / "
                          "moe_prefill: one MoE workload alone; copy: a plain 2 GiB device copy "
                          "that calibrates the HBM byte counters")
+    ap.add_argument("--path", default="auto", choices=["auto", "stream", "tiled", "mx"],
+                    help="expert GEMM kernel for the moe_decode / moe_prefill workloads")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE layer measurements")
     args = ap.parse_args()

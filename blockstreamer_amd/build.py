@@ -54,7 +54,10 @@ def build(verbose: bool = False) -> Path:
     with ThreadPoolExecutor(max_workers=workers) as pool:
         objs = list(pool.map(_compile, sources))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    # -z defs: an undefined symbol (e.g. a kernel handle the compiler did not
+    # emit) fails the build instead of the first load on the GPU
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", *map(str, objs),
+           "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")

@@ -52,6 +52,8 @@ int launch_bwd_prep(const void* dout, int dout_dtype, const float* y, const void
 int launch_dequant_bf16_routed(const uint8_t* blocks, const uint8_t* scales, uint16_t* out,
                                int64_t E, int64_t R, int64_t G, const int* expert_rows,
                                hipStream_t stream);
+int launch_quant_mxfp8(const void* x, int in_dtype, int64_t R, int64_t K, int64_t ldx, uint8_t* q,
+                       int64_t ldq, uint8_t* s, int64_t lds, hipStream_t st);
 
 enum Epi : int {
   EPI_SWIGLU = 0,    // out bf16 [P][N/2] = swiglu(acc + bias), optional f32 pre-activation save
@@ -82,6 +84,9 @@ struct GemmArgs {
   const int2* tiles;     // tiled kernel: (expert, first sorted row) per row tile
   const int* num_tiles;
   int n_tiles_n;         // column tiles per row tile
+  const uint8_t* Aq;     // MX path: E4M3 activations, row stride ldq bytes
+  const uint8_t* As;     // MX path: E8M0 activation scales, row stride ldas bytes (% 4 == 0)
+  int64_t ldq, ldas;
 };
 
 typedef __attribute__((ext_vector_type(8))) short s16x8_t;
@@ -395,6 +400,22 @@ __global__ __launch_bounds__(256) void moe_stream_kernel(GemmArgs a) {
   }
 }
 
+// Logical tile index of this workgroup for the tiled kernels.  The live
+// tiles (num_tiles row tiles x n_tiles_n column tiles; the row-tile count is
+// only known on the device, the grid is sized for the maximum) are split
+// into 8 equal contiguous chunks, one per XCD (workgroups are dispatched
+// round-robin over the 8 XCDs): every XCD gets the same share of the work,
+// and the column tiles of one row tile (and the row tiles of one expert)
+// stay on one XCD's L2.  -1: no tile for this workgroup.  Needs a grid that
+// is a multiple of 8 and at least the live tile count.
+__device__ __forceinline__ int xcd_tile_index(int live) {
+  const int chunk = (live + 7) >> 3;
+  const int slot = (int)(blockIdx.x >> 3);
+  if (slot >= chunk) return -1;
+  const int L = (int)(blockIdx.x & 7) * chunk + slot;
+  return L < live ? L : -1;
+}
+
 // ---------------------------------------------------------------------------
 // LDS-tiled kernel (prefill).
 // ---------------------------------------------------------------------------
@@ -408,14 +429,10 @@ __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
   __shared__ __align__(16) uint16_t sA[2][TL_BM * TL_LDK];
   __shared__ __align__(16) uint16_t sB[2][TL_BN * TL_LDK];
 
-  // XCD-aware order: workgroups dispatched round-robin over the 8 XCDs get
-  // consecutive logical indices per XCD, so the column tiles of one row tile
-  // (and the row tiles of one expert) share an L2.
-  const int nblk = gridDim.x;  // multiple of 8
-  const int L = (blockIdx.x & 7) * (nblk >> 3) + (blockIdx.x >> 3);
+  const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
+  if (L < 0) return;
   const int tile = L / a.n_tiles_n;
   const int nt = L - tile * a.n_tiles_n;
-  if (tile >= *a.num_tiles) return;
   const int2 te = a.tiles[tile];
   const int e = te.x;
   const int m0 = te.y;
@@ -652,11 +669,10 @@ __device__ __forceinline__ void t2_ktile(f32x16_t (&acc)[4][2], const uint8_t* s
 template <int EPI, int T2_NS, int SCHED>
 __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
   __shared__ __align__(1024) uint8_t smem[T2_NS * T2_STAGE];
-  const int nblk = gridDim.x;  // multiple of 8
-  const int L = (blockIdx.x & 7) * (nblk >> 3) + (blockIdx.x >> 3);
+  const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
+  if (L < 0) return;
   const int tile = L / a.n_tiles_n;
   const int nt = L - tile * a.n_tiles_n;
-  if (tile >= *a.num_tiles) return;
   const int2 te = a.tiles[tile];
   const int e = te.x;
   const int m0 = te.y;
@@ -776,22 +792,298 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
   }
 
   // epilogue: lane holds column l32 of each 32x32 block, rows 8*(v/4) + 4*lh + v%4
+  if constexpr (EPI == EPI_SWIGLU) {
+    // lanes 2j (gate column) and 2j+1 (up column) hold the same 16 rows; the
+    // even lane finishes rows v < 8 and the odd lane rows v >= 8, trading
+    // the missing halves with one shuffle per row pair
+    const bool odd = l32 & 1;
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int r = mb * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-      const int64_t pos = m0 + r;
+    for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
-        const int n = n0 + bq[nb];
-        const float val = acc[mb][nb][v] + bias[nb];
-        if constexpr (EPI == EPI_SWIGLU) {
-          const float up = __shfl_xor(val, 1);  // odd weight row = up of the pair
-          if (r < rows && (l32 & 1) == 0 && n + 1 < a.N)
-            epilogue_swiglu<EPI>(a, pos, n, val, up, 0.f, 0.f);
-        } else {
-          if (r < rows && n < a.N) epilogue_one<EPI>(a, pos, n, val, 0.f);
+        const int ng = (n0 + bq[nb]) & ~1;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const float lo = acc[mb][nb][v] + bias[nb];
+          const float hi = acc[mb][nb][v + 8] + bias[nb];
+          const float recv = __shfl_xor(odd ? lo : hi, 1);
+          const float g = odd ? recv : lo;
+          const float u = odd ? hi : recv;
+          const int vv = odd ? v + 8 : v;
+          const int r = mb * 32 + 8 * (vv >> 2) + 4 * lh + (vv & 3);
+          if (r < rows && ng + 1 < a.N) epilogue_swiglu<EPI>(a, m0 + r, ng, g, u, 0.f, 0.f);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = mb * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          const int n = n0 + bq[nb];
+          if (r < rows && n < a.N) epilogue_one<EPI>(a, m0 + r, n, acc[mb][nb][v] + bias[nb], 0.f);
+        }
+      }
+    }
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// Native block-scaled MX kernel (prefill): MXFP8 activations x MXFP4 weights
+// on v_mfma_scale_f32_32x32x64_f8f6f4, no weight decode at all.
+//
+// Operand layout of that instruction (measured on gfx950): for 32 x 32 x 64,
+// lane l = 32*g + i supplies row/column i; its E2M1 operand is the 32
+// consecutive K values 32g .. 32g+31 (nibble j = K offset j, low nibble
+// first) -- exactly one packed 16-byte group of the checkpoint layout -- and
+// its scale byte is that block's E8M0 scale; its E4M3 operand is K values
+// 16g .. 16g+15 (bytes 0-15) and 32+16g .. 32+16g+15 (bytes 16-31), while
+// its scale byte is still the scale of K block g.
+//
+// Tile 128 rows x 256 weight rows, BK = 64 (two MX blocks), NS LDS stages
+// filled only by global_load_lds DMA.  The L1 -> L2 path is limited by the
+// number of requests, not bytes, so every DMA covers whole contiguous runs:
+//  * A stage [128][64] E4M3, 4 lanes per row (64 contiguous bytes); row r's
+//    16-byte chunk c sits at chunk c ^ ((r >> 2) & 3), so the fragment reads
+//    are bank-conflict free;
+//  * B stage [256 rows][2 groups][16 bytes], 2 lanes per row (32 contiguous
+//    bytes);
+//  * scales are loaded once per tile, not per k-step: the B scales of the
+//    tile's 256 weight rows are one contiguous 256*G-byte span of the
+//    checkpoint tensor; the A scales come from rows padded to ldas bytes
+//    (a multiple of 16) by the quantisation kernel.
+// The four waves split N; each computes 128 x 64 (4 x 2 blocks of 32 x 32).
+// Bound: MFMA (FP8 rate, 2x the bf16 rate).
+// ---------------------------------------------------------------------------
+typedef __attribute__((ext_vector_type(8))) int i32x8_t;
+
+constexpr int MX_BM = 128;
+constexpr int MX_BN = 256;
+constexpr int MX_BK = 64;
+constexpr int MX_A_BYTES = MX_BM * MX_BK;   // 8 KiB
+constexpr int MX_B_BYTES = MX_BN * 32;      // 8 KiB
+constexpr int MX_STAGE = MX_A_BYTES + MX_B_BYTES;
+constexpr int MX_DMA_PER_TILE = 2 + 2;      // per wave: A, B
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited on)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// Wait until at most `ahead` tiles of PER loads each are in flight.
+template <int PER, int MAXAHEAD>
+__device__ __forceinline__ void wait_tiles_ahead(int ahead) {
+  if constexpr (MAXAHEAD >= 4) { if (ahead >= 4) { wait_vmcnt<4 * PER>(); return; } }
+  if constexpr (MAXAHEAD >= 3) { if (ahead == 3) { wait_vmcnt<3 * PER>(); return; } }
+  if constexpr (MAXAHEAD >= 2) { if (ahead == 2) { wait_vmcnt<2 * PER>(); return; } }
+  if constexpr (MAXAHEAD >= 1) { if (ahead == 1) { wait_vmcnt<PER>(); return; } }
+  wait_vmcnt<0>();
+}
+
+// Dynamic LDS bytes of moe_mx_kernel: NS stages, A scales, B scales.
+inline size_t mx_smem_bytes(int ns, int K, int64_t ldas) {
+  return (size_t)ns * MX_STAGE + (size_t)MX_BM * ldas + (size_t)MX_BN * (K / 32);
+}
+
+// Activation row read for sorted row r of a tile that starts at sorted row
+// m0 and holds `rows` rows (rows past the tile read the tile's first row).
+// A device function, not a lambda: HIP-Clang does not emit the host-side
+// handle of this kernel template when its body calls a capturing lambda.
+__device__ __forceinline__ int64_t tile_src_row(const GemmArgs& a, int m0, int rows, int r) {
+  const int64_t pos = m0 + (r < rows ? r : 0);
+  return a.row_pair ? (int64_t)(a.row_pair[pos] / a.topk) : pos;
+}
+
+template <int EPI, int MX_NS, bool SB16>
+__global__ __launch_bounds__(256, 2) void moe_mx_kernel(GemmArgs a) {
+  static_assert(MX_NS >= 2 && MX_NS <= 6, "pipeline depth");
+  extern __shared__ __align__(1024) uint8_t smem[];
+  const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
+  if (L < 0) return;
+  const int tile = L / a.n_tiles_n;
+  const int nt = L - tile * a.n_tiles_n;
+  const int2 te = a.tiles[tile];
+  const int e = te.x;
+  const int m0 = te.y;
+  const int rows = min(MX_BM, a.offsets[e] + a.counts[e] - m0);
+  const int n0 = nt * MX_BN;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;  // column quarter: weight rows 64*wave .. +64
+  const int G = a.K / 32;
+  const int KT = a.K / MX_BK;
+  const int l32 = lane & 31;
+  const int lh = lane >> 5;
+  const int ldas = (int)a.ldas;
+  uint8_t* sas = smem + MX_NS * MX_STAGE;  // [128][ldas] A scales
+  uint8_t* sbs = sas + MX_BM * ldas;       // [256][G] B scales
+
+
+  // --- scales, once per tile ----------------------------------------------
+  {
+    // B: bytes [(e*N + n0)*G, +256*G) of the scale tensor; chunks past this
+    // expert's last row read the span's first chunk instead (never used)
+    const uint8_t* span = a.Bs + ((int64_t)e * a.N + n0) * G;
+    const int valid = (min(MX_BN, a.N - n0)) * G;  // bytes belonging to this tile
+    if constexpr (SB16) {
+      const int nch = MX_BN * G / 16;
+      for (int j = wave; j * 64 < nch; j += 4) {
+        const int c = j * 64 + lane;
+        if (c < nch)
+          __builtin_amdgcn_global_load_lds(span + (c * 16 + 16 <= valid ? c * 16 : 0),
+                                           (lds_void*)(sbs + j * 1024), 16, 0, 0);
+      }
+    } else {
+      const int nch = MX_BN * G / 4;
+      for (int j = wave; j * 64 < nch; j += 4) {
+        const int c = j * 64 + lane;
+        if (c < nch)
+          __builtin_amdgcn_global_load_lds(span + (c * 4 + 4 <= valid ? c * 4 : 0),
+                                           (lds_void*)(sbs + j * 256), 4, 0, 0);
+      }
+    }
+    // A: 128 gathered rows of ldas bytes (16-byte chunks)
+    const int cpr = ldas / 16;
+    const int nch = MX_BM * cpr;
+    for (int j = wave; j * 64 < nch; j += 4) {
+      const int c = j * 64 + lane;
+      if (c < nch) {
+        const int r = c / cpr;
+        __builtin_amdgcn_global_load_lds(a.As + tile_src_row(a, m0, rows, r) * a.ldas + (c - r * cpr) * 16,
+                                         (lds_void*)(sas + j * 1024), 16, 0, 0);
+      }
+    }
+  }
+
+  // --- per-lane stage DMA sources (every lane always issues all of them, so
+  //     the per-wave vmcnt arithmetic is exact; rows or columns past the tile
+  //     read a clamped valid address and are never stored) -----------------
+  // A: instruction i = 2*wave + j covers rows 16i .. 16i+15, 4 lanes per row
+  const uint8_t* asrc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = 16 * (2 * wave + j) + (lane >> 2);
+    const int ch = (lane & 3) ^ ((r >> 2) & 3);
+    asrc[j] = a.Aq + tile_src_row(a, m0, rows, r) * a.ldq + ch * 16;
+  }
+  // B: instruction i = 2*wave + h2 covers rows 32i .. 32i+31, 2 lanes per row
+  const uint8_t* bsrc[2];
+#pragma unroll
+  for (int h2 = 0; h2 < 2; ++h2) {
+    const int q = 32 * (2 * wave + h2) + (lane >> 1);
+    const bool ok = n0 + q < a.N;
+    bsrc[h2] = a.Bq + ((int64_t)e * a.N + (ok ? n0 + q : n0)) * G * 16 + (lane & 1) * 16;
+  }
+
+  auto issue = [&](int kt) {
+    uint8_t* st = smem + (kt % MX_NS) * MX_STAGE;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_global_load_lds(asrc[j] + kt * MX_BK,
+                                       (lds_void*)(st + (2 * wave + j) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+      __builtin_amdgcn_global_load_lds(bsrc[h2] + kt * 32,
+                                       (lds_void*)(st + MX_A_BYTES + (2 * wave + h2) * 1024), 16, 0, 0);
+  };
+
+  // this lane's two B rows and their bias
+  int bq[2];
+  float bias[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    bq[nb] = wave * 64 + nb * 32 + l32;
+    const bool ok = n0 + bq[nb] < a.N;
+    bias[nb] = ok ? bias_at(a.bias, a.bias_dtype, (int64_t)e * a.N + n0 + bq[nb]) : 0.f;
+  }
+  // LDS byte offsets of this lane's A chunks lh and 2 + lh in row mb*32 + l32
+  // (the row's swizzle (r >> 2) & 3 does not depend on mb)
+  const int rsw = (l32 >> 2) & 3;
+  const uint32_t aoff0 = (uint32_t)(l32 * 64 + ((lh ^ rsw) * 16));
+  const uint32_t aoff1 = (uint32_t)(l32 * 64 + (((2 + lh) ^ rsw) * 16));
+  const uint8_t* sa_row = sas + l32 * ldas + lh;        // + mb*32*ldas + 2kt
+  const uint8_t* sb_row0 = sbs + bq[0] * G + lh;        // + 2kt
+  const uint8_t* sb_row1 = sbs + bq[1] * G + lh;
+
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  for (int i = 0; i < MX_NS - 1; ++i)
+    if (i < KT) issue(i);
+  for (int kt = 0; kt < KT; ++kt) {
+    // tile kt (and, on the first pass, the scales issued before it) has
+    // landed once at most the tiles issued after it are in flight
+    wait_tiles_ahead<MX_DMA_PER_TILE, MX_NS - 2>(min(MX_NS - 2, KT - 1 - kt));
+    asm volatile("s_barrier" ::: "memory");
+    if (kt + MX_NS - 1 < KT) issue(kt + MX_NS - 1);
+    const uint8_t* st = smem + (kt % MX_NS) * MX_STAGE;
+    const int sb[2] = {(int)sb_row0[2 * kt], (int)sb_row1[2 * kt]};
+    i32x8_t bop[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(st + MX_A_BYTES + bq[nb] * 32 + lh * 16);
+      bop[nb] = i32x8_t{(int)w[0], (int)w[1], (int)w[2], (int)w[3], 0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const uint8_t* ar = st + mb * 32 * 64;
+      const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(ar + aoff0);
+      const u32x4_t w1 = *reinterpret_cast<const u32x4_t*>(ar + aoff1);
+      const i32x8_t aop = {(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3],
+                           (int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
+      const int sa = (int)sa_row[mb * 32 * ldas + 2 * kt];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+        acc[mb][nb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, bop[nb], acc[mb][nb], 0, 4, 0,
+                                                                      sa, 0, sb[nb]);
+    }
+  }
+
+  // epilogue: lane holds column l32 of each 32x32 block, rows 8*(v/4) + 4*lh + v%4
+  if constexpr (EPI == EPI_SWIGLU) {
+    // lanes 2j (gate column) and 2j+1 (up column) hold the same 16 rows; the
+    // even lane finishes rows v < 8 and the odd lane rows v >= 8, trading
+    // the missing halves with one shuffle per row pair
+    const bool odd = l32 & 1;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const int ng = (n0 + bq[nb]) & ~1;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const float lo = acc[mb][nb][v] + bias[nb];
+          const float hi = acc[mb][nb][v + 8] + bias[nb];
+          const float recv = __shfl_xor(odd ? lo : hi, 1);
+          const float g = odd ? recv : lo;
+          const float u = odd ? hi : recv;
+          const int vv = odd ? v + 8 : v;
+          const int r = mb * 32 + 8 * (vv >> 2) + 4 * lh + (vv & 3);
+          if (r < rows && ng + 1 < a.N) epilogue_swiglu<EPI>(a, m0 + r, ng, g, u, 0.f, 0.f);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = mb * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          const int n = n0 + bq[nb];
+          if (r < rows && n < a.N) epilogue_one<EPI>(a, m0 + r, n, acc[mb][nb][v] + bias[nb], 0.f);
         }
       }
     }
@@ -801,7 +1093,7 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-enum Path : int { PATH_AUTO = 0, PATH_STREAM = 1, PATH_TILED = 2 };
+enum Path : int { PATH_AUTO = 0, PATH_STREAM = 1, PATH_TILED = 2, PATH_MX = 3 };
 
 static inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
@@ -814,6 +1106,11 @@ struct Workspace {
   int* num_tiles;
   uint16_t* act;  // [P][I] bf16 gated activations
   float* y;       // [P][H] f32 down-projection output (before the routing weight)
+  uint8_t* hq;    // MX path: [T][H] E4M3 hidden, [T][ldhs] scales
+  uint8_t* hs;
+  uint8_t* aq;    // MX path: [P][I] E4M3 activations, [P][ldas] scales
+  uint8_t* as;
+  int64_t ldhs, ldas;
   int64_t bytes;
 };
 
@@ -836,6 +1133,12 @@ static Workspace carve(void* base, int64_t T, int64_t H, int64_t I, int64_t E, i
   w.num_tiles = reinterpret_cast<int*>(take(4));
   w.act = reinterpret_cast<uint16_t*>(take(P * I * 2));
   w.y = reinterpret_cast<float*>(take(P * H * 4));
+  w.ldhs = align_up(H / 32, 16);
+  w.ldas = align_up(I / 32, 16);
+  w.hq = reinterpret_cast<uint8_t*>(take(T * H));
+  w.hs = reinterpret_cast<uint8_t*>(take(T * w.ldhs));
+  w.aq = reinterpret_cast<uint8_t*>(take(P * I));
+  w.as = reinterpret_cast<uint8_t*>(take(P * w.ldas));
   w.bytes = off;
   return w;
 }
@@ -852,6 +1155,60 @@ static int launch_gemm_dense(const GemmArgs& a, int64_t P, hipStream_t st) {
   }
   hipLaunchKernelGGL((moe_tiled_kernel<EPI, true, true>), dim3((unsigned)grid), dim3(256), 0, st, a);
   BSA_LAUNCH_CHECK("dense grouped GEMM launch");
+  return BSA_OK;
+}
+
+// Block-scaled MX grouped GEMM (K % 64 == 0; 16-byte aligned blocks, 4-byte
+// aligned weight scales; a.Aq / a.As filled by launch_quant_mxfp8 with a
+// 16-byte aligned scale buffer whose row stride is a multiple of 16).
+constexpr int MX_LAUNCH_NS = 2;  // pipeline stages of the launched MX kernel
+
+template <int EPI>
+static int launch_gemm_mx(const GemmArgs& a, int64_t P, hipStream_t st) {
+  constexpr int NS = MX_LAUNCH_NS;
+  if (a.K % MX_BK != 0 || reinterpret_cast<uintptr_t>(a.Bq) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(a.Bs) % 4 != 0 || a.ldas % 16 != 0 || a.ldas < a.K / 32 ||
+      reinterpret_cast<uintptr_t>(a.As) % 16 != 0) {
+    set_error("MX GEMM: needs K %% 64 == 0 (K=%d), 16-byte aligned blocks and 4-byte aligned scales",
+              a.K);
+    return BSA_EINVAL;
+  }
+  const size_t smem = mx_smem_bytes(NS, a.K, a.ldas);
+  if (smem > 160 * 1024) {
+    set_error("MX GEMM: K=%d needs %zu bytes of LDS", a.K, smem);
+    return BSA_EINVAL;
+  }
+  const int64_t max_tiles = (P + MX_BM - 1) / MX_BM + a.E;
+  GemmArgs b = a;
+  b.n_tiles_n = (a.N + MX_BN - 1) / MX_BN;
+  const int64_t grid = align_up(max_tiles * b.n_tiles_n, 8);
+  if (grid > INT32_MAX) {
+    set_error("MX GEMM: grid too large");
+    return BSA_EINVAL;
+  }
+  // more than 64 KiB of dynamic LDS must be allowed per function and device
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    set_error("MX GEMM: no current HIP device");
+    return BSA_EHIP;
+  }
+  static bool allowed[64][2];
+  const bool sb16 = reinterpret_cast<uintptr_t>(a.Bs) % 16 == 0;
+  const void* fn = sb16 ? reinterpret_cast<const void*>(moe_mx_kernel<EPI, MX_LAUNCH_NS, true>)
+                        : reinterpret_cast<const void*>(moe_mx_kernel<EPI, MX_LAUNCH_NS, false>);
+  if (!allowed[dev][sb16]) {
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
+      set_error("MX GEMM: cannot allow %zu bytes of dynamic LDS", smem);
+      return BSA_EHIP;
+    }
+    allowed[dev][sb16] = true;
+  }
+  if (sb16)
+    hipLaunchKernelGGL((moe_mx_kernel<EPI, MX_LAUNCH_NS, true>), dim3((unsigned)grid), dim3(256), smem, st, b);
+  else
+    hipLaunchKernelGGL((moe_mx_kernel<EPI, MX_LAUNCH_NS, false>), dim3((unsigned)grid), dim3(256), smem, st,
+                       b);
+  BSA_LAUNCH_CHECK("MX grouped GEMM launch");
   return BSA_OK;
 }
 
@@ -900,6 +1257,7 @@ static int launch_gemm(const GemmArgs& a, int path, int64_t P, hipStream_t st) {
 }
 
 static int pick_path(int path, int64_t P, int64_t E, int64_t K) {
+  if (path == PATH_MX) return PATH_MX;     // explicit only; checks its own shape
   if (K % TL_BK != 0) return PATH_STREAM;  // the tiled kernel steps K by 64
   if (path != PATH_AUTO) return path;
   // rows per expert on average: weight streaming while they fit one or two
@@ -979,7 +1337,18 @@ static int stage_gate_up(const MoeShape& m, const void* hidden, const void* bloc
   g.num_tiles = w.num_tiles;
   g.n_tiles_n = (int)((2 * m.I + TL_BN - 1) / TL_BN);
   const int64_t P = m.T * m.k;
-  return launch_gemm<EPI_SWIGLU>(g, pick_path(path, P, m.E, m.H), P, st);
+  const int chosen = pick_path(path, P, m.E, m.H);
+  if (chosen == PATH_MX) {
+    // each token's hidden row is quantised once, then gathered per pair
+    int rc = launch_quant_mxfp8(hidden, DT_BF16, m.T, m.H, m.H, w.hq, m.H, w.hs, w.ldhs, st);
+    if (rc) return rc;
+    g.Aq = w.hq;
+    g.ldq = m.H;
+    g.As = w.hs;
+    g.ldas = w.ldhs;
+    return launch_gemm_mx<EPI_SWIGLU>(g, P, st);
+  }
+  return launch_gemm<EPI_SWIGLU>(g, chosen, P, st);
 }
 
 static int stage_down(const MoeShape& m, const void* blocks, const void* scales, const void* bias,
@@ -1005,7 +1374,21 @@ static int stage_down(const MoeShape& m, const void* blocks, const void* scales,
   g.num_tiles = w.num_tiles;
   g.n_tiles_n = (int)((m.H + TL_BN - 1) / TL_BN);
   const int64_t P = m.T * m.k;
-  return launch_gemm<EPI_BIAS_F32>(g, pick_path(path, P, m.E, m.I), P, st);
+  const int chosen = pick_path(path, P, m.E, m.I);
+  if (chosen == PATH_MX) {
+    if (m.I % MX_BK != 0) {
+      set_error("down (MX path): intermediate %lld is not a multiple of 64", (long long)m.I);
+      return BSA_EINVAL;
+    }
+    int rc = launch_quant_mxfp8(w.act, DT_BF16, P, m.I, m.I, w.aq, m.I, w.as, w.ldas, st);
+    if (rc) return rc;
+    g.Aq = w.aq;
+    g.ldq = m.I;
+    g.As = w.as;
+    g.ldas = w.ldas;
+    return launch_gemm_mx<EPI_BIAS_F32>(g, P, st);
+  }
+  return launch_gemm<EPI_BIAS_F32>(g, chosen, P, st);
 }
 
 static bool dtype_ok(int d) { return d >= 0 && d <= 2; }
@@ -1034,7 +1417,7 @@ extern "C" int bsa_moe_gate_up(const void* hidden, int64_t T, int64_t H, int64_t
   int rc = check_shape(m, "gate_up");
   if (rc || T == 0) return rc;
   BSA_REQUIRE(hidden && blocks && scales, "gate_up: null pointer");
-  BSA_REQUIRE(dtype_ok(bias_dtype) && path >= 0 && path <= 2, "gate_up: bad dtype or path");
+  BSA_REQUIRE(dtype_ok(bias_dtype) && path >= 0 && path <= 3, "gate_up: bad dtype or path");
   BSA_REQUIRE(reinterpret_cast<uintptr_t>(hidden) % 16 == 0 && reinterpret_cast<uintptr_t>(blocks) % 8 == 0,
               "gate_up: hidden must be 16-byte and blocks 8-byte aligned");
   Workspace w;
@@ -1052,7 +1435,7 @@ extern "C" int bsa_moe_down(int64_t T, int64_t H, int64_t I, int64_t E, int64_t 
   int rc = check_shape(m, "down");
   if (rc || T == 0) return rc;
   BSA_REQUIRE(blocks && scales, "down: null pointer");
-  BSA_REQUIRE(dtype_ok(bias_dtype) && path >= 0 && path <= 2, "down: bad dtype or path");
+  BSA_REQUIRE(dtype_ok(bias_dtype) && path >= 0 && path <= 3, "down: bad dtype or path");
   BSA_REQUIRE(reinterpret_cast<uintptr_t>(blocks) % 8 == 0, "down: blocks must be 8-byte aligned");
   Workspace w;
   if ((rc = check_ws(m, workspace, workspace_bytes, &w, "down"))) return rc;
@@ -1088,7 +1471,7 @@ extern "C" int bsa_moe_experts_fwd(
   if (rc || T == 0) return rc;
   BSA_REQUIRE(dtype_ok(weight_dtype) && dtype_ok(bias_dtype) && dtype_ok(out_dtype),
               "experts fwd: bad dtype code");
-  BSA_REQUIRE(path >= 0 && path <= 2, "experts fwd: path must be 0, 1 or 2");
+  BSA_REQUIRE(path >= 0 && path <= 3, "experts fwd: path must be 0, 1, 2 or 3");
   BSA_REQUIRE(hidden && router_indices && routing_weights && gate_up_blocks && gate_up_scales &&
                   down_blocks && down_scales && out,
               "experts fwd: null pointer");

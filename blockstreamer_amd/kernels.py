@@ -48,7 +48,32 @@ def dequantize_mxfp4(blocks: Tensor, scales: Tensor, dtype: torch.dtype = torch.
     return out
 
 
-PATHS = {"auto": 0, "stream": 1, "tiled": 2}
+# Expert GEMM kernels: "stream" (weight streaming, decode), "tiled" (bf16
+# MFMA over LDS tiles, prefill), "auto" (by rows per expert) -- all bf16
+# activations x exactly dequantised MXFP4 weights; "mx" (MXFP8 activations x
+# MXFP4 weights on the block-scaled f8f6f4 MFMA; activation quantisation
+# error of a few 1e-2 relative, opt-in only).
+PATHS = {"auto": 0, "stream": 1, "tiled": 2, "mx": 3}
+
+
+def quantize_mxfp8(x: Tensor) -> tuple[Tensor, Tensor]:
+    """OCP MXFP8 (E4M3 + one E8M0 scale per 32) of a ``[R, K]`` tensor.
+
+    Returns ``(codes uint8 [R, K], scales uint8 [R, K/32])``.  The A operand
+    format of the ``"mx"`` GEMM path; no reference counterpart.
+    """
+    if x.dim() != 2 or x.shape[1] % 32 != 0:
+        raise ValueError(f"x must be [rows, K] with K % 32 == 0, got {tuple(x.shape)}")
+    dev = _lib.require_gpu(x)
+    code = _lib.dtype_code(x.dtype)
+    x = x.contiguous()
+    R, K = x.shape
+    q = torch.empty((R, K), dtype=torch.uint8, device=dev)
+    s = torch.empty((R, K // 32), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("bsa_quant_mxfp8", x.data_ptr(), code, R, K, q.data_ptr(), s.data_ptr(), K // 32,
+                  _lib.stream_handle(dev))
+    return q, s
 
 
 def moe_workspace_bytes(T: int, H: int, I: int, E: int, k: int) -> int:
@@ -82,7 +107,8 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
     ``hidden [T, H]``, ``router_indices [T, k]``, ``routing_weights [T, k]``;
     packed experts in the checkpoint layout.  Returns ``out [T, H]`` in the
     dtype of ``hidden``; with ``save=True`` also ``(workspace, gate_up_pre)``
-    for the input-gradient backward.  Activations enter the MFMA as bfloat16.
+    for the input-gradient backward.  Activations enter the MFMA as bfloat16,
+    except on ``path="mx"`` (MXFP8, see ``PATHS``).
     """
     if hidden.dim() != 2:
         raise ValueError(f"hidden_states must be [tokens, hidden], got {tuple(hidden.shape)}")

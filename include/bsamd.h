@@ -99,7 +99,14 @@ int bsa_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
  *                   what a later backward reads
  *   save_gate_up    optional float32 [T*k, 2I]: gate_up pre-activations in
  *                   expert-sorted row order, for the backward
- *   path            0 = automatic, 1 = weight-streaming kernel, 2 = tiled kernel
+ *   path            0 = automatic, 1 = weight-streaming kernel, 2 = tiled kernel,
+ *                   3 = native block-scaled MX kernel (activations quantised
+ *                   to MXFP8 by bsa_quant_mxfp8's rule, then
+ *                   v_mfma_scale_f32_32x32x64_f8f6f4 on the packed MXFP4
+ *                   weights; needs H and I multiples of 64, 16-byte aligned
+ *                   blocks, 4-byte aligned scales; not bit-compatible with
+ *                   paths 0-2: the activation quantisation adds a relative
+ *                   error of a few 1e-2)
  *
  * Gate and up columns are interleaved (gate = even, up = odd), alpha and
  * limit parameterise the clamped SwiGLU.  Each token's k contributions are
@@ -169,6 +176,24 @@ int bsa_router_fwd(const void *hidden, int dtype, int64_t T, int64_t H,
  */
 int bsa_router_topk(const void *logits, int dtype, int64_t T, int64_t E,
                     int64_t k, void *scores, int64_t *indices, void *stream);
+
+/*
+ * OCP MXFP8 quantisation (E4M3 elements, one E8M0 scale per 32 consecutive
+ * elements of a row): the activation format of path 3 above.  No reference
+ * counterpart (the reference multiplies unquantised activations,
+ * block_streamer/gptoss.py:45-75).
+ *
+ *   x       dtype [R, K] (K % 32 == 0, 16-byte aligned)
+ *   q       uint8 [R, K] E4M3 codes
+ *   scales  uint8 [R, scale_ld] (scale_ld >= K/32)
+ *
+ * Per block: X = ceil(log2(max |x| / 448)) clamped to [-127, 127] (-127 for
+ * an all-zero block; 448 is the largest E4M3 value, so nothing saturates),
+ * scale byte X + 127 (255 when the block holds inf or NaN), q = E4M3(x / 2^X)
+ * rounded to nearest even.
+ */
+int bsa_quant_mxfp8(const void *x, int dtype, int64_t R, int64_t K, void *q,
+                    void *scales, int64_t scale_ld, void *stream);
 
 /*
  * Bytes of the extra workspace bsa_moe_experts_bwd needs (dense bf16 copies

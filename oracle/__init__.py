@@ -14,8 +14,12 @@ from .oracle import (  # noqa: F401
     bits_equal_or_both_nan,
     dequantize_expert_ref,
     dequant_table_c,
+    e4m3_decode,
+    experts_mx_ref,
     experts_ref,
     mlp_ref,
+    mxfp8_dequant_ref,
+    mxfp8_quant_ref,
     router_ref,
     topk_softmax_ref,
 )

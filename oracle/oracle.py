@@ -18,6 +18,10 @@ Pinning (how each function is checked, see ``tests/test_oracle.py``):
   NaN is compared as NaN, not by bit pattern.
 * router: brute force over all k-subsets on tiny tie-free inputs, and the
   installed transformers ``GptOssTopKRouter``.
+* MXFP8 quantisation (the native MX path only): against torch's
+  float8_e4m3fn cast for in-range values (a library routine, RNE), closed
+  forms at the format's boundaries (max 448, min normal 2^-6, min subnormal
+  2^-9, ties), and exact round trips of representable inputs.
 * experts: the installed transformers dense twin ``GptOssExperts``
   (TF/models/gpt_oss/modeling_gpt_oss.py:68-114) fed the dequantised
   weights, plus invariants (zero routing weight contributes nothing, token
@@ -234,6 +238,93 @@ def mlp_ref(h: torch.Tensor, router_weight: torch.Tensor, router_bias: torch.Ten
     out = experts_ref(flat, idx, scores, *expert_params, alpha=alpha, limit=limit,
                       dtype=dtype)
     return out.reshape(B, S, H), scores
+
+
+# ----------------------------------------------------------------------------- MXFP8
+# The native block-scaled MFMA path quantises activations to OCP MXFP8.  The
+# reference has no such step (it multiplies unquantised activations,
+# block_streamer/gptoss.py:45-75); this restates the published OCP
+# Microscaling Formats v1.0 conversion (section 6.3: shared exponent from
+# floor(log2(amax)) - emax_elem, emax_elem = 8 for E4M3), with the exponent
+# taken one higher where the block maximum would otherwise exceed 448 (so
+# X = ceil(log2(amax / 448)) and nothing saturates), and round-to-nearest-
+# even elements; in float64 with frexp -- a different method from the
+# kernel's bit arithmetic.
+
+E4M3_MAX = 448.0
+
+
+def e4m3_decode(codes: np.ndarray) -> np.ndarray:
+    """OCP E4M3 (bias 7, no infinities, 0x7F/0xFF = NaN) -> float64."""
+    c = np.asarray(codes).astype(np.int64)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    e = (c >> 3) & 15
+    m = c & 7
+    mag = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    mag = np.where((c & 0x7F) == 0x7F, np.nan, mag)
+    return sign * mag
+
+
+def mxfp8_quant_ref(x: torch.Tensor) -> tuple[np.ndarray, np.ndarray]:
+    """[R, K] floats -> (E4M3 codes uint8 [R, K], E8M0 scale bytes uint8 [R, K/32])."""
+    a = x.detach().double().cpu().numpy()
+    R, K = a.shape
+    blk = a.reshape(R, K // 32, 32)
+    amax = np.abs(blk).max(-1)
+    bad = ~np.isfinite(blk).all(-1)
+    f, e = np.frexp(np.where(np.isfinite(amax), amax, 1.0))   # amax = f * 2^e, f in [0.5, 1)
+    X = np.clip(e - 1 - 8 + (2 * f > 1.75), -127, 127)
+    X = np.where(amax == 0, -127, X)
+    scales = np.where(bad, 255, X + 127).astype(np.uint8)
+    y = blk / np.exp2(X.astype(np.float64))[..., None]
+    mag = np.minimum(np.abs(y), E4M3_MAX)
+    _, ee = np.frexp(mag)
+    ee = np.maximum(ee - 1, -6)                       # subnormals: fixed step 2^-9
+    step = np.exp2(ee - 3.0)
+    q = np.minimum(np.rint(mag / step) * step, E4M3_MAX)
+    _, e2 = np.frexp(q)
+    e2 = e2 - 1
+    normal = q >= 2.0 ** -6
+    mant = np.where(normal, q / np.exp2(e2.astype(np.float64)) * 8 - 8, q / 2.0 ** -9)
+    code = np.where(normal, ((e2 + 7) << 3) + np.rint(mant).astype(np.int64),
+                    np.rint(mant).astype(np.int64))
+    code = code | (np.signbit(y).astype(np.int64) << 7)
+    code = np.where(bad[..., None], (np.signbit(blk).astype(np.int64) << 7) | 0x7F, code)
+    return code.reshape(R, K).astype(np.uint8), scales
+
+
+def mxfp8_dequant_ref(codes: np.ndarray, scales: np.ndarray) -> torch.Tensor:
+    """E4M3 codes [R, K] x 2^(scale - 127) per 32 -> float32 tensor."""
+    v = e4m3_decode(codes)
+    R, K = v.shape
+    s = np.exp2(np.asarray(scales).astype(np.float64) - 127.0)
+    out = v.reshape(R, K // 32, 32) * s[..., None]
+    return torch.from_numpy(out.reshape(R, K).astype(np.float32))
+
+
+def experts_mx_ref(h: torch.Tensor, router_indices: torch.Tensor, routing_weights: torch.Tensor,
+                   gate_up_blocks, gate_up_scales, gate_up_bias, down_blocks, down_scales,
+                   down_bias, alpha: float = 1.702, limit: float = 7.0) -> torch.Tensor:
+    """The MX path's arithmetic: ``experts_ref`` with both GEMMs' activations
+    quantised to MXFP8 (hidden per token; the gated activations after their
+    rounding to bfloat16), float32 elsewhere."""
+    E = gate_up_blocks.shape[0]
+    hq = mxfp8_dequant_ref(*mxfp8_quant_ref(h.float()))
+    out = torch.zeros(h.shape, dtype=torch.float32)
+    mask = F.one_hot(router_indices.to(torch.int64), num_classes=E).permute(2, 1, 0)
+    for e in range(E):
+        top_k_pos, token_idx = torch.where(mask[e])
+        if token_idx.numel() == 0:
+            continue
+        w_gu = dequant_torch(gate_up_blocks[e:e + 1], gate_up_scales[e:e + 1], torch.float32)[0]
+        w_dn = dequant_torch(down_blocks[e:e + 1], down_scales[e:e + 1], torch.float32)[0]
+        gu = hq[token_idx].double() @ w_gu.double() + gate_up_bias[e].double()
+        act = apply_gate_ref(gu.float(), alpha, limit).to(torch.bfloat16)
+        aq = mxfp8_dequant_ref(*mxfp8_quant_ref(act))
+        o = (aq.double() @ w_dn.double() + down_bias[e].double()).float()
+        o = o * routing_weights[token_idx, top_k_pos, None].float()
+        out = out.index_add(0, token_idx, o)
+    return out
 
 
 def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:

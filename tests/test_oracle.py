@@ -256,3 +256,80 @@ def test_apply_gate_ref_clamps():
     assert torch.allclose(got[0, 1], g * torch.sigmoid(g * 1.702) * (-6.0))
     g = torch.tensor(0.5)
     assert torch.allclose(got[0, 2], g * torch.sigmoid(g * 1.702) * 1.25)
+
+
+# ----------------------------------------------------------------------------- MXFP8 oracle
+def _f8(x):
+    return torch.tensor(x, dtype=torch.float64).to(torch.float32).to(torch.float8_e4m3fn)
+
+
+def test_e4m3_decode_matches_torch_float8():
+    """The E4M3 table against torch.float8_e4m3fn (OCP E4M3FN) for all 256 codes."""
+    codes = np.arange(256, dtype=np.uint8)
+    ours = oracle.e4m3_decode(codes)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).to(torch.float64).numpy()
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(ours), nan) and nan.sum() == 2   # 0x7F, 0xFF
+    assert np.array_equal(ours[~nan], ref[~nan])
+    assert ours[0x7E] == 448.0 and ours[0x01] == 2.0 ** -9 and ours[0x08] == 2.0 ** -6
+    assert ours[0x38] == 1.0 and ours[0x80] == 0.0 and np.signbit(ours[0x80])
+
+
+@pytest.mark.parametrize("mag", [1e-3, 1.0, 3.0, 1e4])
+def test_mxfp8_quant_matches_torch_cast_and_scale_rule(mag):
+    """Elements: torch's RNE float8_e4m3fn cast of x / 2^X.  Scales: the rule's
+    closed form 224 < amax / 2^X <= 448 for every nonzero block."""
+    g = torch.Generator().manual_seed(int(mag * 1000) % 9973)
+    x = (torch.randn(96, 320, generator=g) * mag).to(torch.bfloat16).float()
+    x[3, :32] = 0.0                                         # all-zero block
+    q, s = oracle.mxfp8_quant_ref(x)
+    X = s.astype(np.int64) - 127
+    blk = x.double().numpy().reshape(96, 10, 32)
+    amax = np.abs(blk).max(-1)
+    nz = amax > 0
+    ratio = amax[nz] / np.exp2(X[nz])
+    assert (ratio > 224).all() and (ratio <= 448).all()
+    assert s[3, 0] == 0
+    y = (blk / np.exp2(X)[..., None]).reshape(96, 320)
+    cast = torch.from_numpy(y).float().to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(cast, q)
+
+
+def test_mxfp8_quant_known_answers():
+    """Hand-worked block: amax 448 gives X = 0; ties round to even."""
+    row = np.zeros(32)
+    vals = [448.0, 1.0625, 1.1875, 2.0 ** -9, 2.0 ** -10, 3 * 2.0 ** -10, -0.0, -6.5, 224.5]
+    row[:len(vals)] = vals
+    q, s = oracle.mxfp8_quant_ref(torch.from_numpy(row[None]).double())
+    assert s[0, 0] == 127
+    # 448 -> 0x7E; 1.0625 tie -> 1.0 (0x38); 1.1875 tie -> 1.25 (0x3A); 2^-9 -> 0x01;
+    # 2^-10 tie -> 0; 3*2^-10 tie -> 2^-8 (0x02); -0 -> 0x80; -6.5 -> 0xCD (-6.5 exact);
+    # 224.5 -> 224 (0x76)
+    assert list(q[0, :len(vals)]) == [0x7E, 0x38, 0x3A, 0x01, 0x00, 0x02, 0x80, 0xCD, 0x76]
+    # amax 1.0 -> X = ceil(log2(1/448)) = -8, element 1.0 -> 256 (0x78)
+    q, s = oracle.mxfp8_quant_ref(torch.ones(1, 32))
+    assert s[0, 0] == 119 and (q == 0x78).all()
+    # amax 449 -> X = 1 (449/2 = 224.5 -> 224)
+    q, s = oracle.mxfp8_quant_ref(torch.full((1, 32), 449.0))
+    assert s[0, 0] == 128 and (q == 0x76).all()
+    # a non-finite element makes the block NaN (scale 255)
+    bad = torch.ones(1, 64)
+    bad[0, 40] = float("inf")
+    q, s = oracle.mxfp8_quant_ref(bad)
+    assert list(s[0]) == [119, 255] and (q[0, 32:] & 0x7F == 0x7F).all()
+
+
+def test_mxfp8_roundtrip_of_representable_blocks():
+    """Blocks built from E4M3 codes whose largest magnitude is in (224, 448]
+    quantise back to the same codes and scale."""
+    rng = np.random.default_rng(5)
+    codes = rng.integers(0, 0x7E, size=(50, 32), dtype=np.int64)
+    codes[:, 0] = rng.integers(0x77, 0x7F, size=50)           # 240 .. 448
+    codes |= rng.integers(0, 2, size=(50, 32)) << 7
+    X = rng.integers(-20, 20, size=50)
+    v = oracle.e4m3_decode(codes) * np.exp2(X)[:, None]
+    q, s = oracle.mxfp8_quant_ref(torch.from_numpy(v))
+    want = codes.astype(np.uint8)
+    zero = (want & 0x7F) == 0                                 # +-0 keep their sign
+    assert np.array_equal(q[~zero], want[~zero])
+    assert np.array_equal(s[:, 0], (X + 127).astype(np.uint8))
