@@ -592,14 +592,17 @@ __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
 // ---------------------------------------------------------------------------
 // Pipelined LDS-tiled kernel (prefill), 16-byte aligned operands.
 //
-// Tile 128 rows x 256 weight rows, BK = 64 (two scale groups), 3 LDS stages
-// filled only by global_load_lds DMA (no register staging):
-//  * A stage [128][64] bf16; row r's 16-byte chunk c is stored at chunk
-//    c ^ (r & 7), so fragment reads are bank-conflict free;
-//  * B stage kept packed, [2 groups][256 rows][16 bytes], natural row order,
-//    plus per row the 4-byte-aligned dword holding its two scale bytes
-//    (dword DMA writes 4 bytes per lane; G is even, so the pair sits at byte
-//    0 or 2 of that dword).
+// Tile 128 rows x 256 weight rows, BK = 64 (two scale groups), NS LDS stages
+// filled only by global_load_lds DMA (no register staging).  The L1 -> L2
+// path is limited by the number of requests, so every DMA covers contiguous
+// runs:
+//  * A stage [128][64] bf16, 8 lanes per row (128 contiguous bytes); row r's
+//    16-byte chunk c is stored at chunk c ^ (r & 7), so fragment reads are
+//    bank-conflict free;
+//  * B stage kept packed, [256 rows][2 groups][16 bytes], 2 lanes per row
+//    (32 contiguous bytes);
+//  * the B scales of the tile's 256 weight rows, one contiguous 256*G-byte
+//    span of the checkpoint tensor, are loaded once per tile.
 // The four waves split N: each computes 128 x 64 (4 x 2 blocks of
 // v_mfma_f32_32x32x16_bf16), so every B fragment is decoded by one wave
 // only.  k order inside a group: MFMA m (0, 1) takes, in lane half lh,
@@ -611,10 +614,51 @@ constexpr int T2_BM = 128;
 constexpr int T2_BN = 256;
 constexpr int T2_BK = 64;
 constexpr int T2_A_BYTES = T2_BM * T2_BK * 2;          // 16 KiB
-constexpr int T2_B_BYTES = 2 * T2_BN * 16;             // 8 KiB
-constexpr int T2_S_BYTES = T2_BN * 4;                  // 1 KiB: one dword per row
-constexpr int T2_STAGE = T2_A_BYTES + T2_B_BYTES + T2_S_BYTES;
-constexpr int T2_DMA_PER_TILE = 4 + 2 + 1;             // per wave: A, B, scales
+constexpr int T2_B_BYTES = T2_BN * 32;                 // 8 KiB
+constexpr int T2_STAGE = T2_A_BYTES + T2_B_BYTES;
+constexpr int T2_DMA_PER_TILE = 4 + 2;                 // per wave: A, B
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited on)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// Wait until at most `ahead` tiles of PER loads each are in flight.
+template <int PER, int MAXAHEAD>
+__device__ __forceinline__ void wait_tiles_ahead(int ahead) {
+  if constexpr (MAXAHEAD >= 4) { if (ahead >= 4) { wait_vmcnt<4 * PER>(); return; } }
+  if constexpr (MAXAHEAD >= 3) { if (ahead == 3) { wait_vmcnt<3 * PER>(); return; } }
+  if constexpr (MAXAHEAD >= 2) { if (ahead == 2) { wait_vmcnt<2 * PER>(); return; } }
+  if constexpr (MAXAHEAD >= 1) { if (ahead == 1) { wait_vmcnt<PER>(); return; } }
+  wait_vmcnt<0>();
+}
+
+// The E8M0 scales of weight rows n0 .. n0+255 of expert e: bytes
+// [(e*N + n0)*G, +256*G) of the [E][N][G] tensor, one contiguous span, into
+// LDS sbs [256][G] with coalesced DMA (16-byte pieces when the tensor is
+// 16-byte aligned -- the span start then is too, as N % 32 == 0 -- else
+// 4-byte pieces).  Pieces past the expert's last row read the span's first
+// piece instead (those rows are never used).  Issued by all four waves.
+template <bool SB16>
+__device__ __forceinline__ void preload_b_scales(const uint8_t* Bs, int e, int N, int n0, int G,
+                                                 uint8_t* sbs, int wave, int lane) {
+  const uint8_t* span = Bs + ((int64_t)e * N + n0) * G;
+  const int valid = min(256, N - n0) * G;
+  constexpr int PIECE = SB16 ? 16 : 4;
+  const int npiece = 256 * G / PIECE;
+  for (int j = wave; j * 64 < npiece; j += 4) {
+    const int c = j * 64 + lane;
+    if (c < npiece) {
+      const uint8_t* src = span + ((c + 1) * PIECE <= valid ? c * PIECE : 0);
+      if constexpr (SB16)
+        __builtin_amdgcn_global_load_lds(src, (lds_void*)(sbs + j * 64 * PIECE), 16, 0, 0);
+      else
+        __builtin_amdgcn_global_load_lds(src, (lds_void*)(sbs + j * 64 * PIECE), 4, 0, 0);
+    }
+  }
+}
 
 // One BK = 64 step of a wave's 128 x 64 block from LDS stage st, software
 // pipelined by hand: the LDS reads for step s+1 are issued before the eight
@@ -635,7 +679,7 @@ __device__ __forceinline__ void t2_ktile(f32x16_t (&acc)[4][2], const uint8_t* s
   auto loadB = [&](int h) {
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb)
-      bq[h][nb] = *reinterpret_cast<const u32x4_t*>(st + T2_A_BYTES + h * (T2_BN * 16) + boff[nb]);
+      bq[h][nb] = *reinterpret_cast<const u32x4_t*>(st + T2_A_BYTES + boff[nb] + h * 16);
   };
   loadB(0);
   loadA(0, afr[0]);
@@ -666,9 +710,9 @@ __device__ __forceinline__ void t2_ktile(f32x16_t (&acc)[4][2], const uint8_t* s
   }
 }
 
-template <int EPI, int T2_NS, int SCHED>
+template <int EPI, int T2_NS, int SCHED, bool SB16>
 __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
-  __shared__ __align__(1024) uint8_t smem[T2_NS * T2_STAGE];
+  extern __shared__ __align__(1024) uint8_t smem[];  // T2_NS stages, then [256][G] B scales
   const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
   if (L < 0) return;
   const int tile = L / a.n_tiles_n;
@@ -698,19 +742,16 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
     const int64_t src = a.row_pair ? (int64_t)(a.row_pair[pos] / a.topk) : pos;
     asrc[i] = a.A + src * a.lda + ch * 8;
   }
-  // B: instruction i = 2*wave + h2 (0..7): group h = i / 4, row q = 64*(i%4) + lane
+  // B: instruction i = 2*wave + h2 covers rows 32i .. 32i+31, 2 lanes per row
   const uint8_t* bsrc[2];
 #pragma unroll
   for (int h2 = 0; h2 < 2; ++h2) {
-    const int i = 2 * wave + h2;
-    const int q = 64 * (i & 3) + lane;
+    const int q = 32 * (2 * wave + h2) + (lane >> 1);
     const bool ok = n0 + q < a.N;
-    bsrc[h2] = a.Bq + ((int64_t)e * a.N + (ok ? n0 + q : 0)) * G * 16 + (i >> 2) * 16;
+    bsrc[h2] = a.Bq + ((int64_t)e * a.N + (ok ? n0 + q : n0)) * G * 16 + (lane & 1) * 16;
   }
-  // scales: row q = 64*wave + lane; with a 4-byte aligned base and E*N*G a
-  // multiple of 4 (N % 32 == 0) the aligned dword never leaves the tensor
-  const int sq = 64 * wave + lane;
-  const uint8_t* ssrc = a.Bs + ((int64_t)e * a.N + (n0 + sq < a.N ? n0 + sq : 0)) * G;
+  uint8_t* sbs = smem + T2_NS * T2_STAGE;
+  preload_b_scales<SB16>(a.Bs, e, a.N, n0, G, sbs, wave, lane);
 
   auto issue = [&](int kt) {
     uint8_t* st = smem + (kt % T2_NS) * T2_STAGE;
@@ -722,23 +763,16 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
     for (int h2 = 0; h2 < 2; ++h2)
       __builtin_amdgcn_global_load_lds(bsrc[h2] + kt * 32,
                                        (lds_void*)(st + T2_A_BYTES + (2 * wave + h2) * 1024), 16, 0, 0);
-    const uint8_t* sp = ssrc + kt * 2;
-    __builtin_amdgcn_global_load_lds(
-        reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(sp) & ~uintptr_t(3)),
-        (lds_void*)(st + T2_A_BYTES + T2_B_BYTES + wave * 256), 4, 0, 0);
   };
 
-  // this lane's two B rows (weight rows n0 + bq[nb]), scale-pair position, bias
+  // this lane's two B rows (weight rows n0 + bq[nb]) and their bias
   int bq[2];
-  uint32_t spar[2];
   float bias[2];
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
     bq[nb] = wave * 64 + nb * 32 + l32;
     const bool ok = n0 + bq[nb] < a.N;
-    const int64_t row = (int64_t)e * a.N + (ok ? n0 + bq[nb] : 0);
-    spar[nb] = (uint32_t)(reinterpret_cast<uintptr_t>(a.Bs + row * G) & 3u);
-    bias[nb] = ok ? bias_at(a.bias, a.bias_dtype, row) : 0.f;
+    bias[nb] = ok ? bias_at(a.bias, a.bias_dtype, (int64_t)e * a.N + n0 + bq[nb]) : 0.f;
   }
   // LDS byte offsets (within a stage) of this lane's A fragments for step
   // (h, m): chunk 4h + 2lh + m of row l32 sits at chunk ^ (row & 7); rows
@@ -750,7 +784,7 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
     const int h = step >> 1, m = step & 1;
     aoff[step] = (uint32_t)(l32 * 128 + (((4 * h + 2 * lh + m) ^ rsw) * 16));
   }
-  uint32_t boff[2] = {(uint32_t)(bq[0] * 16), (uint32_t)(bq[1] * 16)};
+  uint32_t boff[2] = {(uint32_t)(bq[0] * 32), (uint32_t)(bq[1] * 32)};
 
   f32x16_t acc[4][2];
 #pragma unroll
@@ -769,25 +803,16 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
     // next tiles' loads too and serialise the pipeline.  The previous use of
     // the stage refilled below ended before this barrier (its LDS reads fed
     // MFMAs that have issued).
-    {
-      // tiles issued after kt and still allowed in flight
-      const int ahead = min(T2_NS - 2, KT - 1 - kt);
-      if (ahead >= 2)
-        __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * T2_DMA_PER_TILE) & 15) | (((2 * T2_DMA_PER_TILE) >> 4) << 14));
-      else if (ahead == 1)
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (T2_DMA_PER_TILE & 15) | ((T2_DMA_PER_TILE >> 4) << 14));
-      else
-        __builtin_amdgcn_s_waitcnt(0x0070);
-    }
+    // tiles issued after kt and still allowed in flight (the scale preload
+    // is older than every tile, so the first wait covers it too)
+    wait_tiles_ahead<T2_DMA_PER_TILE, T2_NS - 2>(min(T2_NS - 2, KT - 1 - kt));
     asm volatile("s_barrier" ::: "memory");
     if (kt + T2_NS - 1 < KT) issue(kt + T2_NS - 1);
     const uint8_t* st = smem + (kt % T2_NS) * T2_STAGE;
+    // scale bytes of groups 2kt, 2kt+1 (G is even: a 2-byte aligned pair)
     uint32_t sc[2];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const uint32_t d = *reinterpret_cast<const uint32_t*>(st + T2_A_BYTES + T2_B_BYTES + bq[nb] * 4);
-      sc[nb] = (d >> (((spar[nb] + 2u * (uint32_t)kt) & 3u) * 8u)) & 0xFFFFu;
-    }
+    for (int nb = 0; nb < 2; ++nb) sc[nb] = *reinterpret_cast<const uint16_t*>(sbs + bq[nb] * G + 2 * kt);
     t2_ktile<SCHED>(acc, st, sc, aoff, boff, lh);
   }
 
@@ -869,23 +894,6 @@ constexpr int MX_B_BYTES = MX_BN * 32;      // 8 KiB
 constexpr int MX_STAGE = MX_A_BYTES + MX_B_BYTES;
 constexpr int MX_DMA_PER_TILE = 2 + 2;      // per wave: A, B
 
-// s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited on)
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
-}
-
-// Wait until at most `ahead` tiles of PER loads each are in flight.
-template <int PER, int MAXAHEAD>
-__device__ __forceinline__ void wait_tiles_ahead(int ahead) {
-  if constexpr (MAXAHEAD >= 4) { if (ahead >= 4) { wait_vmcnt<4 * PER>(); return; } }
-  if constexpr (MAXAHEAD >= 3) { if (ahead == 3) { wait_vmcnt<3 * PER>(); return; } }
-  if constexpr (MAXAHEAD >= 2) { if (ahead == 2) { wait_vmcnt<2 * PER>(); return; } }
-  if constexpr (MAXAHEAD >= 1) { if (ahead == 1) { wait_vmcnt<PER>(); return; } }
-  wait_vmcnt<0>();
-}
-
 // Dynamic LDS bytes of moe_mx_kernel: NS stages, A scales, B scales.
 inline size_t mx_smem_bytes(int ns, int K, int64_t ldas) {
   return (size_t)ns * MX_STAGE + (size_t)MX_BM * ldas + (size_t)MX_BN * (K / 32);
@@ -927,27 +935,7 @@ __global__ __launch_bounds__(256, 2) void moe_mx_kernel(GemmArgs a) {
 
   // --- scales, once per tile ----------------------------------------------
   {
-    // B: bytes [(e*N + n0)*G, +256*G) of the scale tensor; chunks past this
-    // expert's last row read the span's first chunk instead (never used)
-    const uint8_t* span = a.Bs + ((int64_t)e * a.N + n0) * G;
-    const int valid = (min(MX_BN, a.N - n0)) * G;  // bytes belonging to this tile
-    if constexpr (SB16) {
-      const int nch = MX_BN * G / 16;
-      for (int j = wave; j * 64 < nch; j += 4) {
-        const int c = j * 64 + lane;
-        if (c < nch)
-          __builtin_amdgcn_global_load_lds(span + (c * 16 + 16 <= valid ? c * 16 : 0),
-                                           (lds_void*)(sbs + j * 1024), 16, 0, 0);
-      }
-    } else {
-      const int nch = MX_BN * G / 4;
-      for (int j = wave; j * 64 < nch; j += 4) {
-        const int c = j * 64 + lane;
-        if (c < nch)
-          __builtin_amdgcn_global_load_lds(span + (c * 4 + 4 <= valid ? c * 4 : 0),
-                                           (lds_void*)(sbs + j * 256), 4, 0, 0);
-      }
-    }
+    preload_b_scales<SB16>(a.Bs, e, a.N, n0, G, sbs, wave, lane);
     // A: 128 gathered rows of ldas bytes (16-byte chunks)
     const int cpr = ldas / 16;
     const int nch = MX_BM * cpr;
@@ -1162,6 +1150,26 @@ static int launch_gemm_dense(const GemmArgs& a, int64_t P, hipStream_t st) {
 // aligned weight scales; a.Aq / a.As filled by launch_quant_mxfp8 with a
 // 16-byte aligned scale buffer whose row stride is a multiple of 16).
 constexpr int MX_LAUNCH_NS = 2;  // pipeline stages of the launched MX kernel
+constexpr int T2_LAUNCH_NS = 2;  // and of the launched bf16 tiled kernel
+
+// Kernels using more than 64 KiB of dynamic LDS must be allowed to, once per
+// kernel and device.  `kind` (0..3) x `epi` (0..3) names the kernel.
+static int allow_big_lds(const void* fn, int kind, int epi) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    set_error("no current HIP device");
+    return BSA_EHIP;
+  }
+  static bool allowed[64][4][4];
+  if (!allowed[dev][kind][epi]) {
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
+      set_error("cannot allow 160 KiB of dynamic LDS for a GEMM kernel");
+      return BSA_EHIP;
+    }
+    allowed[dev][kind][epi] = true;
+  }
+  return BSA_OK;
+}
 
 template <int EPI>
 static int launch_gemm_mx(const GemmArgs& a, int64_t P, hipStream_t st) {
@@ -1186,23 +1194,11 @@ static int launch_gemm_mx(const GemmArgs& a, int64_t P, hipStream_t st) {
     set_error("MX GEMM: grid too large");
     return BSA_EINVAL;
   }
-  // more than 64 KiB of dynamic LDS must be allowed per function and device
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
-    set_error("MX GEMM: no current HIP device");
-    return BSA_EHIP;
-  }
-  static bool allowed[64][2];
   const bool sb16 = reinterpret_cast<uintptr_t>(a.Bs) % 16 == 0;
   const void* fn = sb16 ? reinterpret_cast<const void*>(moe_mx_kernel<EPI, MX_LAUNCH_NS, true>)
                         : reinterpret_cast<const void*>(moe_mx_kernel<EPI, MX_LAUNCH_NS, false>);
-  if (!allowed[dev][sb16]) {
-    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
-      set_error("MX GEMM: cannot allow %zu bytes of dynamic LDS", smem);
-      return BSA_EHIP;
-    }
-    allowed[dev][sb16] = true;
-  }
+  int rc = allow_big_lds(fn, 2 + (sb16 ? 1 : 0), EPI);
+  if (rc) return rc;
   if (sb16)
     hipLaunchKernelGGL((moe_mx_kernel<EPI, MX_LAUNCH_NS, true>), dim3((unsigned)grid), dim3(256), smem, st, b);
   else
@@ -1238,7 +1234,22 @@ static int launch_gemm(const GemmArgs& a, int path, int64_t P, hipStream_t st) {
       set_error("tiled GEMM: grid too large");
       return BSA_EINVAL;
     }
-    hipLaunchKernelGGL((moe_tiled2_kernel<EPI, 3, 0>), dim3((unsigned)grid), dim3(256), 0, st, b);
+    const size_t smem = (size_t)T2_LAUNCH_NS * T2_STAGE + (size_t)T2_BN * (a.K / 32);
+    if (smem > 160 * 1024) {
+      set_error("tiled GEMM: K=%d needs %zu bytes of LDS", a.K, smem);
+      return BSA_EINVAL;
+    }
+    const bool sb16 = reinterpret_cast<uintptr_t>(a.Bs) % 16 == 0;
+    const void* fn = sb16 ? reinterpret_cast<const void*>(moe_tiled2_kernel<EPI, T2_LAUNCH_NS, 0, true>)
+                          : reinterpret_cast<const void*>(moe_tiled2_kernel<EPI, T2_LAUNCH_NS, 0, false>);
+    int rc = allow_big_lds(fn, sb16 ? 1 : 0, EPI);
+    if (rc) return rc;
+    if (sb16)
+      hipLaunchKernelGGL((moe_tiled2_kernel<EPI, T2_LAUNCH_NS, 0, true>), dim3((unsigned)grid), dim3(256),
+                         smem, st, b);
+    else
+      hipLaunchKernelGGL((moe_tiled2_kernel<EPI, T2_LAUNCH_NS, 0, false>), dim3((unsigned)grid), dim3(256),
+                         smem, st, b);
   } else {
     const int64_t max_tiles = (P + TL_BM - 1) / TL_BM + a.E;
     int64_t grid = max_tiles * a.n_tiles_n;
