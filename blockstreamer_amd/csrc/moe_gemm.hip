@@ -321,6 +321,29 @@ inline size_t st_smem_bytes(int K) {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited on)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// Wait until at most min(ahead, MAXAHEAD) tiles of PER loads each are in
+// flight.
+template <int PER, int MAXAHEAD>
+__device__ __forceinline__ void wait_tiles_ahead(int ahead) {
+  if constexpr (MAXAHEAD <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (ahead >= MAXAHEAD) {
+      wait_vmcnt<MAXAHEAD * PER>();
+      return;
+    }
+    wait_tiles_ahead<PER, MAXAHEAD - 1>(ahead);
+  }
+}
+
+
 // Copy `bytes` (a multiple of 16) from global to LDS.  DMA: gfx950
 // global_load_lds_dwordx4, each wave moving 1 KiB per instruction with every
 // load of the workgroup in flight at once (16-byte aligned source).
@@ -487,6 +510,182 @@ __global__ __launch_bounds__(256) void moe_stream_kernel(GemmArgs a) {
       }
     }
     __syncthreads();  // the reduction buffer is the next pass's weight slice
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Part-pipelined weight-streaming kernel (decode) for a K = 32*G known at
+// compile time.  Same work split as moe_stream_kernel (one workgroup per
+// expert x 32 weight rows; in 4-group k-step `step` the lane (col, c) of
+// wave step % 4 handles group 4*step + c of weight rows col and 16 + col),
+// but the slice streams in as parts of four k-steps (16 groups, 8 KiB) and
+// each wave computes its step of part p as soon as part p has landed, while
+// the later parts are still in flight.  vmcnt completes in order, so the A
+// operands of every step of the wave are loaded into registers before the
+// first DMA is issued; all DMA counts are compile-time constants, which
+// keeps both the explicit part waits and the compiler's own waits exact.
+// LDS part layout [32 rows][16 slots][16 bytes], group g of row r in slot
+// (g % 16) ^ (r % 16), so the 16 rows read by one lane quarter hit 16
+// different bank groups.  The cross-wave reduction reuses part 0, which a
+// further pass over more than 16 rows reloads.
+// ---------------------------------------------------------------------------
+template <int EPI, int G>
+__global__ __launch_bounds__(256, 3) void moe_stream_parts_kernel(GemmArgs a) {
+  constexpr int NSTEPS = (G + 3) / 4;
+  constexpr int NPART = (NSTEPS + 3) / 4;   // = k-steps per wave
+  constexpr int PART = ST_BN * 16 * 16;     // 8 KiB
+  constexpr int SCALE_BYTES = ST_BN * G;
+  constexpr int SC_PIECES = (SCALE_BYTES + 1023) / 1024;
+  constexpr int SC_PER_WAVE = (SC_PIECES + 3) / 4;
+  static_assert(2 * NPART + SC_PER_WAVE < 64, "vmcnt range");
+  __shared__ __align__(1024) uint8_t sB[NPART * PART];
+  __shared__ __align__(1024) uint8_t sS[SC_PIECES * 1024];
+  f32x4_t* sRed = reinterpret_cast<f32x4_t*>(sB);  // part 0, once every wave is done with it
+
+  const int slices = a.N / ST_BN;
+  const int e = blockIdx.x / slices;
+  const int slice = blockIdx.x - e * slices;
+  const int cnt = a.counts[e];
+  if (cnt == 0) return;
+  const int row0 = a.offsets[e];
+  const int n0 = slice * ST_BN;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 15;
+  const int c = lane >> 4;
+  const uint8_t* gB = a.Bq + ((int64_t)e * a.N + n0) * G * 16;
+  const uint8_t* gS = a.Bs + ((int64_t)e * a.N + n0) * G;
+
+  // --- A operands of this wave's steps for rows 0..15, and the bias --------
+  u32x4_t an[NPART][4];
+  // (only lanes of existing rows load: at decode an expert has a few rows,
+  // and the address unit would otherwise spend most of its time on copies of
+  // row 0; the other lanes' operands are zero and their rows never stored)
+  auto load_a = [](const GemmArgs& ga, int r0, int cn, int pass0, int cl, int cq, int wv,
+                   u32x4_t (&dst)[NPART][4]) {
+    const int r = pass0 + cl;
+    if (r < cn) {
+      const int64_t pos = r0 + r;
+      const int64_t src = ga.row_pair ? (int64_t)(ga.row_pair[pos] / ga.topk) : pos;
+      const uint16_t* arow = ga.A + src * ga.lda;
+#pragma unroll
+      for (int i = 0; i < NPART; ++i) {
+        const int g = min(4 * (wv + 4 * i) + cq, G - 1);
+        const u32x4_t* pp = reinterpret_cast<const u32x4_t*>(arow + g * 32);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) dst[i][m] = pp[m];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NPART; ++i)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) dst[i][m] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  load_a(a, row0, cnt, 0, col, c, wave, an);
+  const float bias0 = bias_at(a.bias, a.bias_dtype, (int64_t)e * a.N + n0 + col);
+  const float bias1 = bias_at(a.bias, a.bias_dtype, (int64_t)e * a.N + n0 + 16 + col);
+
+  // --- DMA: scales, then the parts in order --------------------------------
+#pragma unroll
+  for (int j = 0; j < SC_PER_WAVE; ++j) {
+    const int q = min(wave + 4 * j, SC_PIECES - 1);
+    const int off = q * 1024 + lane * 16;
+    __builtin_amdgcn_global_load_lds(gS + (off + 16 <= SCALE_BYTES ? off : 0), (lds_void*)(sS + q * 1024),
+                                     16, 0, 0);
+  }
+  // part p, piece i (2 per wave): rows 4i .. 4i+3, lane -> row 4i + lane/16,
+  // slot lane%16 holding group 16p + ((lane%16) ^ (row%16)); groups past G
+  // read group 0 (never used)
+  auto issue_part = [](const uint8_t* gb, uint8_t* sb, int p, int wv, int ln) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = 2 * wv + j;
+      const int row = 4 * i + (ln >> 4);
+      const int g = 16 * p + ((ln & 15) ^ (row & 15));
+      __builtin_amdgcn_global_load_lds(gb + ((int64_t)row * G + (g < G ? g : 0)) * 16,
+                                       (lds_void*)(sb + p * PART + i * 1024), 16, 0, 0);
+    }
+  };
+#pragma unroll
+  for (int p = 0; p < NPART; ++p) issue_part(gB, sB, p, wave, lane);
+
+  // LDS offsets of this lane's two rows (col, 16 + col) for its step of any
+  // part: slot (4*wave + c) ^ col
+  const uint32_t boff0 = (uint32_t)(col * 256 + (((4 * wave + c) ^ col) * 16));
+  const uint32_t boff1 = (uint32_t)((16 + col) * 256 + (((4 * wave + c) ^ col) * 16));
+
+  for (int pass0 = 0; pass0 < cnt; pass0 += 16) {
+    if (pass0 > 0) {
+      // part 0 held the reduction: reload it, and the A rows of this pass
+      load_a(a, row0, cnt, pass0, col, c, wave, an);
+      issue_part(gB, sB, 0, wave, lane);
+      wait_vmcnt<0>();
+      asm volatile("s_barrier" ::: "memory");
+    }
+    f32x4_t acc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int p = 0; p < NPART; ++p) {
+      if (pass0 == 0) {
+        // part p has landed once the later parts' pieces are all that is left
+        wait_tiles_ahead<2, NPART - 1>(NPART - 1 - p);
+        asm volatile("s_barrier" ::: "memory");
+      }
+      const int step = 4 * p + wave;
+      if (step < NSTEPS) {
+        const int g = 4 * step + c;
+        u32x4_t q0 = *reinterpret_cast<const u32x4_t*>(sB + p * PART + boff0);
+        u32x4_t q1 = *reinterpret_cast<const u32x4_t*>(sB + p * PART + boff1);
+        uint32_t s0 = sS[col * G + (g < G ? g : 0)];
+        uint32_t s1 = sS[(16 + col) * G + (g < G ? g : 0)];
+        if (g >= G) {
+          q0 = u32x4_t{0u, 0u, 0u, 0u};
+          q1 = q0;
+          s0 = s1 = 127u;
+        }
+        // decode one 8-code quarter of each row per MFMA pair (few live registers)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const s16x8_t av = __builtin_bit_cast(s16x8_t, an[p][m]);
+          acc[0] = mfma16(av, decode8<true>(q0[m], s0), acc[0]);
+          acc[1] = mfma16(av, decode8<true>(q1[m], s1), acc[1]);
+        }
+      }
+    }
+
+    // LDS-only synchronisation (a bare barrier after the LDS counter): a
+    // __syncthreads() fence would also wait for outstanding global stores
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");  // every wave is done with part 0: it becomes sRed
+    sRed[(wave * 2 + 0) * 64 + lane] = acc[0];
+    sRed[(wave * 2 + 1) * 64 + lane] = acc[1];
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    asm volatile("s_barrier" ::: "memory");
+    if (wave < 2) {
+      const int b = wave;
+      f32x4_t v = sRed[(0 * 2 + b) * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) v += sRed[(w * 2 + b) * 64 + lane];
+      const int n = n0 + 16 * b + col;
+      const float bias = b ? bias1 : bias0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int rr = pass0 + 4 * c + j;
+        const float val = v[j] + bias;
+        if constexpr (EPI == EPI_SWIGLU) {
+          const float up = __shfl_xor(val, 1);  // even column = gate, odd = up
+          if (rr < cnt && (col & 1) == 0) epilogue_swiglu<EPI>(a, row0 + rr, n, val, up, 0.f, 0.f);
+        } else {
+          if (rr < cnt) epilogue_one<EPI>(a, row0 + rr, n, val, 0.f);
+        }
+      }
+    }
+    if (pass0 + 16 < cnt) {
+      // sRed (part 0) is reloaded by the next pass
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      asm volatile("s_barrier" ::: "memory");
+    }
   }
 }
 
@@ -708,23 +907,6 @@ constexpr int T2_A_BYTES = T2_BM * T2_BK * 2;          // 16 KiB
 constexpr int T2_B_BYTES = T2_BN * 32;                 // 8 KiB
 constexpr int T2_STAGE = T2_A_BYTES + T2_B_BYTES;
 constexpr int T2_DMA_PER_TILE = 4 + 2;                 // per wave: A, B
-
-// s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited on)
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
-}
-
-// Wait until at most `ahead` tiles of PER loads each are in flight.
-template <int PER, int MAXAHEAD>
-__device__ __forceinline__ void wait_tiles_ahead(int ahead) {
-  if constexpr (MAXAHEAD >= 4) { if (ahead >= 4) { wait_vmcnt<4 * PER>(); return; } }
-  if constexpr (MAXAHEAD >= 3) { if (ahead == 3) { wait_vmcnt<3 * PER>(); return; } }
-  if constexpr (MAXAHEAD >= 2) { if (ahead == 2) { wait_vmcnt<2 * PER>(); return; } }
-  if constexpr (MAXAHEAD >= 1) { if (ahead == 1) { wait_vmcnt<PER>(); return; } }
-  wait_vmcnt<0>();
-}
 
 // The E8M0 scales of weight rows n0 .. n0+BN-1 of expert e: bytes
 // [(e*N + n0)*G, +BN*G) of the [E][N][G] tensor, one contiguous span, into
@@ -1286,7 +1468,12 @@ static int launch_gemm_mx(const GemmArgs& a, int64_t P, hipStream_t st) {
 template <int EPI>
 static int launch_gemm(const GemmArgs& a, int path, int64_t P, hipStream_t st) {
   const bool align16 = (reinterpret_cast<uintptr_t>(a.Bq) % 16) == 0;
-  if (path == PATH_STREAM) {
+  if (path == PATH_STREAM && a.K == 2880 && a.N % ST_BN == 0 && align16 &&
+      reinterpret_cast<uintptr_t>(a.Bs) % 16 == 0) {
+    // the gpt-oss hidden / intermediate size: the part-pipelined kernel
+    const int64_t grid = (int64_t)a.E * (a.N / ST_BN);
+    hipLaunchKernelGGL((moe_stream_parts_kernel<EPI, 90>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  } else if (path == PATH_STREAM) {
     const int slices = (a.N + ST_BN - 1) / ST_BN;
     const int64_t grid = (int64_t)a.E * slices;
     const size_t smem = st_smem_bytes(a.K);
