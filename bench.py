@@ -251,6 +251,31 @@ def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int
     hbm = wbytes / (gemm_ms / 1e3) / 1e9
     tfl = flops / (gemm_ms / 1e3) / 1e12
     res["path"] = path
+    if T >= 4096 and path != "mx":
+        # the LoRA training use: forward saving the gate_up pre-activations,
+        # then the input-gradient backward (expert weights frozen)
+        g = (torch.randn(T, H, generator=torch.Generator().manual_seed(7)) * 0.1).to(torch.bfloat16).to(dev)
+
+        def fwd_bwd():
+            out, ws, pre = kernels.moe_experts_forward(x, idx, w, *args, save=True)
+            return kernels.moe_experts_backward(g, x, idx, w, args[0], args[1], args[3], args[4], ws, pre)
+
+        for _ in range(2):
+            fwd_bwd()
+        torch.cuda.synchronize()
+        pairs = []
+        for _ in range(max(steps // 2, 3)):
+            a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a0.record()
+            fwd_bwd()
+            a1.record()
+            pairs.append((a0, a1))
+        torch.cuda.synchronize()
+        fb_ms = _median_ms(pairs)
+        fwd_ms = ms["dispatch"] + ms["gate_up"] + ms["down"] + ms["combine"]
+        res["fwd_bwd_ms"] = round(fb_ms, 4)
+        res["bwd_ms"] = round(fb_ms - fwd_ms, 4)
+        res["bwd_TFLOP_per_s"] = round(flops / ((fb_ms - fwd_ms) / 1e3) / 1e12, 1)
     if path == "mx":
         # MXFP8 x MXFP4 on the block-scaled MFMA runs at the FP8 rate
         res["roofline"] = {"bound": "mfma", "achieved": round(tfl, 1), "peak": FP8_PEAK_TFLOPS,

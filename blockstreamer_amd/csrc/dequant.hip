@@ -31,11 +31,12 @@ __device__ __forceinline__ void dq_store8(void* out, size_t elem_off, const uint
     u32x4_t a = {v2[0] << 16, v2[0] & 0xFFFF0000u, v2[1] << 16, v2[1] & 0xFFFF0000u};
     u32x4_t b = {v2[2] << 16, v2[2] & 0xFFFF0000u, v2[3] << 16, v2[3] & 0xFFFF0000u};
     u32x4_t* p = reinterpret_cast<u32x4_t*>(static_cast<float*>(out) + elem_off);
-    p[0] = a;
-    p[1] = b;
+    __builtin_nontemporal_store(a, p);
+    __builtin_nontemporal_store(b, p + 1);
   } else {
     u32x4_t v = {v2[0], v2[1], v2[2], v2[3]};
-    *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(out) + elem_off) = v;
+    // streaming output, written once and not read back here: non-temporal
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(out) + elem_off));
   }
 }
 
