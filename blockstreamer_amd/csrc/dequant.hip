@@ -1,4 +1,4 @@
-// MXFP4 -> dense dequantisation (the K1 kernel).
+// MXFP4 -> dense dequantisation.
 //
 // Replaces transformers integrations/mxfp4.py:257-313
 // (_convert_moe_packed_tensors), reached from block_streamer/gptoss.py:41.
