@@ -689,6 +689,347 @@ __global__ __launch_bounds__(256, 3) void moe_stream_parts_kernel(GemmArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Persistent weight-streaming kernel (decode) for a K = 32*G known at compile
+// time.  Persistent workgroups (WPC per CU) each walk a contiguous run of
+// work items; an item is 16 weight rows (one 16x16x32 MFMA column block) of
+// one expert against one 16-row pass of that expert's sorted rows, items
+// ordered by (hit expert, pass, weight-row slice).  Consecutive items of a
+// workgroup share the expert, so the A operands stay in registers and are
+// reloaded only when the (expert, pass) changes.
+//
+// The items' packed bytes stream through a ring of NB LDS slots by
+// global_load_lds DMA, NB - 1 items ahead of the computation.  A slot holds
+// the item's blocks as G/16 parts [16 rows][16 slots][16 B], group g of row r
+// in slot (g % 16) ^ r, so the 16 rows one lane quarter reads sit in 16
+// different bank groups.  The last part has 16 - G % 16 unused slots per row
+// (groups past G); they carry the item's 16*G scale bytes and its 16 bias
+// values, chunk j (16 bytes) in row j / UN, slot (G % 16 + j % UN) ^ (j / UN).
+// So every wave issues exactly G/16 DMA instructions per item and "item i
+// has landed" is vmcnt <= (G/16) * (items issued after i).  The epilogue's
+// stores also count in vmcnt; leaving them out of that bound only makes the
+// wait stricter.  A reload of the A operands waits for everything.
+//
+// Waves split K as the part kernel does (wave w takes groups 16p + 4w + c).
+// All four partial sums go through LDS; wave w finishes rows 4c + w, adding
+// the partials in wave order, so results equal the part kernel's bit for bit.
+// LDS reads of the ring are inline assembly: the compiler cannot tell which
+// slot a computed address falls in, and for an ordinary LDS load it would
+// wait for every global_load_lds in flight (vmcnt(0)), draining the ring.
+// ---------------------------------------------------------------------------
+constexpr int PS_MAX_E = 256;   // experts the hit-list tables hold
+#ifndef PS_NB
+#define PS_NB 3                 // ring slots per workgroup
+#endif
+constexpr int PS_WPC = PS_NB >= 6 ? 1 : 2;  // workgroups per CU
+
+template <int G>
+struct PsCfg {
+  static constexpr int NP = (G + 15) / 16;                 // 4 KiB parts per item
+  static constexpr int PART = 16 * 16 * 16;
+  static constexpr int SLOT = NP * PART;
+  static constexpr int UN = 16 * NP - G;                   // unused slots per row of the last part
+  static constexpr int LAST = (NP - 1) * PART;
+  static_assert(UN > 0 && 16 * UN >= G + 4, "scales and bias fit the last part's spare slots");
+};
+
+// LDS byte offset, within a slot, of byte b of spare chunk j.
+template <int G>
+__host__ __device__ constexpr uint32_t ps_chunk_off(int j, int b) {
+  using C = PsCfg<G>;
+  return (uint32_t)(C::LAST + (j / C::UN) * 256 + (((G % 16) + j % C::UN) ^ (j / C::UN)) * 16 + b);
+}
+
+// Position in a workgroup's item sequence: hit-list entry h (expert e with
+// cnt rows), pass (16-row block of those rows), slice s (16 weight rows).
+struct PsIt {
+  int h, pass, s, e, cnt;
+};
+
+__device__ __forceinline__ void ps_entry(PsIt& it, const int* sHit) {
+  const int v = __builtin_amdgcn_readfirstlane(sHit[it.h]);
+  it.e = v & 0xFF;
+  it.cnt = v >> 8;
+}
+
+__device__ __forceinline__ void ps_next(PsIt& it, const int* sHit, int S, int nhit) {
+  if (++it.s == S) {
+    it.s = 0;
+    if (++it.pass * 16 >= it.cnt) {
+      it.pass = 0;
+      if (++it.h < nhit) ps_entry(it, sHit);
+    }
+  }
+}
+
+// DMA of one item (expert e, weight rows n0 .. n0+15) into slot sb: G/16
+// instructions per wave, wave w filling rows 4w .. 4w+3 of every part.
+template <int G>
+__device__ __forceinline__ void ps_issue(const GemmArgs& a, uint8_t* sb, int e, int n0, int wave,
+                                         int lane, int eb) {
+  using C = PsCfg<G>;
+  const int64_t r0 = (int64_t)e * a.N + n0;
+  const uint8_t* gB = a.Bq + r0 * (G * 16);
+  const uint8_t* gS = a.Bs + r0 * G;
+  const int row = 4 * wave + (lane >> 4);
+  const int sl = (lane & 15) ^ row;
+#pragma unroll
+  for (int p = 0; p < C::NP; ++p) {
+    const uint8_t* src = gB + (row * G + 16 * p + sl) * 16;
+    if (p == C::NP - 1 && 16 * p + sl >= G) {
+      // a spare slot: scale chunk j, then the bias chunks, else anything valid
+      const int j = row * C::UN + (16 * p + sl - G);
+      if (j < G)
+        src = gS + j * 16;
+      else if (a.bias && (j - G) * 16 < 16 * eb)
+        src = static_cast<const uint8_t*>(a.bias) + r0 * eb + (j - G) * 16;
+      else
+        src = gS;
+    }
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)(sb + p * C::PART + wave * 1024), 16, 0, 0);
+  }
+}
+
+// A operands of this lane for pass `pass` of an expert whose sorted rows
+// start at row0: row pass*16 + col, groups 16p + 4*wave + c (clamped to the
+// last group; those lanes meet zero codes).  Rows past cnt are zero.
+template <int G>
+__device__ __forceinline__ void ps_load_a(const GemmArgs& a, int row0, int cnt, int pass, int col, int c,
+                                          int wave, u32x4_t (&an)[PsCfg<G>::NP][4]) {
+  const int r = pass * 16 + col;
+  if (r < cnt) {
+    const int64_t pos = row0 + r;
+    const int64_t src = a.row_pair ? (int64_t)(a.row_pair[pos] / a.topk) : pos;
+    const uint16_t* arow = a.A + src * a.lda;
+#pragma unroll
+    for (int p = 0; p < PsCfg<G>::NP; ++p) {
+      const int g = min(16 * p + 4 * wave + c, G - 1);
+      const u32x4_t* pp = reinterpret_cast<const u32x4_t*>(arow + g * 32);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) an[p][m] = pp[m];
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < PsCfg<G>::NP; ++p)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) an[p][m] = u32x4_t{0u, 0u, 0u, 0u};
+  }
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p);
+}
+__device__ __forceinline__ u32x4_t lds_read_b128(uint32_t addr) {
+  u32x4_t r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+__device__ __forceinline__ uint32_t lds_read_u8(uint32_t addr) {
+  uint32_t r;
+  asm volatile("ds_read_u8 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+__device__ __forceinline__ uint32_t lds_read_b32(uint32_t addr) {
+  uint32_t r;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+
+// Epilogue of one item: row rr of the pass (rows 4c + wave), column n; the
+// four waves' partial sums are added in wave order.  The bias value (raw
+// bits read from the item's slot) is bias_raw's half selected by col.
+template <int EPI>
+__device__ __forceinline__ void ps_epilogue(const GemmArgs& a, const f32x4_t* sRed, int lane, int wave,
+                                            int col, uint32_t braw, int n, int rr, int cnt, int64_t row0) {
+  const float* red = reinterpret_cast<const float*>(sRed) + lane * 4 + wave;
+  float v = red[0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) v += red[w * 256];
+  float bias = 0.f;
+  if (a.bias) {
+    const int eb = a.bias_dtype == DT_F32 ? 4 : 2;
+    const uint32_t bh = (col * eb) & 2 ? braw >> 16 : braw & 0xFFFFu;
+    if (a.bias_dtype == DT_F32)
+      bias = __uint_as_float(braw);
+    else if (a.bias_dtype == DT_BF16)
+      bias = __uint_as_float(bh << 16);
+    else
+      bias = (float)__builtin_bit_cast(_Float16, (uint16_t)bh);
+  }
+  const float val = v + bias;
+  if constexpr (EPI == EPI_SWIGLU) {
+    const float up = __shfl_xor(val, 1);  // even column = gate, odd = up
+    if (rr < cnt && (col & 1) == 0) epilogue_swiglu<EPI>(a, row0 + rr, n, val, up, 0.f, 0.f);
+  } else {
+    if (rr < cnt) epilogue_one<EPI>(a, row0 + rr, n, val, 0.f);
+  }
+}
+
+template <int EPI, int G, int NB>
+__global__ __launch_bounds__(256, NB >= 6 ? 1 : 2) void moe_stream_persist_kernel(GemmArgs a) {
+  using C = PsCfg<G>;
+  constexpr int NP = C::NP;
+  static_assert(NP == 6, "the ring reads below are written out for six parts");
+  extern __shared__ __align__(1024) uint8_t ring[];          // NB slots
+  __shared__ f32x4_t sRed[4 * 64];                           // partial sums of the four waves
+  __shared__ int sHit[PS_MAX_E];                             // e | cnt << 8, in expert order
+  __shared__ int sRow0[PS_MAX_E];                            // first sorted row of entry h
+  int* sScan = reinterpret_cast<int*>(sRed);                 // prologue scratch: 257 ints
+  int* sHPre = sScan + 512;                                  // prologue: passes before entry h
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 15;
+  const int c = lane >> 4;
+  const int S = a.N / 16;
+  const int eb = a.bias_dtype == DT_F32 ? 4 : 2;
+
+  // --- hit list: experts with rows, their pass prefix, in expert order -----
+  const int cnt_t = tid < a.E ? a.counts[tid] : 0;
+  const int off_t = tid < a.E ? a.offsets[tid] : 0;
+  const int mine = (cnt_t > 0 ? 1 : 0) | (((cnt_t + 15) >> 4) << 16);
+  sScan[tid] = mine;
+  __syncthreads();
+  for (int d = 1; d < 256; d <<= 1) {
+    const int v = tid >= d ? sScan[tid - d] : 0;
+    __syncthreads();
+    sScan[tid] += v;
+    __syncthreads();
+  }
+  const int excl = sScan[tid] - mine;
+  if (cnt_t > 0) {
+    sHit[excl & 0xFFFF] = tid | (cnt_t << 8);
+    sHPre[excl & 0xFFFF] = excl >> 16;
+    sRow0[excl & 0xFFFF] = off_t;
+  }
+  const int last = sScan[255];
+  const int nhit = last & 0xFFFF;
+  const int total = (last >> 16) * S;
+  const int chunk = (total + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int start = (int)blockIdx.x * chunk;
+  const int n_items = min(total - start, chunk);
+  __syncthreads();
+  if (n_items <= 0) return;
+  // entry holding the first item's pass
+  const int q0 = start / S;
+  if (tid == 0) sScan[PS_MAX_E] = 0;
+  __syncthreads();
+  if (tid < nhit) {
+    const int np = ((sHit[tid] >> 8) + 15) >> 4;
+    if (sHPre[tid] <= q0 && q0 < sHPre[tid] + np) sScan[PS_MAX_E] = tid;
+  }
+  __syncthreads();
+  PsIt ci;
+  ci.h = __builtin_amdgcn_readfirstlane(sScan[PS_MAX_E]);
+  ps_entry(ci, sHit);
+  ci.pass = q0 - __builtin_amdgcn_readfirstlane(sHPre[ci.h]);
+  ci.s = start - q0 * S;
+  PsIt ii = ci;
+  __syncthreads();  // the prologue scratch becomes the partial-sum buffer
+
+  // --- A operands of the first group (loaded before any DMA is in flight),
+  // then the first NB items' DMA --------------------------------------------
+  u32x4_t an[NP][4];
+  int row0 = __builtin_amdgcn_readfirstlane(sRow0[ci.h]);
+  ps_load_a<G>(a, row0, ci.cnt, ci.pass, col, c, wave, an);
+  wait_vmcnt<0>();
+  const int npre = min(NB, n_items);
+  for (int j = 0; j < npre; ++j) {
+    ps_issue<G>(a, ring + j * C::SLOT, ii.e, ii.s * 16, wave, lane, eb);
+    ps_next(ii, sHit, S, nhit);
+  }
+  const uint32_t boff = (uint32_t)(col * 256 + (((4 * wave + c) ^ col) * 16));
+  uint32_t soff[NP];  // this lane's scale byte of group 16p + 4*wave + c, row col
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int o = col * G + min(16 * p + 4 * wave + c, G - 1);
+    soff[p] = ps_chunk_off<G>(o >> 4, o & 15);
+  }
+  const uint32_t bofs = ps_chunk_off<G>(G + (col * eb) / 16, ((col * eb) & 15) & ~3);
+  const uint32_t ring0 = lds_addr(ring);
+
+  // Per item i: wait for its DMA, barrier, then finish the epilogue of item
+  // i-1 (its partial sums were written before this barrier), read item i's
+  // slot into registers, barrier (the slot is free), refill the slot with
+  // item i+NB, and only then decode and multiply.  Issuing the refill before
+  // the arithmetic keeps the ring as full as possible.
+  int i = 0;
+  bool pend = false;                    // an item waits for its epilogue
+  int p_n = 0, p_rr = 0, p_cnt = 0;     // that item's column, row, rows, first row
+  int64_t p_row0 = 0;
+  uint32_t p_braw = 0;
+  while (true) {
+    // one (expert, pass) group: its remaining slices within this chunk
+    const int run_end = min(n_items, i + (S - ci.s));
+    for (; i < run_end; ++i) {
+      const int slot = i % NB;
+      const uint32_t sb = ring0 + (uint32_t)(slot * C::SLOT);
+      wait_tiles_ahead<NP, NB - 1>(min(NB - 1, n_items - 1 - i));
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's partial sums are written
+      asm volatile("s_barrier" ::: "memory");
+      if (pend) ps_epilogue<EPI>(a, sRed, lane, wave, col, p_braw, p_n, p_rr, p_cnt, p_row0);
+
+      // this lane's codes and scales of its six groups 16p + 4*wave + c
+      u32x4_t q[NP];
+      uint32_t sc[NP];
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        q[p] = lds_read_b128(sb + p * C::PART + boff);
+        sc[p] = lds_read_u8(sb + soff[p]);
+      }
+      uint32_t braw = 0;
+      if (a.bias) braw = lds_read_b32(sb + bofs);
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]), "+v"(q[4]), "+v"(q[5]),
+                     "+v"(sc[0]), "+v"(sc[1]), "+v"(sc[2]), "+v"(sc[3]), "+v"(sc[4]), "+v"(sc[5]),
+                     "+v"(braw));
+      // every wave has its operands (and is done with the partial sums of
+      // item i-1): the slot and the partial-sum buffer are free
+      asm volatile("s_barrier" ::: "memory");
+      if (i + NB < n_items) {
+        ps_issue<G>(a, ring + slot * C::SLOT, ii.e, ii.s * 16, wave, lane, eb);
+        ps_next(ii, sHit, S, nhit);
+      }
+
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        if (16 * p + 4 * wave < G) {
+          u32x4_t qq = q[p];
+          uint32_t ss = sc[p];
+          if (16 * p + 4 * wave + c >= G) {
+            qq = u32x4_t{0u, 0u, 0u, 0u};
+            ss = 127u;
+          }
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+            acc = mfma16(__builtin_bit_cast(s16x8_t, an[p][m]), decode8<true>(qq[m], ss), acc);
+        }
+      }
+      sRed[wave * 64 + lane] = acc;
+      pend = true;
+      p_braw = braw;
+      p_n = ci.s * 16 + col;
+      p_rr = ci.pass * 16 + 4 * c + wave;
+      p_cnt = ci.cnt;
+      p_row0 = row0;
+      ++ci.s;
+    }
+    if (i >= n_items) break;
+    // next group: reload the A operands (waits for everything in flight)
+    ci.s = S - 1;
+    ps_next(ci, sHit, S, nhit);
+    row0 = __builtin_amdgcn_readfirstlane(sRow0[ci.h]);
+    ps_load_a<G>(a, row0, ci.cnt, ci.pass, col, c, wave, an);
+    wait_vmcnt<0>();
+  }
+  // the last item's epilogue
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+  ps_epilogue<EPI>(a, sRed, lane, wave, col, p_braw, p_n, p_rr, p_cnt, p_row0);
+}
+
 // Logical tile index of this workgroup for the tiled kernels.  The live
 // tiles (num_tiles row tiles x n_tiles_n column tiles; the row-tile count is
 // only known on the device, the grid is sized for the maximum) are split
@@ -1400,7 +1741,7 @@ constexpr int T2_LAUNCH_NS = 2;  // and of the launched bf16 tiled kernel
 
 // Kernels using more than 64 KiB of dynamic LDS must be allowed to, once per
 // kernel and device.  `kind` (0..7) x `epi` (0..3) names the kernel.
-static int allow_big_lds(const void* fn, int kind, int epi) {
+static int allow_big_lds(const void* fn, int kind, int epi, int bytes = 160 * 1024) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
     set_error("no current HIP device");
@@ -1408,8 +1749,8 @@ static int allow_big_lds(const void* fn, int kind, int epi) {
   }
   static bool allowed[64][8][4];
   if (!allowed[dev][kind][epi]) {
-    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
-      set_error("cannot allow 160 KiB of dynamic LDS for a GEMM kernel");
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
+      set_error("cannot allow %d bytes of dynamic LDS for a GEMM kernel", bytes);
       return BSA_EHIP;
     }
     allowed[dev][kind][epi] = true;
@@ -1465,11 +1806,35 @@ static int launch_gemm_mx(const GemmArgs& a, int64_t P, hipStream_t st) {
   return launch_mx_cfg<EPI, 2, 4, 2>(a, P, small, st);
 }
 
+// Compute units of the current device (cached per device).
+static int cu_count() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 template <int EPI>
 static int launch_gemm(const GemmArgs& a, int path, int64_t P, hipStream_t st) {
   const bool align16 = (reinterpret_cast<uintptr_t>(a.Bq) % 16) == 0;
-  if (path == PATH_STREAM && a.K == 2880 && a.N % ST_BN == 0 && align16 &&
-      reinterpret_cast<uintptr_t>(a.Bs) % 16 == 0) {
+  const int cus = cu_count();
+  if (path == PATH_STREAM && a.K == 2880 && a.N % 16 == 0 && a.E <= PS_MAX_E && align16 &&
+      reinterpret_cast<uintptr_t>(a.Bs) % 16 == 0 && reinterpret_cast<uintptr_t>(a.bias) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(a.A) % 16 == 0 && a.lda % 8 == 0 && P <= (1 << 19) && cus > 0) {
+    // the gpt-oss hidden / intermediate size: PS_WPC persistent workgroups per CU
+    constexpr int ring = PS_NB * PsCfg<90>::SLOT;
+    const void* fn = reinterpret_cast<const void*>(moe_stream_persist_kernel<EPI, 90, PS_NB>);
+    int rc = allow_big_lds(fn, 6, EPI, ring);
+    if (rc) return rc;
+    hipLaunchKernelGGL((moe_stream_persist_kernel<EPI, 90, PS_NB>), dim3((unsigned)(cus * PS_WPC)), dim3(256),
+                       ring, st, a);
+  } else if (path == PATH_STREAM && a.K == 2880 && a.N % ST_BN == 0 && align16 &&
+             reinterpret_cast<uintptr_t>(a.Bs) % 16 == 0) {
     // the gpt-oss hidden / intermediate size: the part-pipelined kernel
     const int64_t grid = (int64_t)a.E * (a.N / ST_BN);
     hipLaunchKernelGGL((moe_stream_parts_kernel<EPI, 90>), dim3((unsigned)grid), dim3(256), 0, st, a);

@@ -1,0 +1,99 @@
+"""Decode weight-streaming kernels on the gpt-oss shape (K = 2880).
+
+The persistent kernel (one workgroup per CU walking (expert, pass, slice)
+items through an LDS ring) and the one-workgroup-per-slice part kernel split
+K the same way and add the partial sums in the same order, so their outputs
+must agree bit for bit.  A bias view that is only 2-byte aligned sends the
+same call to the part kernel (the persistent kernel DMAs the bias and needs
+4-byte alignment); everything else is identical.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from blockstreamer_amd import kernels, synthetic
+from tests.conftest import announce
+from tests.moe_util import assert_layer_close, expert_args, oracle_tokens
+
+pytestmark = pytest.mark.gpu
+
+
+def _shifted(x: torch.Tensor) -> torch.Tensor:
+    """Same values, storage starting one element (2 bytes) later."""
+    buf = torch.empty(x.numel() + 1, dtype=x.dtype, device=x.device)
+    buf[1:] = x.reshape(-1)
+    v = buf[1:].view(x.shape)
+    assert v.data_ptr() % 4 == 2
+    return v
+
+
+def _both_kernels(t, idx, w):
+    args = list(expert_args(t))
+    persist = kernels.moe_experts_forward(t["hidden"], idx, w, *args, path="stream")
+    args[2] = _shifted(args[2])
+    args[5] = _shifted(args[5])
+    parts = kernels.moe_experts_forward(t["hidden"], idx, w, *args, path="stream")
+    torch.cuda.synchronize()
+    return persist, parts
+
+
+@pytest.mark.parametrize("T", [1, 64])
+def test_persistent_equals_part_kernel(device, T):
+    shape = synthetic.MoEShape(128, 4, 2880, 2880, T)
+    t = synthetic.moe_layer(shape, seed=4, scale_lo=115, scale_hi=131, router_bias_std=0.5,
+                            device=device)
+    _, w, idx = kernels.router_forward(t["hidden"], t["router_weight"], t["router_bias"], 4)
+    announce(f"persistent vs part kernel T={T}")
+    persist, parts = _both_kernels(t, idx, w)
+    assert torch.equal(persist.view(torch.int16), parts.view(torch.int16))
+
+
+def test_persistent_multi_pass_expert(device):
+    """An expert with 40 rows (three 16-row passes) next to experts with one."""
+    T = 48
+    shape = synthetic.MoEShape(128, 4, 2880, 2880, T)
+    t = synthetic.moe_layer(shape, seed=21, scale_lo=116, scale_hi=120, device=device)
+    idx, w = synthetic.random_routing(T, 128, 4, seed=22, device=device)
+    idx = idx.clone()
+    hot = 77
+    idx[idx == hot] = (hot + 1) % 128       # keep each token's experts distinct
+    idx[:40, 0] = hot
+    idx = idx.contiguous()
+    assert int((idx == hot).sum()) == 40
+    announce("persistent kernel, 40-row expert")
+    persist, parts = _both_kernels(t, idx, w)
+    assert torch.equal(persist.view(torch.int16), parts.view(torch.int16))
+    tokens = torch.tensor([0, 17, 39, 40, 47])
+    want = oracle_tokens(t, idx.cpu(), w.cpu(), tokens)
+    assert_layer_close(persist.cpu()[tokens], want, "40-row expert", absolute=True)
+
+
+def test_persistent_float32_bias_vs_oracle(device):
+    T = 16
+    shape = synthetic.MoEShape(128, 4, 2880, 2880, T)
+    t = synthetic.moe_layer(shape, seed=31, scale_lo=116, scale_hi=120, device=device)
+    t["gate_up_proj_bias"] = t["gate_up_proj_bias"].float()
+    t["down_proj_bias"] = t["down_proj_bias"].float()
+    idx, w = synthetic.random_routing(T, 128, 4, seed=32, device=device)
+    announce("persistent kernel, float32 biases")
+    got = kernels.moe_experts_forward(t["hidden"], idx, w, *expert_args(t), path="stream")
+    args = [a.cpu() for a in expert_args(t)]
+    want = oracle.experts_ref(t["hidden"].cpu(), idx.cpu(), w.cpu().float(), *args)
+    assert_layer_close(got, want, "float32 biases", absolute=True)
+
+
+def test_persistent_single_expert_most_workgroups_idle(device):
+    """T=1, k=1: 180 down items and 360 gate_up items over one workgroup per CU."""
+    shape = synthetic.MoEShape(128, 1, 2880, 2880, 1)
+    t = synthetic.moe_layer(shape, seed=41, scale_lo=116, scale_hi=120, device=device)
+    idx = torch.tensor([[127]], device=device)
+    w = torch.ones(1, 1, dtype=torch.bfloat16, device=device)
+    announce("persistent kernel, one token one expert")
+    persist, parts = _both_kernels(t, idx, w)
+    assert torch.equal(persist.view(torch.int16), parts.view(torch.int16))
+    want = oracle.experts_ref(t["hidden"].cpu(), idx.cpu(), w.cpu().float(),
+                              *[a.cpu() for a in expert_args(t)])
+    assert_layer_close(persist, want, "one token one expert", absolute=True)
