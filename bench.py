@@ -289,7 +289,7 @@ def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int
     elif T * k <= 16 * E:
         res["roofline"] = {"bound": "hbm", "achieved": round(hbm, 1), "peak": HBM_PEAK_GBS,
                            "unit": "GB/s", "frac": round(hbm / HBM_PEAK_GBS, 4),
-                           "kernel": "moe_stream_parts_kernel gate_up + down",
+                           "kernel": "moe_stream_persist_kernel gate_up + down",
                            "algorithmic_bytes": wbytes}
         if T == 64:
             gu_b = traffic_record("moe_layer_gptoss120b_decode_t64", "gate_up_hbm_bytes")

@@ -90,6 +90,7 @@ struct GemmArgs {
 };
 
 typedef __attribute__((ext_vector_type(8))) short s16x8_t;
+typedef __attribute__((ext_vector_type(8))) int i32x8_t;
 
 __device__ __forceinline__ f32x4_t mfma16(s16x8_t a, s16x8_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
@@ -717,11 +718,8 @@ __global__ __launch_bounds__(256, 3) void moe_stream_parts_kernel(GemmArgs a) {
 // slot a computed address falls in, and for an ordinary LDS load it would
 // wait for every global_load_lds in flight (vmcnt(0)), draining the ring.
 // ---------------------------------------------------------------------------
-constexpr int PS_MAX_E = 256;   // experts the hit-list tables hold
-#ifndef PS_NB
-#define PS_NB 3                 // ring slots per workgroup
-#endif
-constexpr int PS_WPC = PS_NB >= 6 ? 1 : 2;  // workgroups per CU
+constexpr int PS_TEAM_NB = 3;   // ring slots per team
+constexpr int PS_TEAMS = 1;     // teams per workgroup (1: two workgroups per CU)
 
 template <int G>
 struct PsCfg {
@@ -748,8 +746,8 @@ struct PsIt {
 
 __device__ __forceinline__ void ps_entry(PsIt& it, const int* sHit) {
   const int v = __builtin_amdgcn_readfirstlane(sHit[it.h]);
-  it.e = v & 0xFF;
-  it.cnt = v >> 8;
+  it.e = v & 0x3FF;
+  it.cnt = v >> 10;
 }
 
 __device__ __forceinline__ void ps_next(PsIt& it, const int* sHit, int S, int nhit) {
@@ -790,29 +788,143 @@ __device__ __forceinline__ void ps_issue(const GemmArgs& a, uint8_t* sb, int e, 
   }
 }
 
-// A operands of this lane for pass `pass` of an expert whose sorted rows
-// start at row0: row pass*16 + col, groups 16p + 4*wave + c (clamped to the
-// last group; those lanes meet zero codes).  Rows past cnt are zero.
+// Activations as two MXFP8 terms.  A bf16 block x (32 values sharing one
+// E8M0 scale) is written hi + lo with
+//   hi = E4M3(x / 2^X),            X  = ceil(log2(amax|x| / 448)),
+//   lo = E4M3((x - hi*2^X) / 2^Y),  Y  = ceil(log2(amax|residual| / 448)),
+// both rounded to nearest even (v_cvt_scalef32_pk_fp8_f32 divides by the
+// scale).  A bf16 value has 8 significant bits and E4M3 4, so the residual of
+// every element within 2^17 of the block maximum is exact in E4M3: hi*2^X +
+// lo*2^Y equals x except for elements below 2^-17 of the block maximum, whose
+// error is below 2^-21 of it.  The packed MXFP4 weights then go to the
+// block-scaled MFMA as they are, two instructions (hi, lo) per 128 k.
+//
+// 16 values of one lane (two u32x4 of bf16) -> 16 hi and 16 lo codes; the
+// block is completed by the partner lane 16 lanes away (lane group c ^ 1).
+// Scale bytes are returned as E8M0 (X + 127, Y + 127).
+__device__ __forceinline__ int mx_block_exp(float amax) {
+  const uint32_t ab = __float_as_uint(amax);
+  const int e = (int)(ab >> 23) - 127;
+  // significand above 1.75 needs the next exponent (448 = 1.75 * 2^8)
+  const int X = e - 8 + ((ab & 0x7FFFFFu) > 0x600000u ? 1 : 0);
+  return min(max(X, -126), 127);
+}
+
+__device__ __forceinline__ void mx_split16(const u32x4_t& v0, const u32x4_t& v1, bool valid, u32x4_t& hi,
+                                           u32x4_t& lo, uint32_t& sh, uint32_t& sl) {
+  float f[16];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    const uint32_t w = d < 4 ? v0[d] : v1[d - 4];
+    f[2 * d] = valid ? __uint_as_float(w << 16) : 0.f;
+    f[2 * d + 1] = valid ? __uint_as_float(w & 0xFFFF0000u) : 0.f;
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(f[j]));
+  amax = fmaxf(amax, __shfl_xor(amax, 16));
+  const int X = mx_block_exp(amax);
+  const float s = __uint_as_float((uint32_t)(X + 127) << 23);
+  float r[16];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    typedef short v2s __attribute__((ext_vector_type(2)));
+    typedef float v2f __attribute__((ext_vector_type(2)));
+    v2s q = {0, 0};
+    q = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(q, f[4 * d], f[4 * d + 1], s, false);
+    q = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(q, f[4 * d + 2], f[4 * d + 3], s, true);
+    const uint32_t w = __builtin_bit_cast(uint32_t, q);
+    hi[d] = w;
+    const v2f d0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((int)w, s, false);
+    const v2f d1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((int)w, s, true);
+    r[4 * d] = f[4 * d] - d0[0];
+    r[4 * d + 1] = f[4 * d + 1] - d0[1];
+    r[4 * d + 2] = f[4 * d + 2] - d1[0];
+    r[4 * d + 3] = f[4 * d + 3] - d1[1];
+  }
+  float rmax = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) rmax = fmaxf(rmax, fabsf(r[j]));
+  rmax = fmaxf(rmax, __shfl_xor(rmax, 16));
+  const int Y = mx_block_exp(rmax);
+  const float sr = __uint_as_float((uint32_t)(Y + 127) << 23);
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    typedef short v2s __attribute__((ext_vector_type(2)));
+    v2s q = {0, 0};
+    q = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(q, r[4 * d], r[4 * d + 1], sr, false);
+    q = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(q, r[4 * d + 2], r[4 * d + 3], sr, true);
+    lo[d] = __builtin_bit_cast(uint32_t, q);
+  }
+  sh = (uint32_t)(X + 127);
+  sl = (uint32_t)(Y + 127);
+}
+
+// v_mfma_scale_f32_16x16x128_f8f6f4 with E4M3 A, E2M1 B; the A scale is byte
+// `sel` of sa (sel folds to a constant once the caller's loop is unrolled).
+__device__ __forceinline__ f32x4_t mfma_mx16(const i32x8_t& a, const i32x8_t& b, f32x4_t c, uint32_t sa,
+                                             int sel, uint32_t sb) {
+  switch (sel) {
+    case 0: return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 4, 0, (int)sa, 0, (int)sb);
+    case 1: return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 4, 1, (int)sa, 0, (int)sb);
+    case 2: return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 4, 2, (int)sa, 0, (int)sb);
+    default: return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 4, 3, (int)sa, 0, (int)sb);
+  }
+}
+
+// FP8 A operands (hi and lo) of this lane for pass `pass` of an expert whose
+// sorted rows start at row0, for the 16x16x128 block-scaled MFMA over the
+// 4-group window 16p + 4*wave of part p: lane group c holds k 16c .. 16c+15
+// (bytes 0-15) and 64+16c .. 64+16c+15 (bytes 16-31) of the window and
+// supplies the scale of window block c.  Rows past cnt repeat the last valid
+// row (their outputs are never stored).  Scale bytes of parts 0-3 / 4-5 are
+// packed into sh[0] / sh[1] (byte p % 4), likewise sl.
 template <int G>
-__device__ __forceinline__ void ps_load_a(const GemmArgs& a, int row0, int cnt, int pass, int col, int c,
-                                          int wave, u32x4_t (&an)[PsCfg<G>::NP][4]) {
-  const int r = pass * 16 + col;
-  if (r < cnt) {
-    const int64_t pos = row0 + r;
-    const int64_t src = a.row_pair ? (int64_t)(a.row_pair[pos] / a.topk) : pos;
-    const uint16_t* arow = a.A + src * a.lda;
+__device__ __forceinline__ void ps_load_a_raw(const GemmArgs& a, int row0, int cnt, int pass, int col, int c,
+                                              int wave, u32x4_t (&raw)[PsCfg<G>::NP][4]) {
+  constexpr int NP = PsCfg<G>::NP;
+  const int r = min(pass * 16 + col, cnt - 1);
+  const int64_t pos = row0 + r;
+  const int64_t src = a.row_pair ? (int64_t)(a.row_pair[pos] / a.topk) : pos;
+  const uint16_t* arow = a.A + src * a.lda;
 #pragma unroll
-    for (int p = 0; p < PsCfg<G>::NP; ++p) {
-      const int g = min(16 * p + 4 * wave + c, G - 1);
-      const u32x4_t* pp = reinterpret_cast<const u32x4_t*>(arow + g * 32);
+  for (int p = 0; p < NP; ++p) {
+    const int gw = 16 * p + 4 * wave;
+    const int k0 = gw + (c >> 1) < G ? 32 * gw + 16 * c : 0;
+    const int k1 = gw + 2 + (c >> 1) < G ? 32 * gw + 64 + 16 * c : 0;
+    const u32x4_t* p0 = reinterpret_cast<const u32x4_t*>(arow + k0);
+    const u32x4_t* p1 = reinterpret_cast<const u32x4_t*>(arow + k1);
+    raw[p][0] = p0[0];
+    raw[p][1] = p0[1];
+    raw[p][2] = p1[0];
+    raw[p][3] = p1[1];
+  }
+}
+
+template <int G>
+__device__ __forceinline__ void ps_quant_a(const u32x4_t (&raw)[PsCfg<G>::NP][4], int c, int wave,
+                                           i32x8_t (&ah)[PsCfg<G>::NP], i32x8_t (&al)[PsCfg<G>::NP],
+                                           uint32_t (&sh)[2], uint32_t (&sl)[2]) {
+  constexpr int NP = PsCfg<G>::NP;
+  sh[0] = sh[1] = sl[0] = sl[1] = 0u;
 #pragma unroll
-      for (int m = 0; m < 4; ++m) an[p][m] = pp[m];
-    }
-  } else {
-#pragma unroll
-    for (int p = 0; p < PsCfg<G>::NP; ++p)
-#pragma unroll
-      for (int m = 0; m < 4; ++m) an[p][m] = u32x4_t{0u, 0u, 0u, 0u};
+  for (int p = 0; p < NP; ++p) {
+    const int gw = 16 * p + 4 * wave;
+    u32x4_t h0, l0, h1, l1;
+    uint32_t xh0, xl0, xh1, xl1;
+    mx_split16(raw[p][0], raw[p][1], gw + (c >> 1) < G, h0, l0, xh0, xl0);
+    mx_split16(raw[p][2], raw[p][3], gw + 2 + (c >> 1) < G, h1, l1, xh1, xl1);
+    ah[p] = i32x8_t{(int)h0[0], (int)h0[1], (int)h0[2], (int)h0[3], (int)h1[0], (int)h1[1], (int)h1[2], (int)h1[3]};
+    al[p] = i32x8_t{(int)l0[0], (int)l0[1], (int)l0[2], (int)l0[3], (int)l1[0], (int)l1[1], (int)l1[2], (int)l1[3]};
+    // lane group c must supply the scale of window block c: groups 0 and 3
+    // hold it (blocks 0 and 3 are their first / second halves), groups 1 and
+    // 2 trade (block 1 is group 2's first half, block 2 group 1's second)
+    const uint32_t offer_h = c == 1 ? xh1 : xh0, offer_l = c == 1 ? xl1 : xl0;
+    const uint32_t got_h = __shfl_xor(offer_h, 48), got_l = __shfl_xor(offer_l, 48);
+    const uint32_t bh = c == 0 ? xh0 : (c == 3 ? xh1 : got_h);
+    const uint32_t bl = c == 0 ? xl0 : (c == 3 ? xl1 : got_l);
+    sh[p >> 2] |= bh << (8 * (p & 3));
+    sl[p >> 2] |= bl << (8 * (p & 3));
   }
 }
 
@@ -865,21 +977,32 @@ __device__ __forceinline__ void ps_epilogue(const GemmArgs& a, const f32x4_t* sR
   }
 }
 
-template <int EPI, int G, int NB>
-__global__ __launch_bounds__(256, NB >= 6 ? 1 : 2) void moe_stream_persist_kernel(GemmArgs a) {
+// TEAMS teams of four waves per workgroup, each team with its own
+// PS_TEAM_NB-slot ring and its own share of the workgroup's contiguous run of
+// items.  TEAMS = 2: one 512-thread workgroup per CU whose teams meet at every
+// barrier, so both halves of a CU finish together.  TEAMS = 1: two
+// independent 256-thread workgroups per CU (more overlap between them, but
+// the CU serves them unevenly).
+template <int EPI, int G, int TEAMS>
+__global__ __launch_bounds__(256 * TEAMS, 3 - TEAMS) void moe_stream_persist_kernel(GemmArgs a) {
   using C = PsCfg<G>;
   constexpr int NP = C::NP;
+  constexpr int NB = PS_TEAM_NB;
+  constexpr int NT = 256 * TEAMS;                            // threads
+  constexpr int MAXE = NT;                                   // experts the hit-list tables hold
   static_assert(NP == 6, "the ring reads below are written out for six parts");
-  extern __shared__ __align__(1024) uint8_t ring[];          // NB slots
-  __shared__ f32x4_t sRed[4 * 64];                           // partial sums of the four waves
-  __shared__ int sHit[PS_MAX_E];                             // e | cnt << 8, in expert order
-  __shared__ int sRow0[PS_MAX_E];                            // first sorted row of entry h
-  int* sScan = reinterpret_cast<int*>(sRed);                 // prologue scratch: 257 ints
-  int* sHPre = sScan + 512;                                  // prologue: passes before entry h
+  extern __shared__ __align__(1024) uint8_t ring[];          // TEAMS x NB slots
+  __shared__ f32x4_t sRed[TEAMS * 4 * 64];                   // partial sums, [team][wave][lane]
+  __shared__ int sHit[MAXE];                                 // e | cnt << 10, in expert order
+  __shared__ int sRow0[MAXE];                                // first sorted row of entry h
+  __shared__ int sSeg[2];                                    // each team's steps to its next reload
+  int* sScan = reinterpret_cast<int*>(sRed);                 // prologue scratch: NT + 2 ints
+  int* sHPre = sScan + NT + 2;                               // prologue: passes before entry h
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int team = TEAMS == 2 ? __builtin_amdgcn_readfirstlane(tid >> 8) : 0;
+  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);   // wave within the team
   const int col = lane & 15;
   const int c = lane >> 4;
   const int S = a.N / 16;
@@ -891,7 +1014,7 @@ __global__ __launch_bounds__(256, NB >= 6 ? 1 : 2) void moe_stream_persist_kerne
   const int mine = (cnt_t > 0 ? 1 : 0) | (((cnt_t + 15) >> 4) << 16);
   sScan[tid] = mine;
   __syncthreads();
-  for (int d = 1; d < 256; d <<= 1) {
+  for (int d = 1; d < NT; d <<= 1) {
     const int v = tid >= d ? sScan[tid - d] : 0;
     __syncthreads();
     sScan[tid] += v;
@@ -899,11 +1022,11 @@ __global__ __launch_bounds__(256, NB >= 6 ? 1 : 2) void moe_stream_persist_kerne
   }
   const int excl = sScan[tid] - mine;
   if (cnt_t > 0) {
-    sHit[excl & 0xFFFF] = tid | (cnt_t << 8);
+    sHit[excl & 0xFFFF] = tid | (cnt_t << 10);
     sHPre[excl & 0xFFFF] = excl >> 16;
     sRow0[excl & 0xFFFF] = off_t;
   }
-  const int last = sScan[255];
+  const int last = sScan[NT - 1];
   const int nhit = last & 0xFFFF;
   const int total = (last >> 16) * S;
   const int chunk = (total + (int)gridDim.x - 1) / (int)gridDim.x;
@@ -911,33 +1034,50 @@ __global__ __launch_bounds__(256, NB >= 6 ? 1 : 2) void moe_stream_persist_kerne
   const int n_items = min(total - start, chunk);
   __syncthreads();
   if (n_items <= 0) return;
-  // entry holding the first item's pass
-  const int q0 = start / S;
-  if (tid == 0) sScan[PS_MAX_E] = 0;
+  // the workgroup's run: team 0 takes the first half, team 1 the rest
+  const int half = TEAMS == 2 ? (n_items + 1) >> 1 : n_items;
+  const int tstart = start + (team ? half : 0);
+  const int tn = team ? n_items - half : half;   // team 1 may have one item less (or none)
+  // entries holding each team's first pass
+  if (tid < 2) sScan[NT + tid] = 0;
   __syncthreads();
   if (tid < nhit) {
-    const int np = ((sHit[tid] >> 8) + 15) >> 4;
-    if (sHPre[tid] <= q0 && q0 < sHPre[tid] + np) sScan[PS_MAX_E] = tid;
+    const int np = ((sHit[tid] >> 10) + 15) >> 4;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int q = min(start + (t ? half : 0), total - 1) / S;
+      if (sHPre[tid] <= q && q < sHPre[tid] + np) sScan[NT + t] = tid;
+    }
   }
   __syncthreads();
   PsIt ci;
-  ci.h = __builtin_amdgcn_readfirstlane(sScan[PS_MAX_E]);
+  const int tq0 = min(tstart, total - 1) / S;
+  ci.h = __builtin_amdgcn_readfirstlane(sScan[NT + team]);
   ps_entry(ci, sHit);
-  ci.pass = q0 - __builtin_amdgcn_readfirstlane(sHPre[ci.h]);
-  ci.s = start - q0 * S;
+  ci.pass = tq0 - __builtin_amdgcn_readfirstlane(sHPre[ci.h]);
+  ci.s = min(tstart, total - 1) - tq0 * S;
   PsIt ii = ci;
   __syncthreads();  // the prologue scratch becomes the partial-sum buffer
 
+  uint8_t* tring = ring + team * (NB * C::SLOT);
+  f32x4_t* tred = sRed + team * 256;
+
   // --- A operands of the first group (loaded before any DMA is in flight),
-  // then the first NB items' DMA --------------------------------------------
-  u32x4_t an[NP][4];
-  int row0 = __builtin_amdgcn_readfirstlane(sRow0[ci.h]);
-  ps_load_a<G>(a, row0, ci.cnt, ci.pass, col, c, wave, an);
-  wait_vmcnt<0>();
-  const int npre = min(NB, n_items);
-  for (int j = 0; j < npre; ++j) {
-    ps_issue<G>(a, ring + j * C::SLOT, ii.e, ii.s * 16, wave, lane, eb);
-    ps_next(ii, sHit, S, nhit);
+  // then the team's first NB items' DMA, then the quantisation -------------
+  i32x8_t ah[NP], al[NP];   // FP8 hi / lo activation operands
+  uint32_t sah[2], sal[2];   // their scale bytes, byte p % 4 of word p / 4
+  int row0 = 0;
+  if (tn > 0) {
+    row0 = __builtin_amdgcn_readfirstlane(sRow0[ci.h]);
+    u32x4_t raw[NP][4];
+    ps_load_a_raw<G>(a, row0, ci.cnt, ci.pass, col, c, wave, raw);
+    wait_vmcnt<0>();
+    const int npre = min(NB, tn);
+    for (int j = 0; j < npre; ++j) {
+      ps_issue<G>(a, tring + j * C::SLOT, ii.e, ii.s * 16, wave, lane, eb);
+      ps_next(ii, sHit, S, nhit);
+    }
+    ps_quant_a<G>(raw, c, wave, ah, al, sah, sal);
   }
   const uint32_t boff = (uint32_t)(col * 256 + (((4 * wave + c) ^ col) * 16));
   uint32_t soff[NP];  // this lane's scale byte of group 16p + 4*wave + c, row col
@@ -947,87 +1087,102 @@ __global__ __launch_bounds__(256, NB >= 6 ? 1 : 2) void moe_stream_persist_kerne
     soff[p] = ps_chunk_off<G>(o >> 4, o & 15);
   }
   const uint32_t bofs = ps_chunk_off<G>(G + (col * eb) / 16, ((col * eb) & 15) & ~3);
-  const uint32_t ring0 = lds_addr(ring);
+  const uint32_t ring0 = lds_addr(tring);
 
-  // Per item i: wait for its DMA, barrier, then finish the epilogue of item
-  // i-1 (its partial sums were written before this barrier), read item i's
-  // slot into registers, barrier (the slot is free), refill the slot with
-  // item i+NB, and only then decode and multiply.  Issuing the refill before
-  // the arithmetic keeps the ring as full as possible.
-  int i = 0;
+  // Per step k (one item per team, team item k): wait for its DMA, barrier,
+  // finish the epilogue of item k-1 (its partial sums were written before
+  // this barrier), read item k's slot into registers, barrier (the slot is
+  // free), refill the slot with item k+NB, and only then multiply.  Segments
+  // end where either team's (expert, pass) changes; that team then reloads
+  // its A operands (waiting for everything it has in flight).
+  const int nsteps = half;
+  int k = 0;
   bool pend = false;                    // an item waits for its epilogue
   int p_n = 0, p_rr = 0, p_cnt = 0;     // that item's column, row, rows, first row
   int64_t p_row0 = 0;
   uint32_t p_braw = 0;
   while (true) {
-    // one (expert, pass) group: its remaining slices within this chunk
-    const int run_end = min(n_items, i + (S - ci.s));
-    for (; i < run_end; ++i) {
-      const int slot = i % NB;
+    // steps until the next group change of either team
+    const int mine_left = k < tn ? min(tn - k, S - ci.s) : nsteps - k;
+    int seg_end = k + mine_left;
+    if constexpr (TEAMS == 2) {
+      // (LDS-only barriers: __syncthreads() would also wait for every DMA in flight)
+      if (lane == 0 && wave == 0) sSeg[team] = mine_left;
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      asm volatile("s_barrier" ::: "memory");
+      seg_end = k + min(sSeg[0], sSeg[1]);
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      asm volatile("s_barrier" ::: "memory");
+    }
+    for (; k < seg_end; ++k) {
+      const bool act = k < tn;
+      const int slot = k % NB;
       const uint32_t sb = ring0 + (uint32_t)(slot * C::SLOT);
-      wait_tiles_ahead<NP, NB - 1>(min(NB - 1, n_items - 1 - i));
+      if (act) wait_tiles_ahead<NP, NB - 1>(min(NB - 1, tn - 1 - k));
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's partial sums are written
       asm volatile("s_barrier" ::: "memory");
-      if (pend) ps_epilogue<EPI>(a, sRed, lane, wave, col, p_braw, p_n, p_rr, p_cnt, p_row0);
+      if (pend) ps_epilogue<EPI>(a, tred, lane, wave, col, p_braw, p_n, p_rr, p_cnt, p_row0);
+      pend = false;
 
-      // this lane's codes and scales of its six groups 16p + 4*wave + c
       u32x4_t q[NP];
       uint32_t sc[NP];
-#pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        q[p] = lds_read_b128(sb + p * C::PART + boff);
-        sc[p] = lds_read_u8(sb + soff[p]);
-      }
       uint32_t braw = 0;
-      if (a.bias) braw = lds_read_b32(sb + bofs);
+      if (act) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          q[p] = lds_read_b128(sb + p * C::PART + boff);
+          sc[p] = lds_read_u8(sb + soff[p]);
+        }
+        if (a.bias) braw = lds_read_b32(sb + bofs);
+      }
       asm volatile("s_waitcnt lgkmcnt(0)"
                    : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]), "+v"(q[4]), "+v"(q[5]),
                      "+v"(sc[0]), "+v"(sc[1]), "+v"(sc[2]), "+v"(sc[3]), "+v"(sc[4]), "+v"(sc[5]),
                      "+v"(braw));
       // every wave has its operands (and is done with the partial sums of
-      // item i-1): the slot and the partial-sum buffer are free
+      // the previous item): the slot and the partial-sum buffer are free
       asm volatile("s_barrier" ::: "memory");
-      if (i + NB < n_items) {
-        ps_issue<G>(a, ring + slot * C::SLOT, ii.e, ii.s * 16, wave, lane, eb);
-        ps_next(ii, sHit, S, nhit);
-      }
-
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        if (16 * p + 4 * wave < G) {
-          u32x4_t qq = q[p];
-          uint32_t ss = sc[p];
-          if (16 * p + 4 * wave + c >= G) {
-            qq = u32x4_t{0u, 0u, 0u, 0u};
-            ss = 127u;
-          }
-#pragma unroll
-          for (int m = 0; m < 4; ++m)
-            acc = mfma16(__builtin_bit_cast(s16x8_t, an[p][m]), decode8<true>(qq[m], ss), acc);
+      if (act) {
+        if (k + NB < tn) {
+          ps_issue<G>(a, tring + slot * C::SLOT, ii.e, ii.s * 16, wave, lane, eb);
+          ps_next(ii, sHit, S, nhit);
         }
+        // groups past G meet zero activations (their slots hold scales)
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          if (16 * p + 4 * wave < G) {
+            const i32x8_t bq = i32x8_t{(int)q[p][0], (int)q[p][1], (int)q[p][2], (int)q[p][3], 0, 0, 0, 0};
+            acc = mfma_mx16(ah[p], bq, acc, sah[p >> 2], p & 3, sc[p]);
+            acc = mfma_mx16(al[p], bq, acc, sal[p >> 2], p & 3, sc[p]);
+          }
+        }
+        tred[wave * 64 + lane] = acc;
+        pend = true;
+        p_braw = braw;
+        p_n = ci.s * 16 + col;
+        p_rr = ci.pass * 16 + 4 * c + wave;
+        p_cnt = ci.cnt;
+        p_row0 = row0;
+        ++ci.s;
       }
-      sRed[wave * 64 + lane] = acc;
-      pend = true;
-      p_braw = braw;
-      p_n = ci.s * 16 + col;
-      p_rr = ci.pass * 16 + 4 * c + wave;
-      p_cnt = ci.cnt;
-      p_row0 = row0;
-      ++ci.s;
     }
-    if (i >= n_items) break;
-    // next group: reload the A operands (waits for everything in flight)
-    ci.s = S - 1;
-    ps_next(ci, sHit, S, nhit);
-    row0 = __builtin_amdgcn_readfirstlane(sRow0[ci.h]);
-    ps_load_a<G>(a, row0, ci.cnt, ci.pass, col, c, wave, an);
-    wait_vmcnt<0>();
+    if (k >= nsteps) break;
+    // this team's group changed: reload its A operands
+    if (k < tn && ci.s == S) {
+      ci.s = S - 1;
+      ps_next(ci, sHit, S, nhit);
+      row0 = __builtin_amdgcn_readfirstlane(sRow0[ci.h]);
+      u32x4_t raw[NP][4];
+      ps_load_a_raw<G>(a, row0, ci.cnt, ci.pass, col, c, wave, raw);
+      wait_vmcnt<0>();
+      ps_quant_a<G>(raw, c, wave, ah, al, sah, sal);
+    }
   }
-  // the last item's epilogue
+  // the last items' epilogues
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   asm volatile("s_barrier" ::: "memory");
-  ps_epilogue<EPI>(a, sRed, lane, wave, col, p_braw, p_n, p_rr, p_cnt, p_row0);
+  if (pend) ps_epilogue<EPI>(a, tred, lane, wave, col, p_braw, p_n, p_rr, p_cnt, p_row0);
 }
 
 // Logical tile index of this workgroup for the tiled kernels.  The live
@@ -1469,7 +1624,6 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
 // per CU with a deeper pipeline) split N; each wave computes 128 x 64 (4 x 2
 // blocks of 32 x 32).  Bound: MFMA (FP8 rate, 2x the bf16 rate).
 // ---------------------------------------------------------------------------
-typedef __attribute__((ext_vector_type(8))) int i32x8_t;
 
 constexpr int MX_BM = 128;
 constexpr int MX_BK = 64;
@@ -1823,16 +1977,17 @@ template <int EPI>
 static int launch_gemm(const GemmArgs& a, int path, int64_t P, hipStream_t st) {
   const bool align16 = (reinterpret_cast<uintptr_t>(a.Bq) % 16) == 0;
   const int cus = cu_count();
-  if (path == PATH_STREAM && a.K == 2880 && a.N % 16 == 0 && a.E <= PS_MAX_E && align16 &&
+  if (path == PATH_STREAM && a.K == 2880 && a.N % 16 == 0 && a.E <= 256 * PS_TEAMS && align16 &&
       reinterpret_cast<uintptr_t>(a.Bs) % 16 == 0 && reinterpret_cast<uintptr_t>(a.bias) % 16 == 0 &&
       reinterpret_cast<uintptr_t>(a.A) % 16 == 0 && a.lda % 8 == 0 && P <= (1 << 19) && cus > 0) {
-    // the gpt-oss hidden / intermediate size: PS_WPC persistent workgroups per CU
-    constexpr int ring = PS_NB * PsCfg<90>::SLOT;
-    const void* fn = reinterpret_cast<const void*>(moe_stream_persist_kernel<EPI, 90, PS_NB>);
+    // the gpt-oss hidden / intermediate size: persistent workgroups, 512
+    // threads per CU
+    constexpr int ring = PS_TEAMS * PS_TEAM_NB * PsCfg<90>::SLOT;
+    const void* fn = reinterpret_cast<const void*>(moe_stream_persist_kernel<EPI, 90, PS_TEAMS>);
     int rc = allow_big_lds(fn, 6, EPI, ring);
     if (rc) return rc;
-    hipLaunchKernelGGL((moe_stream_persist_kernel<EPI, 90, PS_NB>), dim3((unsigned)(cus * PS_WPC)), dim3(256),
-                       ring, st, a);
+    hipLaunchKernelGGL((moe_stream_persist_kernel<EPI, 90, PS_TEAMS>), dim3((unsigned)(cus * (3 - PS_TEAMS))),
+                       dim3(256 * PS_TEAMS), ring, st, a);
   } else if (path == PATH_STREAM && a.K == 2880 && a.N % ST_BN == 0 && align16 &&
              reinterpret_cast<uintptr_t>(a.Bs) % 16 == 0) {
     // the gpt-oss hidden / intermediate size: the part-pipelined kernel

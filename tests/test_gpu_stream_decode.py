@@ -1,11 +1,15 @@
 """Decode weight-streaming kernels on the gpt-oss shape (K = 2880).
 
-The persistent kernel (one workgroup per CU walking (expert, pass, slice)
-items through an LDS ring) and the one-workgroup-per-slice part kernel split
-K the same way and add the partial sums in the same order, so their outputs
-must agree bit for bit.  A bias view that is only 2-byte aligned sends the
-same call to the part kernel (the persistent kernel DMAs the bias and needs
-4-byte alignment); everything else is identical.
+The persistent kernel (persistent workgroups walking (expert, pass, slice)
+items through LDS DMA rings) multiplies the packed MXFP4 weights on the
+block-scaled MFMA with the activations split into two MXFP8 terms (hi + lo,
+exact to 2^-21 of each 32-element block's maximum).  The part kernel decodes
+the weights to bf16 and multiplies on the bf16 MFMA.  Both approximate the
+same float32 product; they are compared with each other (relative L2 <= 2e-3,
+the difference being the bf16 roundings of the two) and with the oracle at
+the layer bar.  A bias view that is only 2-byte aligned sends the same call to
+the part kernel (the persistent kernel DMAs the bias and needs 16-byte
+alignment).
 """
 
 from __future__ import annotations
@@ -16,7 +20,16 @@ import torch
 import oracle
 from blockstreamer_amd import kernels, synthetic
 from tests.conftest import announce
-from tests.moe_util import assert_layer_close, expert_args, oracle_tokens
+from tests.moe_util import assert_layer_close, errors, expert_args, oracle_tokens
+
+KERNEL_AGREEMENT = 2e-3
+
+
+def _agree(persist, parts, what):
+    rel_l2, max_abs, scale = errors(persist, parts)
+    msg = f"{what}: persistent vs part kernel rel_l2={rel_l2:.3e} max_abs={max_abs:.3e} (|max| {scale:.3e})"
+    print(msg)
+    assert rel_l2 <= KERNEL_AGREEMENT, msg
 
 pytestmark = pytest.mark.gpu
 
@@ -26,7 +39,7 @@ def _shifted(x: torch.Tensor) -> torch.Tensor:
     buf = torch.empty(x.numel() + 1, dtype=x.dtype, device=x.device)
     buf[1:] = x.reshape(-1)
     v = buf[1:].view(x.shape)
-    assert v.data_ptr() % 4 == 2
+    assert v.data_ptr() % 16 == 2
     return v
 
 
@@ -48,7 +61,10 @@ def test_persistent_equals_part_kernel(device, T):
     _, w, idx = kernels.router_forward(t["hidden"], t["router_weight"], t["router_bias"], 4)
     announce(f"persistent vs part kernel T={T}")
     persist, parts = _both_kernels(t, idx, w)
-    assert torch.equal(persist.view(torch.int16), parts.view(torch.int16))
+    _agree(persist, parts, f"T={T}")
+    tokens = torch.arange(min(T, 6))
+    want = oracle_tokens(t, idx.cpu(), w.cpu(), tokens)
+    assert_layer_close(persist.cpu()[tokens], want, f"persistent T={T}")
 
 
 def test_persistent_multi_pass_expert(device):
@@ -65,7 +81,7 @@ def test_persistent_multi_pass_expert(device):
     assert int((idx == hot).sum()) == 40
     announce("persistent kernel, 40-row expert")
     persist, parts = _both_kernels(t, idx, w)
-    assert torch.equal(persist.view(torch.int16), parts.view(torch.int16))
+    _agree(persist, parts, "40-row expert")
     tokens = torch.tensor([0, 17, 39, 40, 47])
     want = oracle_tokens(t, idx.cpu(), w.cpu(), tokens)
     assert_layer_close(persist.cpu()[tokens], want, "40-row expert", absolute=True)
@@ -93,7 +109,7 @@ def test_persistent_single_expert_most_workgroups_idle(device):
     w = torch.ones(1, 1, dtype=torch.bfloat16, device=device)
     announce("persistent kernel, one token one expert")
     persist, parts = _both_kernels(t, idx, w)
-    assert torch.equal(persist.view(torch.int16), parts.view(torch.int16))
+    _agree(persist, parts, "one token one expert")
     want = oracle.experts_ref(t["hidden"].cpu(), idx.cpu(), w.cpu().float(),
                               *[a.cpu() for a in expert_args(t)])
     assert_layer_close(persist, want, "one token one expert", absolute=True)
