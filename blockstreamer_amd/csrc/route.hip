@@ -50,28 +50,29 @@ __global__ __launch_bounds__(DISPATCH_THREADS) void moe_dispatch_kernel(
   }
   __syncthreads();
 
-  // 2. exclusive scans of counts and of tile counts (E <= 1024 = one entry per thread)
+  // 2. inclusive scans of counts and of tile counts (E <= 1024 = one entry
+  //    per thread): a shuffle scan within each wave, then the wave totals
   const int my_cnt = tid < E ? s_cnt[tid] : 0;
   const int my_tiles = (my_cnt + BM - 1) / BM;
-  s_scan[tid] = my_cnt;
-  __syncthreads();
-  for (int off = 1; off < DISPATCH_THREADS; off <<= 1) {
-    const int v = tid >= off ? s_scan[tid - off] : 0;
-    __syncthreads();
-    s_scan[tid] += v;
-    __syncthreads();
+  int incl_rows = my_cnt, incl_tiles = my_tiles;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int a = __shfl_up(incl_rows, off);
+    const int b = __shfl_up(incl_tiles, off);
+    if (lane >= off) {
+      incl_rows += a;
+      incl_tiles += b;
+    }
   }
-  const int incl_rows = s_scan[tid];
-  __syncthreads();
-  s_scan[tid] = my_tiles;
-  __syncthreads();
-  for (int off = 1; off < DISPATCH_THREADS; off <<= 1) {
-    const int v = tid >= off ? s_scan[tid - off] : 0;
-    __syncthreads();
-    s_scan[tid] += v;
-    __syncthreads();
+  if (lane == 63) {
+    s_scan[wave] = incl_rows;
+    s_scan[DISPATCH_WAVES + wave] = incl_tiles;
   }
-  const int incl_tiles = s_scan[tid];
+  __syncthreads();
+  for (int w = 0; w < wave; ++w) {
+    incl_rows += s_scan[w];
+    incl_tiles += s_scan[DISPATCH_WAVES + w];
+  }
   if (tid < E) {
     const int start = incl_rows - my_cnt;
     s_off[tid] = start;

@@ -100,19 +100,21 @@ __device__ void topk_softmax_wave(const float* row, int E, int k, int lane, int 
   }
 }
 
-// bf16 logits tile: RT*16 tokens x RE*16 experts per workgroup.  The four
-// waves split the hidden dimension (wave w takes k-steps w, w+4, ...); their
+// bf16 logits tile: RT*16 tokens x RE*16 experts per workgroup.  The W
+// waves split the hidden dimension (wave w takes k-steps w, w+W, ...); their
 // float32 partial sums are added in wave order (deterministic), the bias is
-// added in float32 and the result rounded once to bf16.  Tiles are ordered
+// added in float32 and the result rounded once to bf16.  Small batches use
+// W = 16, so that each wave's loads of the whole hidden dimension are in
+// flight at once (few tiles, one round trip).  Tiles are ordered
 // so that all expert tiles of one token tile run on one XCD (the token rows
 // are then fetched from HBM once into that XCD's L2).
-template <int RT, int RE>
-__global__ __launch_bounds__(256) void logits_bf16_kernel(const uint16_t* __restrict__ hidden,
+template <int RT, int RE, int W>
+__global__ __launch_bounds__(64 * W) void logits_bf16_kernel(const uint16_t* __restrict__ hidden,
                                                           const uint16_t* __restrict__ weight,
                                                           const uint16_t* __restrict__ bias,
                                                           int T, int H, int E,
                                                           uint16_t* __restrict__ logits) {
-  __shared__ float s_part[3][RT][RE][4][64];
+  __shared__ float s_part[W - 1][RT][RE][4][64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -145,11 +147,11 @@ __global__ __launch_bounds__(256) void logits_bf16_kernel(const uint16_t* __rest
     for (int j = 0; j < RE; ++j) acc[r][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // D k-steps per round: all loads of a round are issued before its MFMAs
   constexpr int D = RT * RE == 1 ? 8 : 4;
-  for (int base = wave; base < nks; base += 4 * D) {
+  for (int base = wave; base < nks; base += W * D) {
     rs16x8_t av[D][RT], bv[D][RE];
 #pragma unroll
     for (int u = 0; u < D; ++u) {
-      const int ks = min(base + 4 * u, nks - 1);
+      const int ks = min(base + W * u, nks - 1);
 #pragma unroll
       for (int r = 0; r < RT; ++r) av[u][r] = *reinterpret_cast<const rs16x8_t*>(arow[r] + ks * 32);
 #pragma unroll
@@ -160,7 +162,7 @@ __global__ __launch_bounds__(256) void logits_bf16_kernel(const uint16_t* __rest
     }
 #pragma unroll
     for (int u = 0; u < D; ++u) {
-      if (base + 4 * u >= nks) break;
+      if (base + W * u >= nks) break;
 #pragma unroll
       for (int r = 0; r < RT; ++r)
 #pragma unroll
@@ -192,9 +194,8 @@ __global__ __launch_bounds__(256) void logits_bf16_kernel(const uint16_t* __rest
       for (int i = 0; i < 4; ++i) {
         const int t = t0 + r * 16 + 4 * lk + i;
         float v = acc[r][j][i];
-        v += s_part[0][r][j][i][lane];
-        v += s_part[1][r][j][i][lane];
-        v += s_part[2][r][j][i][lane];
+#pragma unroll
+        for (int w = 0; w < W - 1; ++w) v += s_part[w][r][j][i][lane];
         if (t < T) logits[(int64_t)t * E + e] = (uint16_t)f32_to_bf16_bits(v + bv);
       }
   }
@@ -271,13 +272,13 @@ extern "C" int bsa_router_fwd(const void* hidden, int dtype, int64_t T, int64_t 
     // logits tiles, then top-k + softmax from the (L2-resident) logits
     if (T >= 4096) {
       const int64_t nblk = ((T + 31) / 32) * ((E + 31) / 32);
-      hipLaunchKernelGGL((logits_bf16_kernel<2, 2>), dim3((unsigned)nblk), dim3(256), 0, st,
+      hipLaunchKernelGGL((logits_bf16_kernel<2, 2, 4>), dim3((unsigned)nblk), dim3(256), 0, st,
                          static_cast<const uint16_t*>(hidden), static_cast<const uint16_t*>(weight),
                          static_cast<const uint16_t*>(bias), (int)T, (int)H, (int)E,
                          static_cast<uint16_t*>(logits));
     } else {
       const int64_t nblk = ((T + 15) / 16) * ((E + 15) / 16);
-      hipLaunchKernelGGL((logits_bf16_kernel<1, 1>), dim3((unsigned)nblk), dim3(256), 0, st,
+      hipLaunchKernelGGL((logits_bf16_kernel<1, 1, 16>), dim3((unsigned)nblk), dim3(1024), 0, st,
                          static_cast<const uint16_t*>(hidden), static_cast<const uint16_t*>(weight),
                          static_cast<const uint16_t*>(bias), (int)T, (int)H, (int)E,
                          static_cast<uint16_t*>(logits));
