@@ -183,14 +183,31 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
   }
   const int64_t obase = (int64_t)t * H;
   if ((H & 3) == 0) {
-    for (int h = threadIdx.x * 4; h < H; h += blockDim.x * 4) {
+    // blockIdx.y selects a slice of 4 * blockDim.x columns
+    for (int h = (blockIdx.y * blockDim.x + threadIdx.x) * 4; h < H; h += gridDim.y * blockDim.x * 4) {
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int j = 0; j < n; ++j) {
-        const float4 y = *reinterpret_cast<const float4*>(Y + (int64_t)pos[j] * H + h);
-        acc.x += wt[j] * y.x;
-        acc.y += wt[j] * y.y;
-        acc.z += wt[j] * y.z;
-        acc.w += wt[j] * y.w;
+      if (n <= 4) {
+        // the common top-k: all rows' loads in flight together
+        float4 y[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (j < n) y[j] = *reinterpret_cast<const float4*>(Y + (int64_t)pos[j] * H + h);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (j < n) {
+            acc.x += wt[j] * y[j].x;
+            acc.y += wt[j] * y[j].y;
+            acc.z += wt[j] * y[j].z;
+            acc.w += wt[j] * y[j].w;
+          }
+      } else {
+        for (int j = 0; j < n; ++j) {
+          const float4 y = *reinterpret_cast<const float4*>(Y + (int64_t)pos[j] * H + h);
+          acc.x += wt[j] * y.x;
+          acc.y += wt[j] * y.y;
+          acc.z += wt[j] * y.z;
+          acc.w += wt[j] * y.w;
+        }
       }
       if (out_dtype == DT_BF16) {
         uint2 v = make_uint2(pack_bf16x2(acc.x, acc.y), pack_bf16x2(acc.z, acc.w));
@@ -203,7 +220,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
       }
     }
   } else {
-    for (int h = threadIdx.x; h < H; h += blockDim.x) {
+    for (int h = blockIdx.y * blockDim.x + threadIdx.x; h < H; h += gridDim.y * blockDim.x) {
       float acc = 0.f;
       for (int j = 0; j < n; ++j) acc += wt[j] * Y[(int64_t)pos[j] * H + h];
       store_f32_as(out, obase + h, acc, out_dtype);
@@ -261,8 +278,12 @@ int launch_combine(const float* Y, const int64_t* idx, const void* w, int w_dtyp
                    const int* pair_pos, int T, int k, int H, void* out, int out_dtype,
                    hipStream_t st) {
   if (T == 0) return BSA_OK;
-  hipLaunchKernelGGL(moe_combine_kernel, dim3(T), dim3(256), 0, st, Y, idx, w, w_dtype, pair_pos,
-                     T, k, H, out, out_dtype);
+  // small batches: several workgroups per token (more loads in flight)
+  int slices = (H + 1023) / 1024;
+  if (slices > 4) slices = 4;
+  if (T >= 1024) slices = 1;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T, (unsigned)slices), dim3(256), 0, st, Y, idx, w,
+                     w_dtype, pair_pos, T, k, H, out, out_dtype);
   BSA_LAUNCH_CHECK("combine launch");
   return BSA_OK;
 }
