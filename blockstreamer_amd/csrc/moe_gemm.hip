@@ -1901,7 +1901,8 @@ static int allow_big_lds(const void* fn, int kind, int epi, int bytes = 160 * 10
     set_error("no current HIP device");
     return BSA_EHIP;
   }
-  static bool allowed[64][8][4];
+  // kinds: 4-5 tiled kernel, 6 persistent decode kernel, 8-15 MX kernel configurations
+  static bool allowed[64][16][4];
   if (!allowed[dev][kind][epi]) {
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
       set_error("cannot allow %d bytes of dynamic LDS for a GEMM kernel", bytes);
@@ -1925,7 +1926,7 @@ static int launch_mx_cfg(const GemmArgs& a, int64_t P, size_t smem, hipStream_t 
   const bool sb16 = reinterpret_cast<uintptr_t>(a.Bs) % 16 == 0;
   const void* fn = sb16 ? reinterpret_cast<const void*>(moe_mx_kernel<EPI, NS, true, WN, NBW>)
                         : reinterpret_cast<const void*>(moe_mx_kernel<EPI, NS, false, WN, NBW>);
-  int rc = allow_big_lds(fn, (NBW == 4 ? 2 : 0) + (sb16 ? 1 : 0), EPI);
+  int rc = allow_big_lds(fn, 8 + (WN == 8 ? 4 : 0) + (NBW == 4 ? 2 : 0) + (sb16 ? 1 : 0), EPI);
   if (rc) return rc;
   if (sb16)
     hipLaunchKernelGGL((moe_mx_kernel<EPI, NS, true, WN, NBW>), dim3((unsigned)grid), dim3(64 * WN), smem,
