@@ -1698,6 +1698,7 @@ __global__ __launch_bounds__(64 * WN, NBW == 2 ? 2 : 1) void moe_mx_kernel(GemmA
   const int e = te.x;
   const int m0 = te.y;
   const int rows = min(MX_BM, a.offsets[e] + a.counts[e] - m0);
+  const int mbn = __builtin_amdgcn_readfirstlane((rows + 31) >> 5);  // 32-row blocks with rows
   const int n0 = nt * BN;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1801,6 +1802,7 @@ __global__ __launch_bounds__(64 * WN, NBW == 2 ? 2 : 1) void moe_mx_kernel(GemmA
     }
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
+      if (mb >= mbn) continue;  // row block past the tile's valid rows
       const uint8_t* ar = st + mb * 32 * 64;
       const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(ar + aoff0);
       const u32x4_t w1 = *reinterpret_cast<const u32x4_t*>(ar + aoff1);
