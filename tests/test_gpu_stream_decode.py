@@ -113,3 +113,26 @@ def test_persistent_single_expert_most_workgroups_idle(device):
     want = oracle.experts_ref(t["hidden"].cpu(), idx.cpu(), w.cpu().float(),
                               *[a.cpu() for a in expert_args(t)])
     assert_layer_close(persist, want, "one token one expert", absolute=True)
+
+
+@pytest.mark.parametrize("bias", ["f16", "none"])
+def test_persistent_f16_or_no_bias_vs_oracle(device, bias):
+    T = 24
+    shape = synthetic.MoEShape(128, 4, 2880, 2880, T)
+    t = synthetic.moe_layer(shape, seed=51, scale_lo=116, scale_hi=120, device=device)
+    idx, w = synthetic.random_routing(T, 128, 4, seed=52, device=device)
+    args = list(expert_args(t))
+    if bias == "f16":
+        args[2] = args[2].half()
+        args[5] = args[5].half()
+        ref_args = [a.cpu() for a in args]
+    else:
+        ref_args = [a.cpu() for a in args]
+        ref_args[2] = torch.zeros_like(ref_args[2])
+        ref_args[5] = torch.zeros_like(ref_args[5])
+        args[2] = None
+        args[5] = None
+    announce(f"persistent kernel, bias {bias}")
+    got = kernels.moe_experts_forward(t["hidden"], idx, w, *args, path="stream")
+    want = oracle.experts_ref(t["hidden"].cpu(), idx.cpu(), w.cpu().float(), *ref_args)
+    assert_layer_close(got, want, f"bias {bias}", absolute=True)
