@@ -790,18 +790,20 @@ __device__ __forceinline__ void ps_issue(const GemmArgs& a, uint8_t* sb, int e, 
 
 // Activations as two MXFP8 terms.  A bf16 block x (32 values sharing one
 // E8M0 scale) is written hi + lo with
-//   hi = E4M3(x / 2^X),            X  = ceil(log2(amax|x| / 448)),
-//   lo = E4M3((x - hi*2^X) / 2^Y),  Y  = ceil(log2(amax|residual| / 448)),
+//   hi = E4M3(x / 2^X),              X = ceil(log2(amax|x| / 448)),
+//   lo = E4M3((x - hi*2^X) / 2^(X-4)),
 // both rounded to nearest even (v_cvt_scalef32_pk_fp8_f32 divides by the
-// scale).  A bf16 value has 8 significant bits and E4M3 4, so the residual of
-// every element within 2^17 of the block maximum is exact in E4M3: hi*2^X +
-// lo*2^Y equals x except for elements below 2^-17 of the block maximum, whose
-// error is below 2^-21 of it.  The packed MXFP4 weights then go to the
-// block-scaled MFMA as they are, two instructions (hi, lo) per 128 k.
+// scale).  Every x/2^X is at most 448, where E4M3 steps are at most 32, so
+// the residual is at most 16 * 2^X and lo at most 256: nothing saturates.  A
+// bf16 value has 8 significant bits and E4M3 4, and E4M3 keeps 4 bits down to
+// 2^-6: hi*2^X + lo*2^(X-4) equals x for every element above 2^-14 of the
+// block maximum, and misses smaller ones by less than 2^-22 of it.  The
+// packed MXFP4 weights then go to the block-scaled MFMA as they are, two
+// instructions (hi, lo) per 128 k.
 //
 // 16 values of one lane (two u32x4 of bf16) -> 16 hi and 16 lo codes; the
 // block is completed by the partner lane 16 lanes away (lane group c ^ 1).
-// Scale bytes are returned as E8M0 (X + 127, Y + 127).
+// The hi scale byte (E8M0, X + 127) is returned; lo's is 4 less.
 __device__ __forceinline__ int mx_block_exp(float amax) {
   const uint32_t ab = __float_as_uint(amax);
   const int e = (int)(ab >> 23) - 127;
@@ -811,7 +813,7 @@ __device__ __forceinline__ int mx_block_exp(float amax) {
 }
 
 __device__ __forceinline__ void mx_split16(const u32x4_t& v0, const u32x4_t& v1, bool valid, u32x4_t& hi,
-                                           u32x4_t& lo, uint32_t& sh, uint32_t& sl) {
+                                           u32x4_t& lo, uint32_t& sh) {
   float f[16];
 #pragma unroll
   for (int d = 0; d < 8; ++d) {
@@ -842,12 +844,9 @@ __device__ __forceinline__ void mx_split16(const u32x4_t& v0, const u32x4_t& v1,
     r[4 * d + 2] = f[4 * d + 2] - d1[0];
     r[4 * d + 3] = f[4 * d + 3] - d1[1];
   }
-  float rmax = 0.f;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) rmax = fmaxf(rmax, fabsf(r[j]));
-  rmax = fmaxf(rmax, __shfl_xor(rmax, 16));
-  const int Y = mx_block_exp(rmax);
-  const float sr = __uint_as_float((uint32_t)(Y + 127) << 23);
+  // 2^(X-4); X >= -126, so for X < -122 the float is subnormal-free only
+  // down to 2^-126: clamp (such blocks hold values below 2^-118)
+  const float sr = __uint_as_float((uint32_t)max(X + 123, 1) << 23);
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
     typedef short v2s __attribute__((ext_vector_type(2)));
@@ -857,7 +856,6 @@ __device__ __forceinline__ void mx_split16(const u32x4_t& v0, const u32x4_t& v1,
     lo[d] = __builtin_bit_cast(uint32_t, q);
   }
   sh = (uint32_t)(X + 127);
-  sl = (uint32_t)(Y + 127);
 }
 
 // v_mfma_scale_f32_16x16x128_f8f6f4 with E4M3 A, E2M1 B; the A scale is byte
@@ -911,18 +909,18 @@ __device__ __forceinline__ void ps_quant_a(const u32x4_t (&raw)[PsCfg<G>::NP][4]
   for (int p = 0; p < NP; ++p) {
     const int gw = 16 * p + 4 * wave;
     u32x4_t h0, l0, h1, l1;
-    uint32_t xh0, xl0, xh1, xl1;
-    mx_split16(raw[p][0], raw[p][1], gw + (c >> 1) < G, h0, l0, xh0, xl0);
-    mx_split16(raw[p][2], raw[p][3], gw + 2 + (c >> 1) < G, h1, l1, xh1, xl1);
+    uint32_t xh0, xh1;
+    mx_split16(raw[p][0], raw[p][1], gw + (c >> 1) < G, h0, l0, xh0);
+    mx_split16(raw[p][2], raw[p][3], gw + 2 + (c >> 1) < G, h1, l1, xh1);
     ah[p] = i32x8_t{(int)h0[0], (int)h0[1], (int)h0[2], (int)h0[3], (int)h1[0], (int)h1[1], (int)h1[2], (int)h1[3]};
     al[p] = i32x8_t{(int)l0[0], (int)l0[1], (int)l0[2], (int)l0[3], (int)l1[0], (int)l1[1], (int)l1[2], (int)l1[3]};
     // lane group c must supply the scale of window block c: groups 0 and 3
     // hold it (blocks 0 and 3 are their first / second halves), groups 1 and
     // 2 trade (block 1 is group 2's first half, block 2 group 1's second)
-    const uint32_t offer_h = c == 1 ? xh1 : xh0, offer_l = c == 1 ? xl1 : xl0;
-    const uint32_t got_h = __shfl_xor(offer_h, 48), got_l = __shfl_xor(offer_l, 48);
+    const uint32_t offer_h = c == 1 ? xh1 : xh0;
+    const uint32_t got_h = __shfl_xor(offer_h, 48);
     const uint32_t bh = c == 0 ? xh0 : (c == 3 ? xh1 : got_h);
-    const uint32_t bl = c == 0 ? xl0 : (c == 3 ? xl1 : got_l);
+    const uint32_t bl = bh > 4u ? bh - 4u : 1u;   // lo scale 2^(X-4), as in mx_split16
     sh[p >> 2] |= bh << (8 * (p & 3));
     sl[p >> 2] |= bl << (8 * (p & 3));
   }
@@ -1012,21 +1010,28 @@ __global__ __launch_bounds__(256 * TEAMS, 3 - TEAMS) void moe_stream_persist_ker
   const int cnt_t = tid < a.E ? a.counts[tid] : 0;
   const int off_t = tid < a.E ? a.offsets[tid] : 0;
   const int mine = (cnt_t > 0 ? 1 : 0) | (((cnt_t + 15) >> 4) << 16);
-  sScan[tid] = mine;
-  __syncthreads();
-  for (int d = 1; d < NT; d <<= 1) {
-    const int v = tid >= d ? sScan[tid - d] : 0;
-    __syncthreads();
-    sScan[tid] += v;
-    __syncthreads();
+  // inclusive scan: shuffles within each wave, then the wave totals
+  int incl = mine;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int v = __shfl_up(incl, off);
+    if (lane >= off) incl += v;
   }
-  const int excl = sScan[tid] - mine;
+  if (lane == 63) sScan[tid >> 6] = incl;
+  __syncthreads();
+  int last = 0;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) {
+    const int v = sScan[w];
+    if (w < (tid >> 6)) incl += v;
+    last += v;
+  }
+  const int excl = incl - mine;
   if (cnt_t > 0) {
     sHit[excl & 0xFFFF] = tid | (cnt_t << 10);
     sHPre[excl & 0xFFFF] = excl >> 16;
     sRow0[excl & 0xFFFF] = off_t;
   }
-  const int last = sScan[NT - 1];
   const int nhit = last & 0xFFFF;
   const int total = (last >> 16) * S;
   const int chunk = (total + (int)gridDim.x - 1) / (int)gridDim.x;

@@ -3,7 +3,7 @@
 The persistent kernel (persistent workgroups walking (expert, pass, slice)
 items through LDS DMA rings) multiplies the packed MXFP4 weights on the
 block-scaled MFMA with the activations split into two MXFP8 terms (hi + lo,
-exact to 2^-21 of each 32-element block's maximum).  The part kernel decodes
+exact for every element above 2^-14 of its 32-element block's maximum).  The part kernel decodes
 the weights to bf16 and multiplies on the bf16 MFMA.  Both approximate the
 same float32 product; they are compared with each other (relative L2 <= 2e-3,
 the difference being the bf16 roundings of the two) and with the oracle at
