@@ -1879,10 +1879,166 @@ static Workspace carve(void* base, int64_t T, int64_t H, int64_t I, int64_t E, i
   return w;
 }
 
-// Grouped GEMM with a dense bf16 B [E][N][K] (K % 64 == 0): the backward
-// products with transposed weights, fed by the dequant kernel's [K, N] output.
+// ---------------------------------------------------------------------------
+// Dense-B tiled kernel (the backward's transposed-weight GEMMs): A bf16 rows
+// in expert-sorted order, B dense bf16 [E][N][K] (weight row n, k
+// contiguous), as the dequantisation writes them.  Tile 128 rows x 256
+// weight rows, BK = 64, two LDS stages filled only by global_load_lds DMA
+// (A and B rows of 128 bytes, 16-byte chunk c of row r at chunk c ^ (r & 7),
+// so the fragment reads are bank-conflict free).  Eight waves, each 64 x 64
+// (2 x 2 blocks of v_mfma_f32_32x32x16_bf16), one workgroup per CU.
+// ---------------------------------------------------------------------------
+constexpr int D2_BM = 128;
+constexpr int D2_BN = 256;
+constexpr int D2_BK = 64;
+constexpr int D2_A_BYTES = D2_BM * D2_BK * 2;   // 16 KiB
+constexpr int D2_B_BYTES = D2_BN * D2_BK * 2;   // 32 KiB
+constexpr int D2_STAGE = D2_A_BYTES + D2_B_BYTES;
+constexpr int D2_NS = 3;
+constexpr int D2_DMA_PER_TILE = 2 + 4;          // per wave: A, B
+
+// One stage's DMA of the dense-B kernel (k-tile kt).  A device function, not
+// a lambda: HIP-Clang does not emit the host-side handle of a kernel template
+// whose body calls a capturing lambda.
+__device__ __forceinline__ void d2_issue(uint8_t* smem, int kt, int wave, const uint16_t* const* asrc,
+                                         const uint16_t* const* bsrc) {
+  uint8_t* st = smem + (kt % D2_NS) * D2_STAGE;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    __builtin_amdgcn_global_load_lds(asrc[j] + kt * D2_BK, (lds_void*)(st + (2 * wave + j) * 1024), 16, 0, 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    __builtin_amdgcn_global_load_lds(bsrc[j] + kt * D2_BK, (lds_void*)(st + D2_A_BYTES + (4 * wave + j) * 1024),
+                                     16, 0, 0);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(512, 1) void moe_dense2_kernel(GemmArgs a) {
+  extern __shared__ __align__(1024) uint8_t smem[];  // D2_NS stages
+  const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
+  if (L < 0) return;
+  const int tile = L / a.n_tiles_n;
+  const int nt = L - tile * a.n_tiles_n;
+  const int2 te = a.tiles[tile];
+  const int e = te.x;
+  const int m0 = te.y;
+  const int rows = min(D2_BM, a.offsets[e] + a.counts[e] - m0);
+  const int n0 = nt * D2_BN;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 2;   // rows 64*wm .. +64
+  const int wn = wave & 3;    // weight rows 64*wn .. +64
+  const int KT = a.K / D2_BK;
+  const int l32 = lane & 31;
+  const int lh = lane >> 5;
+
+  // --- DMA sources: instruction j of wave w covers rows 8*(.) .. +7, eight
+  //     lanes per 128-byte row; past-the-tile rows read a valid row ----------
+  const uint16_t* asrc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = 8 * (2 * wave + j) + (lane >> 3);
+    const int ch = (lane & 7) ^ (r & 7);
+    asrc[j] = a.A + tile_src_row(a, m0, rows, r) * a.lda + ch * 8;
+  }
+  const uint16_t* bsrc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int q = 8 * (4 * wave + j) + (lane >> 3);
+    const int ch = (lane & 7) ^ (q & 7);
+    const int n = n0 + q < a.N ? n0 + q : n0;
+    bsrc[j] = a.Bd + ((int64_t)e * a.N + n) * a.K + ch * 8;
+  }
+
+  // fragment offsets: step s (16 k) reads chunk 2s + lh of the lane's row
+  uint32_t aoff[2][4], boff[2][4];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int r = 64 * wm + 32 * b + l32;
+    const int q = 64 * wn + 32 * b + l32;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      aoff[b][s] = (uint32_t)(r * 128 + (((2 * s + lh) ^ (r & 7)) * 16));
+      boff[b][s] = (uint32_t)(D2_A_BYTES + q * 128 + (((2 * s + lh) ^ (q & 7)) * 16));
+    }
+  }
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  for (int i = 0; i < D2_NS - 1; ++i)
+    if (i < KT) d2_issue(smem, i, wave, asrc, bsrc);
+  for (int kt = 0; kt < KT; ++kt) {
+    // tile kt has landed once at most the tiles issued after it are in
+    // flight; a bare s_barrier (a __syncthreads() fence would wait for them too)
+    wait_tiles_ahead<D2_DMA_PER_TILE, D2_NS - 2>(min(D2_NS - 2, KT - 1 - kt));
+    asm volatile("s_barrier" ::: "memory");
+    if (kt + D2_NS - 1 < KT) d2_issue(smem, kt + D2_NS - 1, wave, asrc, bsrc);
+    const uint8_t* st = smem + (kt % D2_NS) * D2_STAGE;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      s16x8_t af[2], bf[2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        af[b] = *reinterpret_cast<const s16x8_t*>(st + aoff[b][s]);
+        bf[b] = *reinterpret_cast<const s16x8_t*>(st + boff[b][s]);
+      }
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = mfma32(af[mb], bf[nb], acc[mb][nb]);
+    }
+    // the stage refilled at the next iteration's issue() is this one: every
+    // wave's reads of it are done before that iteration's barrier
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  }
+
+  // epilogue: lane holds column l32 of each 32x32 block, rows 8*(v/4) + 4*lh + v%4
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int n = n0 + 64 * wn + 32 * nb + l32;
+      if (n >= a.N) continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = 64 * wm + 32 * mb + 8 * (v >> 2) + 4 * lh + (v & 3);
+        if (r < rows) epilogue_one<EPI>(a, m0 + r, n, acc[mb][nb][v], 0.f);
+      }
+    }
+}
+
+static int allow_big_lds(const void* fn, int kind, int epi, int bytes);
+
+// Grouped GEMM with a dense bf16 B [E][N][K]: the backward products with
+// transposed weights, fed by the dequant kernel's [K, N] output.  The dense-B
+// kernel needs K % 64 == 0 and 16-byte aligned rows; other shapes take the
+// tiled kernel.
 template <int EPI>
 static int launch_gemm_dense(const GemmArgs& a, int64_t P, hipStream_t st) {
+  if (a.K % D2_BK == 0 && reinterpret_cast<uintptr_t>(a.A) % 16 == 0 && a.lda % 8 == 0 &&
+      reinterpret_cast<uintptr_t>(a.Bd) % 16 == 0) {
+    GemmArgs b = a;
+    b.n_tiles_n = (a.N + D2_BN - 1) / D2_BN;
+    const int64_t max_tiles = (P + D2_BM - 1) / D2_BM + a.E;
+    const int64_t grid = align_up(max_tiles * b.n_tiles_n, 8);
+    if (grid > INT32_MAX) {
+      set_error("dense grouped GEMM: grid too large");
+      return BSA_EINVAL;
+    }
+    const size_t smem = (size_t)D2_NS * D2_STAGE;
+    int rc = allow_big_lds(reinterpret_cast<const void*>(moe_dense2_kernel<EPI>), 7, EPI, (int)smem);
+    if (rc) return rc;
+    hipLaunchKernelGGL((moe_dense2_kernel<EPI>), dim3((unsigned)grid), dim3(512), smem, st, b);
+    BSA_LAUNCH_CHECK("dense grouped GEMM launch");
+    return BSA_OK;
+  }
   const int64_t max_tiles = (P + TL_BM - 1) / TL_BM + a.E;
   const int64_t grid = align_up(max_tiles * a.n_tiles_n, 8);
   if (grid > INT32_MAX) {
@@ -1908,7 +2064,8 @@ static int allow_big_lds(const void* fn, int kind, int epi, int bytes = 160 * 10
     set_error("no current HIP device");
     return BSA_EHIP;
   }
-  // kinds: 4-5 tiled kernel, 6 persistent decode kernel, 8-15 MX kernel configurations
+  // kinds: 4-5 tiled kernel, 6 persistent decode kernel, 7 dense-B kernel,
+  // 8-15 MX kernel configurations
   static bool allowed[64][16][4];
   if (!allowed[dev][kind][epi]) {
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
