@@ -87,12 +87,10 @@ template <int OUT, bool ALIGN16>
 __global__ __launch_bounds__(256) void dequant_vec_kernel(const uint8_t* __restrict__ blocks,
                                                           const uint8_t* __restrict__ scales,
                                                           void* __restrict__ out, int R, int G,
-                                                          int row_tiles, int mode,
-                                                          const int* __restrict__ expert_rows) {
+                                                          int row_tiles, int mode) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int e = blockIdx.x / row_tiles;
-  if (expert_rows && expert_rows[e] == 0) return;  // expert not routed to: skip
   const int rt = blockIdx.x - e * row_tiles;
   const int r = rt * DQ_ROWS + 8 * (lane % DQ_ROWG);
   const int K = G * 32;
@@ -174,8 +172,7 @@ __global__ __launch_bounds__(256) void dequant_generic_kernel(const uint8_t* __r
 
 template <int OUT>
 static int launch_dequant(const uint8_t* blocks, const uint8_t* scales, void* out, int64_t E,
-                          int64_t R, int64_t G, int mode, hipStream_t stream,
-                          const int* expert_rows = nullptr) {
+                          int64_t R, int64_t G, int mode, hipStream_t stream) {
   const uintptr_t bp = reinterpret_cast<uintptr_t>(blocks);
   const uintptr_t op = reinterpret_cast<uintptr_t>(out);
   // The vectorised kernel decodes in whichever way `mode` asks (mode 1 makes
@@ -191,10 +188,10 @@ static int launch_dequant(const uint8_t* blocks, const uint8_t* scales, void* ou
     }
     if (bp % 16 == 0)
       hipLaunchKernelGGL((dequant_vec_kernel<OUT, true>), dim3((unsigned)nblk), dim3(256), 0,
-                         stream, blocks, scales, out, (int)R, (int)G, row_tiles, mode, expert_rows);
+                         stream, blocks, scales, out, (int)R, (int)G, row_tiles, mode);
     else
       hipLaunchKernelGGL((dequant_vec_kernel<OUT, false>), dim3((unsigned)nblk), dim3(256), 0,
-                         stream, blocks, scales, out, (int)R, (int)G, row_tiles, mode, expert_rows);
+                         stream, blocks, scales, out, (int)R, (int)G, row_tiles, mode);
   } else {
     const int64_t n = E * R * G * 16;
     int64_t nb = (n + 255) / 256;
@@ -204,14 +201,6 @@ static int launch_dequant(const uint8_t* blocks, const uint8_t* scales, void* ou
   }
   BSA_LAUNCH_CHECK("dequant launch");
   return BSA_OK;
-}
-
-// bf16 dequant of the experts with expert_rows[e] > 0 (the backward's
-// transposed-weight operands); the others are left untouched.
-int launch_dequant_bf16_routed(const uint8_t* blocks, const uint8_t* scales, uint16_t* out,
-                               int64_t E, int64_t R, int64_t G, const int* expert_rows,
-                               hipStream_t stream) {
-  return launch_dequant<DT_BF16>(blocks, scales, out, E, R, G, 0, stream, expert_rows);
 }
 
 }  // namespace bsa

@@ -49,9 +49,6 @@ int launch_combine(const float* Y, const int64_t* idx, const void* w, int w_dtyp
 int launch_bwd_prep(const void* dout, int dout_dtype, const float* y, const void* w, int w_dtype,
                     const int* pair_pos, int P, int k, int H, uint16_t* dy, float* grad_w,
                     hipStream_t st);
-int launch_dequant_bf16_routed(const uint8_t* blocks, const uint8_t* scales, uint16_t* out,
-                               int64_t E, int64_t R, int64_t G, const int* expert_rows,
-                               hipStream_t stream);
 int launch_quant_mxfp8(const void* x, int in_dtype, int64_t R, int64_t K, int64_t ldx, uint8_t* q,
                        int64_t ldq, uint8_t* s, int64_t lds, hipStream_t st);
 
@@ -70,7 +67,6 @@ struct GemmArgs {
   int topk;
   const uint8_t* Bq;     // packed [E][N][K/32][16]
   const uint8_t* Bs;     // scales [E][N][K/32]
-  const uint16_t* Bd;    // dense bf16 [E][N][K] (backward GEMMs) instead of Bq/Bs
   const void* bias;      // [E][N] or null
   int bias_dtype;
   const int* counts;     // rows per expert
@@ -1214,7 +1210,7 @@ constexpr int TL_BN = 128;
 constexpr int TL_BK = 64;
 constexpr int TL_LDK = TL_BK + 8;  // padded row, bf16 elements (144 bytes)
 
-template <int EPI, bool ALIGN16, bool BDENSE>
+template <int EPI, bool ALIGN16>
 __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
   __shared__ __align__(16) uint16_t sA[2][TL_BM * TL_LDK];
   __shared__ __align__(16) uint16_t sB[2][TL_BN * TL_LDK];
@@ -1252,40 +1248,20 @@ __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
   const int brr = tid >> 1;
   const int bgs = tid & 1;
   const bool bok = n0 + brr < a.N;
-  const uint8_t* bq = BDENSE ? nullptr
-                             : a.Bq + ((int64_t)e * a.N + (bok ? n0 + brr : 0)) * G * 16 + bgs * 16;
-  const uint8_t* bs = BDENSE ? nullptr : a.Bs + ((int64_t)e * a.N + (bok ? n0 + brr : 0)) * G + bgs;
+  const uint8_t* bq = a.Bq + ((int64_t)e * a.N + (bok ? n0 + brr : 0)) * G * 16 + bgs * 16;
+  const uint8_t* bs = a.Bs + ((int64_t)e * a.N + (bok ? n0 + brr : 0)) * G + bgs;
   const int bcol = (EPI == EPI_SWIGLU) ? ((brr & 1) ? 64 + (brr >> 1) : (brr >> 1)) : brr;
-  // dense B: 4 units of 16 bytes per thread per k-tile, like A
-  const uint16_t* bdp[4];
-  bool bdok[4];
-  if constexpr (BDENSE) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = (tid >> 3) + 32 * i;
-      bdok[i] = n0 + r < a.N;
-      bdp[i] = a.Bd + ((int64_t)e * a.N + (bdok[i] ? n0 + r : 0)) * a.K + akc * 8;
-    }
-  }
 
   u32x4_t ra[4];
   u32x4_t rb;
-  u32x4_t rbd[4];
   uint32_t rs;
   auto gload = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       ra[i] = aok[i] ? *reinterpret_cast<const u32x4_t*>(aptr[i] + kt * TL_BK)
                      : u32x4_t{0u, 0u, 0u, 0u};
-    if constexpr (BDENSE) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        rbd[i] = bdok[i] ? *reinterpret_cast<const u32x4_t*>(bdp[i] + kt * TL_BK)
-                         : u32x4_t{0u, 0u, 0u, 0u};
-    } else {
-      rb = bok ? load16<ALIGN16>(bq + kt * 32) : u32x4_t{0u, 0u, 0u, 0u};
-      rs = bok ? (uint32_t)bs[kt * 2] : 127u;
-    }
+    rb = bok ? load16<ALIGN16>(bq + kt * 32) : u32x4_t{0u, 0u, 0u, 0u};
+    rs = bok ? (uint32_t)bs[kt * 2] : 127u;
   };
   auto lstore = [&](int buf) {
 #pragma unroll
@@ -1293,20 +1269,12 @@ __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
       const int r = (tid >> 3) + 32 * i;
       *reinterpret_cast<u32x4_t*>(&sA[buf][r * TL_LDK + akc * 8]) = ra[i];
     }
-    if constexpr (BDENSE) {
+    uint16_t* dst = &sB[buf][bcol * TL_LDK + bgs * 32];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = (tid >> 3) + 32 * i;
-        *reinterpret_cast<u32x4_t*>(&sB[buf][r * TL_LDK + akc * 8]) = rbd[i];
-      }
-    } else {
-      uint16_t* dst = &sB[buf][bcol * TL_LDK + bgs * 32];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        uint32_t d[4];
-        mx_dword_to_bf16x8(rb[q], rs, true, d);
-        *reinterpret_cast<u32x4_t*>(dst + q * 8) = u32x4_t{d[0], d[1], d[2], d[3]};
-      }
+    for (int q = 0; q < 4; ++q) {
+      uint32_t d[4];
+      mx_dword_to_bf16x8(rb[q], rs, true, d);
+      *reinterpret_cast<u32x4_t*>(dst + q * 8) = u32x4_t{d[0], d[1], d[2], d[3]};
     }
   };
 
@@ -1880,41 +1848,121 @@ static Workspace carve(void* base, int64_t T, int64_t H, int64_t I, int64_t E, i
 }
 
 // ---------------------------------------------------------------------------
-// Dense-B tiled kernel (the backward's transposed-weight GEMMs): A bf16 rows
-// in expert-sorted order, B dense bf16 [E][N][K] (weight row n, k
-// contiguous), as the dequantisation writes them.  Tile 128 rows x 256
-// weight rows, BK = 64, two LDS stages filled only by global_load_lds DMA
-// (A and B rows of 128 bytes, 16-byte chunk c of row r at chunk c ^ (r & 7),
-// so the fragment reads are bank-conflict free).  Eight waves, each 64 x 64
-// (2 x 2 blocks of v_mfma_f32_32x32x16_bf16), one workgroup per CU.
+// Backward products straight from the packed weights (no dense copy).
+// out[pos][n] = sum_k A[pos][k] * W[e][k][n] where W is the MXFP4 checkpoint
+// tensor read along its rows: Bq [E][K][N/32][16] (row k of expert e holds
+// output columns n, 32 per block) and Bs [E][K][N/32].  For the input
+// gradient, K is the forward GEMM's output index (2I for gate_up, H for
+// down) and N its reduction index.  The scales vary along K within an MFMA's
+// reduction, so the weights are decoded to bf16 (not the block-scaled MFMA).
+//
+// Tile 128 rows x 512 columns, BK = 64 weight rows, four waves, one
+// workgroup per CU.  Wave w owns every row and columns 128w .. 128w+127; lane
+// (c = lane & 31, g = lane >> 5) of MFMA column block j (0..3) is column
+// 128w + 4c + j, so the lane's four columns are one packed 16-bit word per
+// weight row.  Per 16-k step the lane reads, for its 8 rows k = 8g .. 8g+7,
+// that word and the row's scale byte, converts each byte with
+// v_cvt_scalef32_pk_bf16_fp4 (two columns of one row) and pairs rows with
+// v_perm: 16 conversions + 16 permutes feed 16 MFMAs (4 x 4 blocks of
+// v_mfma_f32_32x32x16_bf16), and the epilogue stores 4 contiguous columns.
+// Stage (NS of them, global_load_lds DMA only):
+//  * A [128][64] bf16, 16-byte chunk c of row r at chunk c ^ (r & 7);
+//  * Q [64][256 B] packed weights, chunk c of row r at chunk c ^ (r & 15);
+//  * S: the 16 scale bytes of each weight row (blocks 16 nt .. 16 nt + 15,
+//    an unaligned run) as the two aligned 16-byte chunks that cover it;
+//    rows 16 v .. 16 v + 15 at [v][row & 15][32 B] (1 KiB per wave's DMA,
+//    lanes 32..63 repeating lanes 0..31).
+// The byte offset of a row's run within its first chunk repeats every 64
+// rows (64 * N/32 is a multiple of 16), so it is computed once per tile.
 // ---------------------------------------------------------------------------
-constexpr int D2_BM = 128;
-constexpr int D2_BN = 256;
-constexpr int D2_BK = 64;
-constexpr int D2_A_BYTES = D2_BM * D2_BK * 2;   // 16 KiB
-constexpr int D2_B_BYTES = D2_BN * D2_BK * 2;   // 32 KiB
-constexpr int D2_STAGE = D2_A_BYTES + D2_B_BYTES;
-constexpr int D2_NS = 3;
-constexpr int D2_DMA_PER_TILE = 2 + 4;          // per wave: A, B
+constexpr int BT_BM = 128;
+constexpr int BT_BN = 512;
+constexpr int BT_BK = 64;
+constexpr int BT_A_BYTES = BT_BM * BT_BK * 2;  // 16 KiB
+constexpr int BT_Q_BYTES = BT_BK * BT_BN / 2;  // 16 KiB
+constexpr int BT_S_BYTES = 4 * 1024;
+constexpr int BT_STAGE = BT_A_BYTES + BT_Q_BYTES + BT_S_BYTES;
+constexpr int BT_NS = 4;
+constexpr int BT_DMA_PER_TILE = 4 + 4 + 1;  // per wave: A, Q, S
 
-// One stage's DMA of the dense-B kernel (k-tile kt).  A device function, not
-// a lambda: HIP-Clang does not emit the host-side handle of a kernel template
-// whose body calls a capturing lambda.
-__device__ __forceinline__ void d2_issue(uint8_t* smem, int kt, int wave, const uint16_t* const* asrc,
-                                         const uint16_t* const* bsrc) {
-  uint8_t* st = smem + (kt % D2_NS) * D2_STAGE;
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-    __builtin_amdgcn_global_load_lds(asrc[j] + kt * D2_BK, (lds_void*)(st + (2 * wave + j) * 1024), 16, 0, 0);
+__device__ __forceinline__ void bt_issue(uint8_t* smem, int kt, int wave, const uint16_t* const* asrc,
+                                         const uint8_t* const* qsrc, int64_t qstep, const uint8_t* bs,
+                                         int64_t soff, int64_t sstep, int64_t slast) {
+  uint8_t* st = smem + (kt % BT_NS) * BT_STAGE;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    __builtin_amdgcn_global_load_lds(bsrc[j] + kt * D2_BK, (lds_void*)(st + D2_A_BYTES + (4 * wave + j) * 1024),
+    __builtin_amdgcn_global_load_lds(asrc[j] + kt * BT_BK, (lds_void*)(st + (4 * wave + j) * 1024), 16, 0, 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    __builtin_amdgcn_global_load_lds(qsrc[j] + kt * qstep, (lds_void*)(st + BT_A_BYTES + (4 * wave + j) * 1024),
                                      16, 0, 0);
+  // the second chunk of the tensor's last rows may start past its end: read
+  // the last whole chunk instead (those bytes are not used)
+  __builtin_amdgcn_global_load_lds(bs + min(soff + kt * sstep, slast),
+                                   (lds_void*)(st + BT_A_BYTES + BT_Q_BYTES + wave * 1024), 16, 0, 0);
+}
+
+// Step s's weight words (one 16-bit word per row: the lane's 4 columns) and
+// scale bytes of the lane's 8 rows.
+__device__ __forceinline__ void bt_read_q(const uint8_t* st, int s, const uint32_t (&qa)[8],
+                                          const uint32_t (&sa)[8], uint32_t (&raw)[8], uint32_t (&sb)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    raw[i] = *reinterpret_cast<const uint16_t*>(st + qa[i] + 4096 * s);
+    sb[i] = st[sa[i] + 1024 * s];
+  }
+}
+
+// The four 32-row A fragments of one 16-k step (aoff: the step's offset).
+__device__ __forceinline__ void bt_read_a(const uint8_t* st, uint32_t aoff, s16x8_t (&af)[4]) {
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) af[mb] = *reinterpret_cast<const s16x8_t*>(st + aoff + mb * 4096);
+}
+
+// 8 rows x 4 columns of E2M1 codes -> the 4 columns' B fragments (8 k values
+// each, rows in order, two per dword).
+__device__ __forceinline__ void bt_decode(const uint32_t (&raw)[8], const uint32_t (&sb)[8], u32x4_t (&bq)[4]) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const float s0 = mx_scale_f32(sb[2 * d]), s1 = mx_scale_f32(sb[2 * d + 1]);
+    const uint32_t lo0 = mx_byte_to_bf16x2_hw<0>(raw[2 * d], s0);
+    const uint32_t lo1 = mx_byte_to_bf16x2_hw<0>(raw[2 * d + 1], s1);
+    const uint32_t hi0 = mx_byte_to_bf16x2_hw<1>(raw[2 * d], s0);
+    const uint32_t hi1 = mx_byte_to_bf16x2_hw<1>(raw[2 * d + 1], s1);
+    bq[0][d] = pack_lo16(lo0, lo1);
+    bq[1][d] = pack_hi16(lo0, lo1);
+    bq[2][d] = pack_lo16(hi0, hi1);
+    bq[3][d] = pack_hi16(hi0, hi1);
+  }
+}
+
+// Four adjacent output columns n .. n+3 of row pos; pre holds the row's saved
+// (gate, up) pairs of those columns (EPI_SWIGLU_BWD).
+template <int EPI>
+__device__ __forceinline__ void bt_store4(const GemmArgs& a, int64_t pos, int n, const float (&v)[4],
+                                          const f32x4_t (&pre)[2]) {
+  if constexpr (EPI == EPI_SWIGLU_BWD) {
+    const f32x4_t p0 = pre[0], p1 = pre[1];
+    const float g[4] = {p0[0], p0[2], p1[0], p1[2]};
+    const float u[4] = {p0[1], p0[3], p1[1], p1[3]};
+    u32x4_t o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float dg, du;
+      swiglu_bwd(g[j], u[j], v[j], a.alpha, a.limit, &dg, &du);
+      o[j] = pack_bf16x2(dg, du);
+    }
+    *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(a.out) + pos * a.ldo + 2 * n) = o;
+  } else {
+    static_assert(EPI == EPI_STORE, "packed-weight backward epilogue");
+    f32x4_t o = {v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.out) + pos * a.ldo + n) = o;
+  }
 }
 
 template <int EPI>
-__global__ __launch_bounds__(512, 1) void moe_dense2_kernel(GemmArgs a) {
-  extern __shared__ __align__(1024) uint8_t smem[];  // D2_NS stages
+__global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
+  extern __shared__ __align__(1024) uint8_t smem[];  // BT_NS stages
   const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
   if (L < 0) return;
   const int tile = L / a.n_tiles_n;
@@ -1922,137 +1970,192 @@ __global__ __launch_bounds__(512, 1) void moe_dense2_kernel(GemmArgs a) {
   const int2 te = a.tiles[tile];
   const int e = te.x;
   const int m0 = te.y;
-  const int rows = min(D2_BM, a.offsets[e] + a.counts[e] - m0);
-  const int n0 = nt * D2_BN;
+  const int rows = min(BT_BM, a.offsets[e] + a.counts[e] - m0);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 2;   // rows 64*wm .. +64
-  const int wn = wave & 3;    // weight rows 64*wn .. +64
-  const int KT = a.K / D2_BK;
-  const int l32 = lane & 31;
-  const int lh = lane >> 5;
+  const int c = lane & 31;
+  const int g = lane >> 5;
+  const int KT = a.K / BT_BK;
+  const int NB = a.N >> 5;               // scale bytes (and 16-byte chunks) per weight row
+  const int64_t wrow0 = (int64_t)e * a.K;  // first weight row of the expert
 
-  // --- DMA sources: instruction j of wave w covers rows 8*(.) .. +7, eight
-  //     lanes per 128-byte row; past-the-tile rows read a valid row ----------
-  const uint16_t* asrc[2];
+  // --- DMA sources -----------------------------------------------------------
+  const uint16_t* asrc[4];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int r = 8 * (2 * wave + j) + (lane >> 3);
+  for (int j = 0; j < 4; ++j) {
+    const int r = 8 * (4 * wave + j) + (lane >> 3);
     const int ch = (lane & 7) ^ (r & 7);
     asrc[j] = a.A + tile_src_row(a, m0, rows, r) * a.lda + ch * 8;
   }
-  const uint16_t* bsrc[4];
+  const uint8_t* qsrc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int q = 8 * (4 * wave + j) + (lane >> 3);
-    const int ch = (lane & 7) ^ (q & 7);
-    const int n = n0 + q < a.N ? n0 + q : n0;
-    bsrc[j] = a.Bd + ((int64_t)e * a.N + n) * a.K + ch * 8;
+    const int q = 4 * (4 * wave + j) + (lane >> 4);
+    const int sc = (lane & 15) ^ (q & 15);
+    int gc = nt * 16 + sc;
+    if (gc >= NB) gc = nt * 16;  // columns past N: any chunk of the row
+    qsrc[j] = a.Bq + ((wrow0 + q) * NB + gc) * 16;
+  }
+  const int64_t qstep = (int64_t)BT_BK * NB * 16;
+  int64_t soff;  // byte offset into Bs of this lane's scale chunk
+  {
+    const int r = 16 * wave + ((lane & 31) >> 1);
+    const int64_t o = (wrow0 + r) * NB + nt * 16;
+    soff = (o & ~(int64_t)15) + 16 * (lane & 1);
+  }
+  const int64_t sstep = (int64_t)BT_BK * NB;
+  const int64_t slast = (int64_t)a.E * a.K * NB - 16;  // last whole chunk (size % 16 == 0)
+
+  // --- fragment addresses (step s adds 4096 s to Q, 1024 s to S) -------------
+  uint32_t aoff[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) aoff[s] = (uint32_t)(c * 128 + (((2 * s + g) ^ (c & 7)) * 16));
+  uint32_t qa[8], sa[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int rr = 8 * g + i;  // row within the 16-row step
+    qa[i] = (uint32_t)(BT_A_BYTES + rr * 256 + (((4 * wave + (c >> 3)) ^ rr) * 16) + 2 * (c & 7));
+    const int run = (int)(((wrow0 + rr) * NB) & 15);
+    sa[i] = (uint32_t)(BT_A_BYTES + BT_Q_BYTES + rr * 32 + run + 4 * wave + (c >> 3));
   }
 
-  // fragment offsets: step s (16 k) reads chunk 2s + lh of the lane's row
-  uint32_t aoff[2][4], boff[2][4];
+  f32x16_t acc[4][4];
 #pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    const int r = 64 * wm + 32 * b + l32;
-    const int q = 64 * wn + 32 * b + l32;
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      aoff[b][s] = (uint32_t)(r * 128 + (((2 * s + lh) ^ (r & 7)) * 16));
-      boff[b][s] = (uint32_t)(D2_A_BYTES + q * 128 + (((2 * s + lh) ^ (q & 7)) * 16));
-    }
-  }
-
-  f32x16_t acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  for (int i = 0; i < D2_NS - 1; ++i)
-    if (i < KT) d2_issue(smem, i, wave, asrc, bsrc);
+  // Software pipeline: during step s of tile kt the wave runs step s's 16
+  // MFMAs, decodes step s+1's B fragments (words read one step earlier) and
+  // reads step s+1's A fragments and step s+2's weight words -- across the
+  // tile boundary, from tile kt+1's stage.  So the barrier at the top of
+  // iteration kt certifies tile kt+1 (tile kt was certified one iteration
+  // earlier), and the stage refilled there (kt+3's, last read for tile kt-1)
+  // is free.  Words of step t sit in buffer t % 2.
+  for (int i = 0; i < BT_NS - 1; ++i)
+    if (i < KT) bt_issue(smem, i, wave, asrc, qsrc, qstep, a.Bs, soff, sstep, slast);
+  wait_tiles_ahead<BT_DMA_PER_TILE, BT_NS - 2>(min(BT_NS - 2, KT - 1));
+  asm volatile("s_barrier" ::: "memory");
+  uint32_t raw0[8], sb0[8], raw1[8], sb1[8];
+  s16x8_t af[4];
+  u32x4_t bq[4];
+  bt_read_q(smem, 0, qa, sa, raw0, sb0);
+  bt_read_q(smem, 1, qa, sa, raw1, sb1);
+  bt_read_a(smem, aoff[0], af);
+  bt_decode(raw0, sb0, bq);
   for (int kt = 0; kt < KT; ++kt) {
-    // tile kt has landed once at most the tiles issued after it are in
+    // tile kt+1 has landed once at most the tiles issued after it are in
     // flight; a bare s_barrier (a __syncthreads() fence would wait for them too)
-    wait_tiles_ahead<D2_DMA_PER_TILE, D2_NS - 2>(min(D2_NS - 2, KT - 1 - kt));
+    wait_tiles_ahead<BT_DMA_PER_TILE, BT_NS - 3>(KT - 2 - kt);
     asm volatile("s_barrier" ::: "memory");
-    if (kt + D2_NS - 1 < KT) d2_issue(smem, kt + D2_NS - 1, wave, asrc, bsrc);
-    const uint8_t* st = smem + (kt % D2_NS) * D2_STAGE;
+    if (kt + BT_NS - 1 < KT) bt_issue(smem, kt + BT_NS - 1, wave, asrc, qsrc, qstep, a.Bs, soff, sstep, slast);
+    const uint8_t* st = smem + (kt % BT_NS) * BT_STAGE;
+    // past the last tile this stage holds stale data: read, never used
+    const uint8_t* sn = smem + ((kt + 1) % BT_NS) * BT_STAGE;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      s16x8_t af[2], bf[2];
+      s16x8_t afn[4];
+      bt_read_a(s < 3 ? st : sn, aoff[(s + 1) & 3], afn);
+      if (s % 2 == 0)
+        bt_read_q(s < 2 ? st : sn, (s + 2) & 3, qa, sa, raw0, sb0);
+      else
+        bt_read_q(s < 2 ? st : sn, (s + 2) & 3, qa, sa, raw1, sb1);
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        af[b] = *reinterpret_cast<const s16x8_t*>(st + aoff[b][s]);
-        bf[b] = *reinterpret_cast<const s16x8_t*>(st + boff[b][s]);
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[mb][j] = mfma32(af[mb], __builtin_bit_cast(s16x8_t, bq[j]), acc[mb][j]);
+      u32x4_t bqn[4];
+      if (s % 2 == 0)
+        bt_decode(raw1, sb1, bqn);
+      else
+        bt_decode(raw0, sb0, bqn);
+      // interleave: each MFMA followed by 2-3 decode VALU ops and 1-2 LDS reads
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       }
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+      for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = mfma32(af[mb], bf[nb], acc[mb][nb]);
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) af[mb] = afn[mb];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bq[j] = bqn[j];
     }
-    // the stage refilled at the next iteration's issue() is this one: every
-    // wave's reads of it are done before that iteration's barrier
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   }
 
-  // epilogue: lane holds column l32 of each 32x32 block, rows 8*(v/4) + 4*lh + v%4
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int n = n0 + 64 * wn + 32 * nb + l32;
-      if (n >= a.N) continue;
-#pragma unroll
+  // epilogue: block (mb, j), register v is row 32 mb + 8 (v / 4) + 4 g + v % 4,
+  // column 128 wave + 4 c + j
+  const int n = nt * BT_BN + 128 * wave + 4 * c;
+  if (n >= a.N) return;
+#pragma clang loop unroll(full)
+  for (int mb = 0; mb < 4; ++mb) {
+    // one 32-row block at a time: its 16 rows' saved pre-activations are
+    // loaded together (the row loop would otherwise wait on each in turn)
+    f32x4_t pre[16][2];
+    if constexpr (EPI == EPI_SWIGLU_BWD) {
+#pragma clang loop unroll(full)
       for (int v = 0; v < 16; ++v) {
-        const int r = 64 * wm + 32 * mb + 8 * (v >> 2) + 4 * lh + (v & 3);
-        if (r < rows) epilogue_one<EPI>(a, m0 + r, n, acc[mb][nb][v], 0.f);
+        const int r = 32 * mb + 8 * (v >> 2) + 4 * g + (v & 3);
+        const f32x4_t* sp =
+            reinterpret_cast<const f32x4_t*>(a.save_pre + (int64_t)(m0 + min(r, rows - 1)) * (2 * (int64_t)a.N) + 2 * n);
+        pre[v][0] = sp[0];
+        pre[v][1] = sp[1];
       }
     }
+#pragma clang loop unroll(full)
+    for (int v = 0; v < 16; ++v) {
+      const int r = 32 * mb + 8 * (v >> 2) + 4 * g + (v & 3);
+      if (r < rows) {
+        const float o[4] = {acc[mb][0][v], acc[mb][1][v], acc[mb][2][v], acc[mb][3][v]};
+        bt_store4<EPI>(a, m0 + r, n, o, pre[v]);
+      }
+    }
+  }
 }
 
 static int allow_big_lds(const void* fn, int kind, int epi, int bytes);
 
-// Grouped GEMM with a dense bf16 B [E][N][K]: the backward products with
-// transposed weights, fed by the dequant kernel's [K, N] output.  The dense-B
-// kernel needs K % 64 == 0 and 16-byte aligned rows; other shapes take the
-// tiled kernel.
-template <int EPI>
-static int launch_gemm_dense(const GemmArgs& a, int64_t P, hipStream_t st) {
-  if (a.K % D2_BK == 0 && reinterpret_cast<uintptr_t>(a.A) % 16 == 0 && a.lda % 8 == 0 &&
-      reinterpret_cast<uintptr_t>(a.Bd) % 16 == 0) {
-    GemmArgs b = a;
-    b.n_tiles_n = (a.N + D2_BN - 1) / D2_BN;
-    const int64_t max_tiles = (P + D2_BM - 1) / D2_BM + a.E;
-    const int64_t grid = align_up(max_tiles * b.n_tiles_n, 8);
-    if (grid > INT32_MAX) {
-      set_error("dense grouped GEMM: grid too large");
-      return BSA_EINVAL;
-    }
-    const size_t smem = (size_t)D2_NS * D2_STAGE;
-    int rc = allow_big_lds(reinterpret_cast<const void*>(moe_dense2_kernel<EPI>), 7, EPI, (int)smem);
-    if (rc) return rc;
-    hipLaunchKernelGGL((moe_dense2_kernel<EPI>), dim3((unsigned)grid), dim3(512), smem, st, b);
-    BSA_LAUNCH_CHECK("dense grouped GEMM launch");
-    return BSA_OK;
-  }
-  const int64_t max_tiles = (P + TL_BM - 1) / TL_BM + a.E;
-  const int64_t grid = align_up(max_tiles * a.n_tiles_n, 8);
-  if (grid > INT32_MAX) {
-    set_error("dense grouped GEMM: grid too large");
-    return BSA_EINVAL;
-  }
-  hipLaunchKernelGGL((moe_tiled_kernel<EPI, true, true>), dim3((unsigned)grid), dim3(256), 0, st, a);
-  BSA_LAUNCH_CHECK("dense grouped GEMM launch");
-  return BSA_OK;
+// Grouped GEMM on the packed weights read along their rows (the backward
+// products): a.Bq [E][K][N/32][16], a.Bs [E][K][N/32].
+static bool bwd_packed_ok(const GemmArgs& a) {
+  auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  return a.N % 32 == 0 && a.K % BT_BK == 0 && al16(a.A) && a.lda % 8 == 0 && al16(a.Bq) && al16(a.Bs) &&
+         al16(a.out) && !a.row_pair && ((int64_t)a.E * a.K * (a.N / 32)) % 16 == 0;
 }
 
-// Block-scaled MX grouped GEMM (K % 64 == 0; 16-byte aligned blocks, 4-byte
-// aligned weight scales; a.Aq / a.As filled by launch_quant_mxfp8 with a
-// 16-byte aligned scale buffer whose row stride is a multiple of 16).
+template <int EPI>
+static int launch_gemm_packed_rows(const GemmArgs& a, int64_t P, hipStream_t st) {
+  GemmArgs b = a;
+  b.n_tiles_n = (a.N + BT_BN - 1) / BT_BN;
+  const int64_t max_tiles = (P + BT_BM - 1) / BT_BM + a.E;
+  const int64_t grid = align_up(max_tiles * b.n_tiles_n, 8);
+  if (grid > INT32_MAX) {
+    set_error("packed-weight grouped GEMM: grid too large");
+    return BSA_EINVAL;
+  }
+  const size_t smem = (size_t)BT_NS * BT_STAGE;
+  int rc = allow_big_lds(reinterpret_cast<const void*>(moe_bwd_packed_kernel<EPI>), 3, EPI, (int)smem);
+  if (rc) return rc;
+  hipLaunchKernelGGL((moe_bwd_packed_kernel<EPI>), dim3((unsigned)grid), dim3(256), smem, st, b);
+  BSA_LAUNCH_CHECK("packed-weight grouped GEMM launch");
+  return BSA_OK;
+}
 
 constexpr int T2_LAUNCH_NS = 2;  // and of the launched bf16 tiled kernel
 
@@ -2064,8 +2167,8 @@ static int allow_big_lds(const void* fn, int kind, int epi, int bytes = 160 * 10
     set_error("no current HIP device");
     return BSA_EHIP;
   }
-  // kinds: 4-5 tiled kernel, 6 persistent decode kernel, 7 dense-B kernel,
-  // 8-15 MX kernel configurations
+  // kinds: 3 packed-weight backward kernel, 4-5 tiled kernel, 6 persistent
+  // decode kernel, 8-15 MX kernel configurations
   static bool allowed[64][16][4];
   if (!allowed[dev][kind][epi]) {
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
@@ -2206,9 +2309,9 @@ static int launch_gemm(const GemmArgs& a, int path, int64_t P, hipStream_t st) {
       return BSA_EINVAL;
     }
     if (align16)
-      hipLaunchKernelGGL((moe_tiled_kernel<EPI, true, false>), dim3((unsigned)grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((moe_tiled_kernel<EPI, true>), dim3((unsigned)grid), dim3(256), 0, st, a);
     else
-      hipLaunchKernelGGL((moe_tiled_kernel<EPI, false, false>), dim3((unsigned)grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((moe_tiled_kernel<EPI, false>), dim3((unsigned)grid), dim3(256), 0, st, a);
   }
   BSA_LAUNCH_CHECK("grouped GEMM launch");
   return BSA_OK;
@@ -2452,8 +2555,6 @@ extern "C" int bsa_moe_experts_fwd(
 namespace bsa {
 
 struct BwdWorkspace {
-  uint16_t* w_gate_up;  // dense bf16 [E][H][2I] (dequant of gate_up: [K=H, N=2I])
-  uint16_t* w_down;     // dense bf16 [E][I][H]  (dequant of down:    [K=I, N=H])
   uint16_t* dy;         // [P][H] bf16: dOut rows scaled by the routing weight
   uint16_t* dgu;        // [P][2I] bf16: gradient of the gate_up pre-activations
   float* dx;            // [P][H] f32: per-row input gradients
@@ -2471,8 +2572,6 @@ static BwdWorkspace carve_bwd(void* base, int64_t T, int64_t H, int64_t I, int64
     off = align_up(off + bytes, 256);
     return r;
   };
-  w.w_gate_up = reinterpret_cast<uint16_t*>(take(E * H * 2 * I * 2));
-  w.w_down = reinterpret_cast<uint16_t*>(take(E * I * H * 2));
   w.dy = reinterpret_cast<uint16_t*>(take(P * H * 2));
   w.dgu = reinterpret_cast<uint16_t*>(take(P * 2 * I * 2));
   w.dx = reinterpret_cast<float*>(take(P * H * 4));
@@ -2516,6 +2615,10 @@ extern "C" int bsa_moe_experts_bwd(
               (long long)bwd_workspace_bytes, (long long)b.bytes);
   BSA_REQUIRE(reinterpret_cast<uintptr_t>(bwd_workspace) % 256 == 0,
               "experts bwd: backward workspace must be 256-byte aligned");
+  auto al16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+  BSA_REQUIRE(al16(gate_up_blocks) && al16(gate_up_scales) && al16(down_blocks) && al16(down_scales),
+              "experts bwd: gate_up/down blocks and scales must be 16-byte aligned");
+  BSA_REQUIRE(al16(save_gate_up), "experts bwd: save_gate_up must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t P = T * k;
 
@@ -2525,21 +2628,10 @@ extern "C" int bsa_moe_experts_bwd(
     return rc;
   if (!grad_hidden) return BSA_OK;
 
-  // 2. dense bf16 weights of the routed experts, in the [K, N] orientation
-  if ((rc = launch_dequant_bf16_routed(static_cast<const uint8_t*>(gate_up_blocks),
-                                       static_cast<const uint8_t*>(gate_up_scales), b.w_gate_up, E,
-                                       2 * I, H / 32, w.counts, st)))
-    return rc;
-  if ((rc = launch_dequant_bf16_routed(static_cast<const uint8_t*>(down_blocks),
-                                       static_cast<const uint8_t*>(down_scales), b.w_down, E, H,
-                                       I / 32, w.counts, st)))
-    return rc;
-
-  // 3. d(act) = dY @ W_down^T with the SwiGLU backward in the epilogue -> d(gate_up)
+  // 2. d(act) = dY @ W_down^T with the SwiGLU backward in the epilogue -> d(gate_up)
   GemmArgs g{};
   g.A = b.dy;
   g.lda = H;
-  g.Bd = b.w_down;  // rows = intermediate index, K = hidden
   g.counts = w.counts;
   g.offsets = w.offsets;
   g.E = (int)E;
@@ -2552,14 +2644,10 @@ extern "C" int bsa_moe_experts_bwd(
   g.limit = limit;
   g.tiles = w.tiles;
   g.num_tiles = w.num_tiles;
-  g.n_tiles_n = (int)((I + TL_BN - 1) / TL_BN);
-  if ((rc = launch_gemm_dense<EPI_SWIGLU_BWD>(g, P, st))) return rc;
-
-  // 4. dX rows = d(gate_up) @ W_gate_up^T
+  // 3. dX rows = d(gate_up) @ W_gate_up^T
   GemmArgs g2{};
   g2.A = b.dgu;
   g2.lda = 2 * I;
-  g2.Bd = b.w_gate_up;  // rows = hidden index, K = 2I
   g2.counts = w.counts;
   g2.offsets = w.offsets;
   g2.E = (int)E;
@@ -2570,10 +2658,19 @@ extern "C" int bsa_moe_experts_bwd(
   g2.out_dtype = DT_F32;
   g2.tiles = w.tiles;
   g2.num_tiles = w.num_tiles;
-  g2.n_tiles_n = (int)((H + TL_BN - 1) / TL_BN);
-  if ((rc = launch_gemm_dense<EPI_STORE>(g2, P, st))) return rc;
 
-  // 5. per-token sum of its k rows (ascending expert order)
+  // The checkpoint tensors read along their rows are exactly the transposed
+  // weights: W_down [E][H][I/32] blocks give rows = hidden (reduction),
+  // columns = intermediate.
+  g.Bq = static_cast<const uint8_t*>(down_blocks);
+  g.Bs = static_cast<const uint8_t*>(down_scales);
+  g2.Bq = static_cast<const uint8_t*>(gate_up_blocks);
+  g2.Bs = static_cast<const uint8_t*>(gate_up_scales);
+  BSA_REQUIRE(bwd_packed_ok(g) && bwd_packed_ok(g2), "experts bwd: unsupported operand layout");
+  if ((rc = launch_gemm_packed_rows<EPI_SWIGLU_BWD>(g, P, st))) return rc;
+  if ((rc = launch_gemm_packed_rows<EPI_STORE>(g2, P, st))) return rc;
+
+  // 4. per-token sum of its k rows (ascending expert order)
   return launch_combine(b.dx, router_indices, nullptr, DT_F32, w.pair_pos, (int)T, (int)k, (int)H,
                         grad_hidden, grad_hidden_dtype, st);
 }

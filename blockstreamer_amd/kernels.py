@@ -83,6 +83,11 @@ def moe_workspace_bytes(T: int, H: int, I: int, E: int, k: int) -> int:
     return out.value
 
 
+def _aligned16(t: Tensor) -> Tensor:
+    """``t`` itself when its storage starts on a 16-byte boundary, else a copy."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _aligned_bytes(nbytes: int, device, align: int = 256) -> Tensor:
     buf = torch.empty(nbytes + align, dtype=torch.uint8, device=device)
     off = (-buf.data_ptr()) % align
@@ -251,16 +256,19 @@ def moe_experts_backward(grad_out: Tensor, hidden: Tensor, router_indices: Tenso
     g_code = _lib.dtype_code(g.dtype)
     idx = router_indices.to(torch.int64).contiguous()
     w = routing_weights.contiguous()
+    # the backward kernels DMA the packed weights in 16-byte pieces
+    gub, gus, dnb, dns = (_aligned16(_as_u8(x)) for x in (gate_up_blocks, gate_up_scales,
+                                                           down_blocks, down_scales))
+    pre = _aligned16(gate_up_pre.contiguous())
     bwd_bytes = moe_bwd_workspace_bytes(T, H, I, E, k)
     bws = _aligned_bytes(bwd_bytes, dev)
     grad_h = torch.empty((T, H), dtype=hidden.dtype, device=dev) if need_hidden else None
     grad_w = torch.empty((T, k), dtype=torch.float32, device=dev) if need_weights else None
     with torch.cuda.device(dev):
         _lib.call("bsa_moe_experts_bwd", g.data_ptr(), g_code, T, H, I, E, k, idx.data_ptr(),
-                  w.data_ptr(), _lib.dtype_code(w.dtype), _as_u8(gate_up_blocks).data_ptr(),
-                  _as_u8(gate_up_scales).data_ptr(), _as_u8(down_blocks).data_ptr(),
-                  _as_u8(down_scales).data_ptr(), float(alpha), float(limit),
-                  workspace.data_ptr(), workspace.numel(), gate_up_pre.data_ptr(), bws.data_ptr(),
+                  w.data_ptr(), _lib.dtype_code(w.dtype), gub.data_ptr(), gus.data_ptr(),
+                  dnb.data_ptr(), dns.data_ptr(), float(alpha), float(limit),
+                  workspace.data_ptr(), workspace.numel(), pre.data_ptr(), bws.data_ptr(),
                   bwd_bytes, grad_h.data_ptr() if grad_h is not None else None,
                   _lib.dtype_code(hidden.dtype),
                   grad_w.data_ptr() if grad_w is not None else None, _lib.stream_handle(dev))

@@ -196,8 +196,9 @@ int bsa_quant_mxfp8(const void *x, int dtype, int64_t R, int64_t K, void *q,
                     void *scales, int64_t scale_ld, void *stream);
 
 /*
- * Bytes of the extra workspace bsa_moe_experts_bwd needs (dense bf16 copies
- * of the routed experts' weights and the per-row gradients).
+ * Bytes of the extra workspace bsa_moe_experts_bwd needs (the per-row
+ * gradients: weighted output gradient, gate_up gradient, input gradient).
+ * The weights are read packed; no dense copy is made.
  */
 int bsa_moe_bwd_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
                                 int64_t k, int64_t *bytes);
@@ -218,7 +219,9 @@ int bsa_moe_bwd_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
  *   grad_hidden     grad_hidden_dtype [T, H], or NULL to skip
  *   grad_weights    float32 [T, k] gradient of routing_weights, or NULL
  *
- * H must be a multiple of 64.  Dropped (token, slot) pairs get a zero
+ * H must be a multiple of 64.  The packed blocks and scales and
+ * save_gate_up must be 16-byte aligned (the kernels move them in 16-byte
+ * DMA pieces); otherwise BSA_EINVAL.  Dropped (token, slot) pairs get a zero
  * routing-weight gradient.
  */
 int bsa_moe_experts_bwd(

@@ -166,3 +166,51 @@ def test_mxfp4_matmul_gradient_and_memory(device):
     sum(y.sum() for y in chained).backward()
     dense_bytes = weight.numel() * weight.element_size()
     assert peak < dense_bytes * 16
+
+
+def _shift1(x: torch.Tensor) -> torch.Tensor:
+    """Same bytes, storage starting one byte past a 16-byte boundary."""
+    buf = torch.empty(x.numel() + 16, dtype=x.dtype, device=x.device)
+    off = (1 - buf.data_ptr()) % 16
+    v = buf[off:off + x.numel()].view(x.shape)
+    v.copy_(x)
+    assert v.data_ptr() % 16 == 1
+    return v
+
+
+def _backward_call(t, idx, w, g, blocks_scales):
+    _, ws, pre = kernels.moe_experts_forward(t["hidden"], idx, w, *expert_args(t), save=True)
+    gub, gus, dnb, dns = blocks_scales
+    return kernels.moe_experts_backward(g, t["hidden"], idx, w, gub, gus, dnb, dns, ws, pre)
+
+
+def test_backward_unaligned_weight_views(device):
+    """Weights viewed one byte off a 16-byte boundary: the wrapper copies them
+    to aligned storage and the result is the aligned call's, bit for bit."""
+    E, k, H, I, T = 8, 2, 256, 256, 40
+    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=61, scale_lo=116,
+                            scale_hi=122, device=device)
+    idx, w = synthetic.random_routing(T, E, k, seed=62, dtype=torch.float32, device=device)
+    g = torch.randn(T, H, device=device).to(torch.bfloat16)
+    keys = ("gate_up_proj_blocks", "gate_up_proj_scales", "down_proj_blocks", "down_proj_scales")
+    announce("moe backward, unaligned weight views")
+    gh0, gw0 = _backward_call(t, idx, w, g, [t[n] for n in keys])
+    gh1, gw1 = _backward_call(t, idx, w, g, [_shift1(t[n]) for n in keys])
+    torch.cuda.synchronize()
+    assert torch.equal(gh0, gh1) and torch.equal(gw0, gw1)
+
+
+def test_backward_c_abi_rejects_unaligned_weights(device, monkeypatch):
+    """The C entry point refuses weights that are not 16-byte aligned."""
+    E, k, H, I, T = 8, 2, 256, 256, 8
+    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=63, scale_lo=116, scale_hi=122,
+                            device=device)
+    idx, w = synthetic.random_routing(T, E, k, seed=64, dtype=torch.float32, device=device)
+    g = torch.randn(T, H, device=device).to(torch.bfloat16)
+    monkeypatch.setattr(kernels, "_aligned16", lambda x: x)
+    keys = ("gate_up_proj_blocks", "gate_up_proj_scales", "down_proj_blocks", "down_proj_scales")
+    bs = [t[n] for n in keys]
+    bs[3] = _shift1(bs[3])
+    announce("moe backward C-ABI, unaligned down scales")
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        _backward_call(t, idx, w, g, bs)
