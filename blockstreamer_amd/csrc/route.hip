@@ -256,10 +256,81 @@ __global__ __launch_bounds__(256) void moe_bwd_prep_kernel(
   if (lane == 0) grad_w[pair] = dot;
 }
 
+// The same with 8 consecutive elements per lane and 16-byte accesses
+// (H % 8 == 0, 16-byte aligned rows); DT is dout's dtype.
+template <int DT>
+__global__ __launch_bounds__(256) void moe_bwd_prep_vec_kernel(
+    const void* __restrict__ dout, const float* __restrict__ y, const void* __restrict__ w, int w_dtype,
+    const int* __restrict__ pair_pos, int P, int k, int H, uint16_t* __restrict__ dy,
+    float* __restrict__ grad_w) {
+  const int lane = threadIdx.x & 63;
+  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pair >= P) return;
+  const int pos = pair_pos[pair];
+  if (pos < 0) {
+    if (lane == 0) grad_w[pair] = 0.f;
+    return;
+  }
+  const int64_t t = pair / k;
+  const float wv = load_f32(w, pair, w_dtype);
+  const f32x4_t* yr = reinterpret_cast<const f32x4_t*>(y + (int64_t)pos * H);
+  u32x4_t* dyr = reinterpret_cast<u32x4_t*>(dy + (int64_t)pos * H);
+  float dot = 0.f;
+  for (int c = lane; c < H / 8; c += 64) {
+    float g[8];
+    if constexpr (DT == DT_F32) {
+      const f32x4_t* gr = reinterpret_cast<const f32x4_t*>(static_cast<const float*>(dout) + t * H);
+      const f32x4_t a = gr[2 * c], b = gr[2 * c + 1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        g[i] = a[i];
+        g[4 + i] = b[i];
+      }
+    } else {
+      const u32x4_t q = reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(dout) + t * H)[c];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (DT == DT_BF16) {
+          g[2 * i] = __uint_as_float(q[i] << 16);
+          g[2 * i + 1] = __uint_as_float(q[i] & 0xFFFF0000u);
+        } else {
+          g[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(q[i] & 0xFFFFu));
+          g[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(q[i] >> 16));
+        }
+      }
+    }
+    const f32x4_t y0 = yr[2 * c], y1 = yr[2 * c + 1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dot += g[i] * y0[i] + g[4 + i] * y1[i];
+    u32x4_t o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(g[2 * i] * wv, g[2 * i + 1] * wv);
+    dyr[c] = o;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) dot += __shfl_xor(dot, off);
+  if (lane == 0) grad_w[pair] = dot;
+}
+
 int launch_bwd_prep(const void* dout, int dout_dtype, const float* y, const void* w, int w_dtype,
                     const int* pair_pos, int P, int k, int H, uint16_t* dy, float* grad_w,
                     hipStream_t st) {
   if (P == 0) return BSA_OK;
+  auto al16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+  if (H % 8 == 0 && al16(dout) && al16(y) && al16(dy)) {
+    const dim3 grid((P + 3) / 4);
+    if (dout_dtype == DT_F32)
+      hipLaunchKernelGGL(moe_bwd_prep_vec_kernel<DT_F32>, grid, dim3(256), 0, st, dout, y, w, w_dtype,
+                         pair_pos, P, k, H, dy, grad_w);
+    else if (dout_dtype == DT_F16)
+      hipLaunchKernelGGL(moe_bwd_prep_vec_kernel<DT_F16>, grid, dim3(256), 0, st, dout, y, w, w_dtype,
+                         pair_pos, P, k, H, dy, grad_w);
+    else
+      hipLaunchKernelGGL(moe_bwd_prep_vec_kernel<DT_BF16>, grid, dim3(256), 0, st, dout, y, w, w_dtype,
+                         pair_pos, P, k, H, dy, grad_w);
+    BSA_LAUNCH_CHECK("backward prep launch");
+    return BSA_OK;
+  }
   hipLaunchKernelGGL(moe_bwd_prep_kernel, dim3((P + 3) / 4), dim3(256), 0, st, dout, dout_dtype, y,
                      w, w_dtype, pair_pos, P, k, H, dy, grad_w);
   BSA_LAUNCH_CHECK("backward prep launch");

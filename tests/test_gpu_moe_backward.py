@@ -214,3 +214,33 @@ def test_backward_c_abi_rejects_unaligned_weights(device, monkeypatch):
     announce("moe backward C-ABI, unaligned down scales")
     with pytest.raises(ValueError, match="16-byte aligned"):
         _backward_call(t, idx, w, g, bs)
+
+
+def _shift2(x: torch.Tensor) -> torch.Tensor:
+    """Same values, storage starting 2 bytes past a 16-byte boundary."""
+    buf = torch.empty(x.numel() + 16, dtype=x.dtype, device=x.device)
+    off = (2 // x.element_size() - buf.data_ptr() // x.element_size()) % (16 // x.element_size())
+    v = buf[off:off + x.numel()].view(x.shape)
+    v.copy_(x)
+    assert v.data_ptr() % 16 == 2
+    return v
+
+
+def test_backward_grad_out_dtypes_and_layouts(device):
+    """bf16, float32 and float16 output gradients (vectorised prep) and a bf16
+    view 2 bytes off alignment (element-wise prep) give the same gradients."""
+    E, k, H, I, T = 8, 2, 256, 256, 24
+    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=71, scale_lo=116,
+                            scale_hi=122, device=device)
+    idx, w = synthetic.random_routing(T, E, k, seed=72, dtype=torch.float32, device=device)
+    # multiples of 1/64 in [-1, 1): exact in every dtype
+    g = (torch.randint(-64, 64, (T, H), device=device) / 64).to(torch.bfloat16)
+    keys = ("gate_up_proj_blocks", "gate_up_proj_scales", "down_proj_blocks", "down_proj_scales")
+    bs = [t[n] for n in keys]
+    announce("moe backward, grad_out dtypes and layouts")
+    gh0, gw0 = _backward_call(t, idx, w, g, bs)
+    for what, gg in (("float32", g.float()), ("float16", g.half()), ("unaligned", _shift2(g))):
+        gh1, gw1 = _backward_call(t, idx, w, gg, bs)
+        torch.cuda.synchronize()
+        assert torch.equal(gh0, gh1), what
+        assert torch.allclose(gw0, gw1, rtol=1e-5, atol=1e-6), what
