@@ -228,6 +228,85 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
   }
 }
 
+// moe_combine_kernel for top-k <= 4 and H <= 4096 (H % 4 == 0, 16-byte
+// aligned rows): the slot entries are loaded together, and all of a token's
+// row loads (IT passes of 1024 columns x k rows, 16 bytes each) are in flight
+// before the first sum.  Same slot order, same sums.
+template <int IT>
+__global__ __launch_bounds__(256) void moe_combine4_kernel(
+    const float* __restrict__ Y, const int64_t* __restrict__ idx, const void* __restrict__ w,
+    int w_dtype, const int* __restrict__ pair_pos, int k, int H, void* __restrict__ out,
+    int out_dtype) {
+  const int64_t t = blockIdx.x;
+  int ps[4];
+  int64_t ex[4];
+  float wv[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    ps[p] = p < k ? pair_pos[t * k + p] : -1;
+    ex[p] = p < k ? idx[t * k + p] : 0;
+    wv[p] = p < k ? (w ? load_f32(w, t * k + p, w_dtype) : 1.0f) : 0.f;
+  }
+  // valid slots in ascending expert order (ties keep slot order)
+  int pos[4];
+  float wt[4];
+  int64_t es[4];
+  int n = 0;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    if (ps[p] < 0) continue;
+    int j = n;
+#pragma unroll
+    for (int q = 3; q > 0; --q)
+      if (q == j && es[q - 1] > ex[p]) {
+        es[q] = es[q - 1];
+        pos[q] = pos[q - 1];
+        wt[q] = wt[q - 1];
+        --j;
+      }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (q == j) {
+        es[q] = ex[p];
+        pos[q] = ps[p];
+        wt[q] = wv[p];
+      }
+    ++n;
+  }
+  float4 y[IT][4];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int h = (it * 256 + (int)threadIdx.x) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (h < H && j < n) y[it][j] = *reinterpret_cast<const float4*>(Y + (int64_t)pos[j] * H + h);
+  }
+  const int64_t obase = t * H;
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int h = (it * 256 + (int)threadIdx.x) * 4;
+    if (h >= H) continue;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (j < n) {
+        acc.x += wt[j] * y[it][j].x;
+        acc.y += wt[j] * y[it][j].y;
+        acc.z += wt[j] * y[it][j].z;
+        acc.w += wt[j] * y[it][j].w;
+      }
+    if (out_dtype == DT_BF16) {
+      uint2 v = make_uint2(pack_bf16x2(acc.x, acc.y), pack_bf16x2(acc.z, acc.w));
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + obase + h) = v;
+    } else {
+      store_f32_as(out, obase + h, acc.x, out_dtype);
+      store_f32_as(out, obase + h + 1, acc.y, out_dtype);
+      store_f32_as(out, obase + h + 2, acc.z, out_dtype);
+      store_f32_as(out, obase + h + 3, acc.w, out_dtype);
+    }
+  }
+}
+
 // Backward prep, one wave per (token, slot) pair (block_streamer/gptoss.py:175
 // differentiated): grad_w[t,p] = <dOut[t], y[pos]> (y = down output + bias,
 // before the routing weight) and dY[pos] = bf16(dOut[t] * w[t,p]).
@@ -349,6 +428,18 @@ int launch_combine(const float* Y, const int64_t* idx, const void* w, int w_dtyp
                    const int* pair_pos, int T, int k, int H, void* out, int out_dtype,
                    hipStream_t st) {
   if (T == 0) return BSA_OK;
+  if (T >= 1024 && k <= 4 && H % 4 == 0 && H <= 4096 && reinterpret_cast<uintptr_t>(Y) % 16 == 0 &&
+      (out_dtype != DT_BF16 || reinterpret_cast<uintptr_t>(out) % 8 == 0)) {
+    const int it = (H + 1023) / 1024;
+    auto fn = it == 1 ? moe_combine4_kernel<1>
+              : it == 2 ? moe_combine4_kernel<2>
+              : it == 3 ? moe_combine4_kernel<3>
+                        : moe_combine4_kernel<4>;
+    hipLaunchKernelGGL(fn, dim3((unsigned)T), dim3(256), 0, st, Y, idx, w, w_dtype, pair_pos, k, H, out,
+                       out_dtype);
+    BSA_LAUNCH_CHECK("combine launch");
+    return BSA_OK;
+  }
   // small batches: several workgroups per token (more loads in flight)
   int slices = (H + 1023) / 1024;
   if (slices > 4) slices = 4;

@@ -207,3 +207,25 @@ def test_shard_blob_views_8_byte_aligned(device, path):
     want = oracle.experts_ref(t["hidden"].cpu(), idx.cpu(), w.cpu().float(),
                               *[a.cpu() for a in expert_args(t)])
     assert_layer_close(got, want, f"8-byte views {path}")
+
+
+@pytest.mark.parametrize("k", [2, 3, 4])
+def test_combine_batched_equals_split(device, k):
+    """1100 tokens take the batched combine (all loads of a token in flight),
+    550 the per-slice one: same slot order and sums, so the outputs agree bit
+    for bit, with masked (index E) and repeated slots."""
+    E, H, I, T = 8, 256, 256, 1100
+    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=80 + k, scale_lo=118,
+                            scale_hi=124, device=device)
+    idx, w = synthetic.random_routing(T, E, k, seed=90 + k, device=device)
+    idx = idx.clone()
+    idx[::7, k - 1] = E                 # masked slot
+    idx[3::11, 0] = idx[3::11, k - 1]   # repeated expert (masked where that slot is)
+    idx = idx.contiguous()
+    args = expert_args(t)
+    announce(f"combine batched vs split, k={k}")
+    full = kernels.moe_experts_forward(t["hidden"], idx, w, *args, path="tiled")
+    parts = [kernels.moe_experts_forward(t["hidden"][s].contiguous(), idx[s].contiguous(),
+                                         w[s].contiguous(), *args, path="tiled")
+             for s in (slice(0, 550), slice(550, T))]
+    assert torch.equal(full.view(torch.int16), torch.cat(parts).view(torch.int16))
