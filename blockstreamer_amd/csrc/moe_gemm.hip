@@ -1883,24 +1883,93 @@ constexpr int BT_Q_BYTES = BT_BK * BT_BN / 2;  // 16 KiB
 constexpr int BT_S_BYTES = 4 * 1024;
 constexpr int BT_STAGE = BT_A_BYTES + BT_Q_BYTES + BT_S_BYTES;
 constexpr int BT_NS = 4;
-constexpr int BT_DMA_PER_TILE = 4 + 4 + 1;  // per wave: A, Q, S
 
-__device__ __forceinline__ void bt_issue(uint8_t* smem, int kt, int wave, const uint16_t* const* asrc,
-                                         const uint8_t* const* qsrc, int64_t qstep, const uint8_t* bs,
-                                         int64_t soff, int64_t sstep, int64_t slast) {
-  uint8_t* st = smem + (kt % BT_NS) * BT_STAGE;
+// DMA sources of one workgroup tile.  The activations (this library's own
+// buffers) always move in 16-byte pieces; the packed weights and scales move
+// in 16-byte pieces when both tensors are 16-byte aligned (W4 = false: 4 + 1
+// instructions per wave per stage) and in 4-byte pieces otherwise (W4 = true:
+// 16 + 2; views into a staging blob are only 8-byte aligned).  Either way the
+// stage layout is the one described above.
+template <bool W4>
+struct BtSrc {
+  static constexpr int DMA_PER_TILE = 4 + (W4 ? 16 + 2 : 4 + 1);  // per wave: A, Q, S
+  const uint16_t* asrc[4];
+  const uint8_t* bq;
+  const uint8_t* bs;
+  int64_t q[W4 ? 1 : 4];   // byte offsets into bq (W4: of this lane's word in instruction 0)
+  int64_t sc[W4 ? 2 : 1];  // byte offsets into bs of this lane's chunk
+  int qsw, qvalid;         // W4: the lane's chunk position, valid chunks of the tile
+  int64_t qrow, qstep, sstep, slast;
+
+  __device__ __forceinline__ void init(const GemmArgs& a, int m0, int rows, int nt, int64_t wrow0, int NB,
+                                       int wave, int lane) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    __builtin_amdgcn_global_load_lds(asrc[j] + kt * BT_BK, (lds_void*)(st + (4 * wave + j) * 1024), 16, 0, 0);
+    for (int j = 0; j < 4; ++j) {
+      const int r = 8 * (4 * wave + j) + (lane >> 3);
+      const int ch = (lane & 7) ^ (r & 7);
+      asrc[j] = a.A + tile_src_row(a, m0, rows, r) * a.lda + ch * 8;
+    }
+    bq = a.Bq;
+    bs = a.Bs;
+    qvalid = NB - nt * 16;  // chunks of the tile's columns that exist (>= 16: all)
+    qrow = (int64_t)NB * 16;
+    qstep = (int64_t)BT_BK * NB * 16;
+    sstep = (int64_t)BT_BK * NB;
+    slast = (int64_t)a.E * a.K * NB - 16;  // last whole chunk (the size is a multiple of 16)
+    if constexpr (W4) {
+      // instruction j: weight row 16 wave + j, lane = 4-byte word of the row's 256 bytes
+      qsw = lane >> 2;
+      q[0] = ((wrow0 + 16 * wave) * NB + nt * 16) * 16 + (lane & 3) * 4;
+      // instruction i: rows 16 wave + 8 i + lane / 8, word lane % 8 of the two chunks
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    __builtin_amdgcn_global_load_lds(qsrc[j] + kt * qstep, (lds_void*)(st + BT_A_BYTES + (4 * wave + j) * 1024),
-                                     16, 0, 0);
-  // the second chunk of the tensor's last rows may start past its end: read
-  // the last whole chunk instead (those bytes are not used)
-  __builtin_amdgcn_global_load_lds(bs + min(soff + kt * sstep, slast),
-                                   (lds_void*)(st + BT_A_BYTES + BT_Q_BYTES + wave * 1024), 16, 0, 0);
-}
+      for (int i = 0; i < 2; ++i) {
+        const int r = 16 * wave + 8 * i + (lane >> 3);
+        const int64_t o = (wrow0 + r) * NB + nt * 16;
+        sc[i] = (o & ~(int64_t)15) + 16 * ((lane & 7) >> 2);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 4 * (4 * wave + j) + (lane >> 4);
+        const int c = (lane & 15) ^ (r & 15);
+        q[j] = ((wrow0 + r) * NB + nt * 16 + (c < qvalid ? c : 0)) * 16;  // past N: any chunk
+      }
+      // rows 16 wave .. +15, two chunks each; lanes 32..63 repeat 0..31
+      const int r = 16 * wave + ((lane & 31) >> 1);
+      const int64_t o = (wrow0 + r) * NB + nt * 16;
+      sc[0] = (o & ~(int64_t)15) + 16 * (lane & 1);
+    }
+  }
+
+  __device__ __forceinline__ void issue(uint8_t* smem, int kt, int wave, int lane) const {
+    uint8_t* st = smem + (kt % BT_NS) * BT_STAGE;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_global_load_lds(asrc[j] + kt * BT_BK, (lds_void*)(st + (4 * wave + j) * 1024), 16, 0, 0);
+    uint8_t* sq = st + BT_A_BYTES;
+    uint8_t* ss = st + BT_A_BYTES + BT_Q_BYTES + wave * 1024;
+    // the second chunk of the tensor's last rows may start past its end: read
+    // the last whole chunk instead (those bytes are not used)
+    if constexpr (W4) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int c = qsw ^ j;  // row 16 wave + j keeps source chunk c at position qsw
+        const int64_t off = q[0] + kt * qstep + j * qrow + (c < qvalid ? c : 0) * 16;
+        __builtin_amdgcn_global_load_lds(bq + off, (lds_void*)(sq + (16 * wave + j) * 256), 4, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        __builtin_amdgcn_global_load_lds(bs + min(sc[i] + kt * sstep, slast) + (lane & 3) * 4,
+                                         (lds_void*)(ss + i * 256), 4, 0, 0);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        __builtin_amdgcn_global_load_lds(bq + q[j] + kt * qstep, (lds_void*)(sq + (4 * wave + j) * 1024), 16, 0,
+                                         0);
+      __builtin_amdgcn_global_load_lds(bs + min(sc[0] + kt * sstep, slast), (lds_void*)ss, 16, 0, 0);
+    }
+  }
+};
 
 // Step s's weight words (one 16-bit word per row: the lane's 4 columns) and
 // scale bytes of the lane's 8 rows.
@@ -1960,7 +2029,7 @@ __device__ __forceinline__ void bt_store4(const GemmArgs& a, int64_t pos, int n,
   }
 }
 
-template <int EPI>
+template <int EPI, bool W4>
 __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
   extern __shared__ __align__(1024) uint8_t smem[];  // BT_NS stages
   const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
@@ -1980,32 +2049,9 @@ __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
   const int NB = a.N >> 5;               // scale bytes (and 16-byte chunks) per weight row
   const int64_t wrow0 = (int64_t)e * a.K;  // first weight row of the expert
 
-  // --- DMA sources -----------------------------------------------------------
-  const uint16_t* asrc[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = 8 * (4 * wave + j) + (lane >> 3);
-    const int ch = (lane & 7) ^ (r & 7);
-    asrc[j] = a.A + tile_src_row(a, m0, rows, r) * a.lda + ch * 8;
-  }
-  const uint8_t* qsrc[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int q = 4 * (4 * wave + j) + (lane >> 4);
-    const int sc = (lane & 15) ^ (q & 15);
-    int gc = nt * 16 + sc;
-    if (gc >= NB) gc = nt * 16;  // columns past N: any chunk of the row
-    qsrc[j] = a.Bq + ((wrow0 + q) * NB + gc) * 16;
-  }
-  const int64_t qstep = (int64_t)BT_BK * NB * 16;
-  int64_t soff;  // byte offset into Bs of this lane's scale chunk
-  {
-    const int r = 16 * wave + ((lane & 31) >> 1);
-    const int64_t o = (wrow0 + r) * NB + nt * 16;
-    soff = (o & ~(int64_t)15) + 16 * (lane & 1);
-  }
-  const int64_t sstep = (int64_t)BT_BK * NB;
-  const int64_t slast = (int64_t)a.E * a.K * NB - 16;  // last whole chunk (size % 16 == 0)
+  BtSrc<W4> src;
+  src.init(a, m0, rows, nt, wrow0, NB, wave, lane);
+  constexpr int DPT = BtSrc<W4>::DMA_PER_TILE;
 
   // --- fragment addresses (step s adds 4096 s to Q, 1024 s to S) -------------
   uint32_t aoff[4];
@@ -2036,8 +2082,8 @@ __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
   // earlier), and the stage refilled there (kt+3's, last read for tile kt-1)
   // is free.  Words of step t sit in buffer t % 2.
   for (int i = 0; i < BT_NS - 1; ++i)
-    if (i < KT) bt_issue(smem, i, wave, asrc, qsrc, qstep, a.Bs, soff, sstep, slast);
-  wait_tiles_ahead<BT_DMA_PER_TILE, BT_NS - 2>(min(BT_NS - 2, KT - 1));
+    if (i < KT) src.issue(smem, i, wave, lane);
+  wait_tiles_ahead<DPT, BT_NS - 2>(min(BT_NS - 2, KT - 1));
   asm volatile("s_barrier" ::: "memory");
   uint32_t raw0[8], sb0[8], raw1[8], sb1[8];
   s16x8_t af[4];
@@ -2049,9 +2095,9 @@ __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
   for (int kt = 0; kt < KT; ++kt) {
     // tile kt+1 has landed once at most the tiles issued after it are in
     // flight; a bare s_barrier (a __syncthreads() fence would wait for them too)
-    wait_tiles_ahead<BT_DMA_PER_TILE, BT_NS - 3>(KT - 2 - kt);
+    wait_tiles_ahead<DPT, BT_NS - 3>(KT - 2 - kt);
     asm volatile("s_barrier" ::: "memory");
-    if (kt + BT_NS - 1 < KT) bt_issue(smem, kt + BT_NS - 1, wave, asrc, qsrc, qstep, a.Bs, soff, sstep, slast);
+    if (kt + BT_NS - 1 < KT) src.issue(smem, kt + BT_NS - 1, wave, lane);
     const uint8_t* st = smem + (kt % BT_NS) * BT_STAGE;
     // past the last tile this stage holds stale data: read, never used
     const uint8_t* sn = smem + ((kt + 1) % BT_NS) * BT_STAGE;
@@ -2131,12 +2177,19 @@ __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
 
 static int allow_big_lds(const void* fn, int kind, int epi, int bytes);
 
+// Explicit instantiations: the host compiler otherwise drops the handle of
+// the first of these named in the launcher below.
+template __global__ void moe_bwd_packed_kernel<EPI_STORE, false>(GemmArgs);
+template __global__ void moe_bwd_packed_kernel<EPI_STORE, true>(GemmArgs);
+template __global__ void moe_bwd_packed_kernel<EPI_SWIGLU_BWD, false>(GemmArgs);
+template __global__ void moe_bwd_packed_kernel<EPI_SWIGLU_BWD, true>(GemmArgs);
+
 // Grouped GEMM on the packed weights read along their rows (the backward
 // products): a.Bq [E][K][N/32][16], a.Bs [E][K][N/32].
 static bool bwd_packed_ok(const GemmArgs& a) {
-  auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-  return a.N % 32 == 0 && a.K % BT_BK == 0 && al16(a.A) && a.lda % 8 == 0 && al16(a.Bq) && al16(a.Bs) &&
-         al16(a.out) && !a.row_pair && ((int64_t)a.E * a.K * (a.N / 32)) % 16 == 0;
+  auto al = [](const void* p, int n) { return reinterpret_cast<uintptr_t>(p) % n == 0; };
+  return a.N % 32 == 0 && a.K % BT_BK == 0 && al(a.A, 16) && a.lda % 8 == 0 && al(a.Bq, 4) && al(a.Bs, 4) &&
+         al(a.out, 16) && !a.row_pair && ((int64_t)a.E * a.K * (a.N / 32)) % 16 == 0;
 }
 
 template <int EPI>
@@ -2150,9 +2203,11 @@ static int launch_gemm_packed_rows(const GemmArgs& a, int64_t P, hipStream_t st)
     return BSA_EINVAL;
   }
   const size_t smem = (size_t)BT_NS * BT_STAGE;
-  int rc = allow_big_lds(reinterpret_cast<const void*>(moe_bwd_packed_kernel<EPI>), 3, EPI, (int)smem);
+  const bool w16 = reinterpret_cast<uintptr_t>(a.Bq) % 16 == 0 && reinterpret_cast<uintptr_t>(a.Bs) % 16 == 0;
+  void (*fn)(GemmArgs) = w16 ? moe_bwd_packed_kernel<EPI, false> : moe_bwd_packed_kernel<EPI, true>;
+  int rc = allow_big_lds(reinterpret_cast<const void*>(fn), w16 ? 3 : 2, EPI, (int)smem);
   if (rc) return rc;
-  hipLaunchKernelGGL((moe_bwd_packed_kernel<EPI>), dim3((unsigned)grid), dim3(256), smem, st, b);
+  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), smem, st, b);
   BSA_LAUNCH_CHECK("packed-weight grouped GEMM launch");
   return BSA_OK;
 }
@@ -2167,7 +2222,7 @@ static int allow_big_lds(const void* fn, int kind, int epi, int bytes = 160 * 10
     set_error("no current HIP device");
     return BSA_EHIP;
   }
-  // kinds: 3 packed-weight backward kernel, 4-5 tiled kernel, 6 persistent
+  // kinds: 2-3 packed-weight backward kernel, 4-5 tiled kernel, 6 persistent
   // decode kernel, 8-15 MX kernel configurations
   static bool allowed[64][16][4];
   if (!allowed[dev][kind][epi]) {
@@ -2615,10 +2670,10 @@ extern "C" int bsa_moe_experts_bwd(
               (long long)bwd_workspace_bytes, (long long)b.bytes);
   BSA_REQUIRE(reinterpret_cast<uintptr_t>(bwd_workspace) % 256 == 0,
               "experts bwd: backward workspace must be 256-byte aligned");
-  auto al16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
-  BSA_REQUIRE(al16(gate_up_blocks) && al16(gate_up_scales) && al16(down_blocks) && al16(down_scales),
-              "experts bwd: gate_up/down blocks and scales must be 16-byte aligned");
-  BSA_REQUIRE(al16(save_gate_up), "experts bwd: save_gate_up must be 16-byte aligned");
+  auto al = [](const void* q, int n) { return reinterpret_cast<uintptr_t>(q) % n == 0; };
+  BSA_REQUIRE(al(gate_up_blocks, 4) && al(gate_up_scales, 4) && al(down_blocks, 4) && al(down_scales, 4),
+              "experts bwd: gate_up/down blocks and scales must be 4-byte aligned");
+  BSA_REQUIRE(al(save_gate_up, 16), "experts bwd: save_gate_up must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t P = T * k;
 

@@ -83,9 +83,9 @@ def moe_workspace_bytes(T: int, H: int, I: int, E: int, k: int) -> int:
     return out.value
 
 
-def _aligned16(t: Tensor) -> Tensor:
-    """``t`` itself when its storage starts on a 16-byte boundary, else a copy."""
-    return t if t.data_ptr() % 16 == 0 else t.clone()
+def _aligned(t: Tensor, n: int) -> Tensor:
+    """``t`` itself when its storage starts on an n-byte boundary, else a copy."""
+    return t if t.data_ptr() % n == 0 else t.clone()
 
 
 def _aligned_bytes(nbytes: int, device, align: int = 256) -> Tensor:
@@ -256,10 +256,11 @@ def moe_experts_backward(grad_out: Tensor, hidden: Tensor, router_indices: Tenso
     g_code = _lib.dtype_code(g.dtype)
     idx = router_indices.to(torch.int64).contiguous()
     w = routing_weights.contiguous()
-    # the backward kernels DMA the packed weights in 16-byte pieces
-    gub, gus, dnb, dns = (_aligned16(_as_u8(x)) for x in (gate_up_blocks, gate_up_scales,
-                                                           down_blocks, down_scales))
-    pre = _aligned16(gate_up_pre.contiguous())
+    # the backward kernels DMA the packed weights in 16- or 4-byte pieces
+    # (staging-blob views are 8-byte aligned) and the pre-activations in 16
+    gub, gus, dnb, dns = (_aligned(_as_u8(x), 4) for x in (gate_up_blocks, gate_up_scales,
+                                                            down_blocks, down_scales))
+    pre = _aligned(gate_up_pre.contiguous(), 16)
     bwd_bytes = moe_bwd_workspace_bytes(T, H, I, E, k)
     bws = _aligned_bytes(bwd_bytes, dev)
     grad_h = torch.empty((T, H), dtype=hidden.dtype, device=dev) if need_hidden else None

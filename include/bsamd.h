@@ -219,9 +219,9 @@ int bsa_moe_bwd_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
  *   grad_hidden     grad_hidden_dtype [T, H], or NULL to skip
  *   grad_weights    float32 [T, k] gradient of routing_weights, or NULL
  *
- * H must be a multiple of 64.  The packed blocks and scales and
- * save_gate_up must be 16-byte aligned (the kernels move them in 16-byte
- * DMA pieces); otherwise BSA_EINVAL.  Dropped (token, slot) pairs get a zero
+ * H must be a multiple of 64.  The packed blocks and scales must be 4-byte
+ * aligned (16-byte aligned ones move in 16-byte DMA pieces, others in 4-byte
+ * pieces) and save_gate_up 16-byte aligned; otherwise BSA_EINVAL.  Dropped (token, slot) pairs get a zero
  * routing-weight gradient.
  */
 int bsa_moe_experts_bwd(

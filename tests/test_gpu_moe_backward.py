@@ -168,13 +168,13 @@ def test_mxfp4_matmul_gradient_and_memory(device):
     assert peak < dense_bytes * 16
 
 
-def _shift1(x: torch.Tensor) -> torch.Tensor:
-    """Same bytes, storage starting one byte past a 16-byte boundary."""
+def _shift(x: torch.Tensor, by: int) -> torch.Tensor:
+    """Same bytes (uint8), storage starting `by` bytes past a 16-byte boundary."""
     buf = torch.empty(x.numel() + 16, dtype=x.dtype, device=x.device)
-    off = (1 - buf.data_ptr()) % 16
+    off = (by - buf.data_ptr()) % 16
     v = buf[off:off + x.numel()].view(x.shape)
     v.copy_(x)
-    assert v.data_ptr() % 16 == 1
+    assert v.data_ptr() % 16 == by
     return v
 
 
@@ -184,35 +184,37 @@ def _backward_call(t, idx, w, g, blocks_scales):
     return kernels.moe_experts_backward(g, t["hidden"], idx, w, gub, gus, dnb, dns, ws, pre)
 
 
-def test_backward_unaligned_weight_views(device):
-    """Weights viewed one byte off a 16-byte boundary: the wrapper copies them
-    to aligned storage and the result is the aligned call's, bit for bit."""
+@pytest.mark.parametrize("by", [8, 4, 1])
+def test_backward_unaligned_weight_views(device, by):
+    """Weights viewed `by` bytes past a 16-byte boundary (staging-blob views are
+    8-byte aligned): 8 and 4 take the 4-byte DMA kernel, 1 a copy made by the
+    wrapper.  Every result is the aligned call's, bit for bit."""
     E, k, H, I, T = 8, 2, 256, 256, 40
     t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=61, scale_lo=116,
                             scale_hi=122, device=device)
     idx, w = synthetic.random_routing(T, E, k, seed=62, dtype=torch.float32, device=device)
     g = torch.randn(T, H, device=device).to(torch.bfloat16)
     keys = ("gate_up_proj_blocks", "gate_up_proj_scales", "down_proj_blocks", "down_proj_scales")
-    announce("moe backward, unaligned weight views")
+    announce(f"moe backward, weight views {by} bytes off alignment")
     gh0, gw0 = _backward_call(t, idx, w, g, [t[n] for n in keys])
-    gh1, gw1 = _backward_call(t, idx, w, g, [_shift1(t[n]) for n in keys])
+    gh1, gw1 = _backward_call(t, idx, w, g, [_shift(t[n], by) for n in keys])
     torch.cuda.synchronize()
     assert torch.equal(gh0, gh1) and torch.equal(gw0, gw1)
 
 
 def test_backward_c_abi_rejects_unaligned_weights(device, monkeypatch):
-    """The C entry point refuses weights that are not 16-byte aligned."""
+    """The C entry point refuses weights that are not 4-byte aligned."""
     E, k, H, I, T = 8, 2, 256, 256, 8
     t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=63, scale_lo=116, scale_hi=122,
                             device=device)
     idx, w = synthetic.random_routing(T, E, k, seed=64, dtype=torch.float32, device=device)
     g = torch.randn(T, H, device=device).to(torch.bfloat16)
-    monkeypatch.setattr(kernels, "_aligned16", lambda x: x)
+    monkeypatch.setattr(kernels, "_aligned", lambda x, n: x)
     keys = ("gate_up_proj_blocks", "gate_up_proj_scales", "down_proj_blocks", "down_proj_scales")
     bs = [t[n] for n in keys]
-    bs[3] = _shift1(bs[3])
+    bs[3] = _shift(bs[3], 2)
     announce("moe backward C-ABI, unaligned down scales")
-    with pytest.raises(ValueError, match="16-byte aligned"):
+    with pytest.raises(ValueError, match="4-byte aligned"):
         _backward_call(t, idx, w, g, bs)
 
 
