@@ -42,7 +42,8 @@
 namespace bsa {
 
 int launch_dispatch(const int64_t* idx, int P, int E, int BM, int* counts, int* offsets,
-                    int* row_pair, int* pair_pos, int2* tiles, int* num_tiles, hipStream_t st);
+                    int* row_pair, int* pair_pos, int2* tiles, int* num_tiles, int* hist,
+                    hipStream_t st);
 int launch_combine(const float* Y, const int64_t* idx, const void* w, int w_dtype,
                    const int* pair_pos, int T, int k, int H, void* out, int out_dtype,
                    hipStream_t st);
@@ -2421,9 +2422,11 @@ static int check_ws(const MoeShape& m, void* workspace, int64_t bytes, Workspace
   return BSA_OK;
 }
 
+// The chunked dispatch's per-chunk histograms ([P/2048][E] int32) live in the
+// activation buffer, which gate_up overwrites afterwards.
 static int stage_dispatch(const MoeShape& m, const int64_t* idx, const Workspace& w, hipStream_t st) {
   return launch_dispatch(idx, (int)(m.T * m.k), (int)m.E, TL_BM, w.counts, w.offsets, w.row_pair,
-                         w.pair_pos, w.tiles, w.num_tiles, st);
+                         w.pair_pos, w.tiles, w.num_tiles, reinterpret_cast<int*>(w.act), st);
 }
 
 static int stage_gate_up(const MoeShape& m, const void* hidden, const void* blocks, const void* scales,

@@ -2,8 +2,9 @@
 //
 // Dispatch replaces block_streamer/gptoss.py:143-154 (one_hot, permute, sum,
 // nonzero, where, and the gather of hidden rows), which costs three host
-// synchronisations per call.  Here one workgroup builds, on the device, the
-// expert-sorted order of the T*k (token, slot) pairs:
+// synchronisations per call.  Here the device builds (one workgroup, or two
+// launches over chunks for large batches) the expert-sorted order of the
+// T*k (token, slot) pairs:
 //   counts[e], offsets[e] (exclusive scan), row_pair[pos] = t*k + p for the
 //   pos-th sorted row, pair_pos[t*k + p] = pos (or -1 for a dropped pair), and
 //   the grouped-GEMM tile list (expert, first row) for tiles of BM rows.
@@ -23,36 +24,16 @@ constexpr int DISPATCH_THREADS = 1024;
 constexpr int DISPATCH_WAVES = DISPATCH_THREADS / 64;
 constexpr int DISPATCH_MAX_E = 1024;
 
-__global__ __launch_bounds__(DISPATCH_THREADS) void moe_dispatch_kernel(
-    const int64_t* __restrict__ idx, int P, int E, int BM, int* __restrict__ counts,
-    int* __restrict__ offsets, int* __restrict__ row_pair, int* __restrict__ pair_pos,
-    int2* __restrict__ tiles, int* __restrict__ num_tiles) {
-  __shared__ int s_cnt[DISPATCH_MAX_E];
-  __shared__ int s_off[DISPATCH_MAX_E];
-  __shared__ int s_run[DISPATCH_MAX_E];
-  __shared__ int s_tile[DISPATCH_MAX_E];
-  __shared__ int s_scan[DISPATCH_THREADS];
-  __shared__ uint8_t s_wc[DISPATCH_WAVES][DISPATCH_MAX_E];
-
+// Exclusive scans over experts (one entry per thread, E <= DISPATCH_THREADS)
+// of the row counts and of the row-tile counts: a shuffle scan within each
+// wave, then the wave totals.  Returns expert tid's first sorted row; with
+// `write`, also stores counts, offsets, the tile list and the tile count.
+__device__ __forceinline__ int dispatch_scan(int my_cnt, int E, int BM, int* s_scan, bool write,
+                                             int* __restrict__ counts, int* __restrict__ offsets,
+                                             int2* __restrict__ tiles, int* __restrict__ num_tiles) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  for (int e = tid; e < E; e += DISPATCH_THREADS) {
-    s_cnt[e] = 0;
-    s_run[e] = 0;
-  }
-  __syncthreads();
-
-  // 1. histogram
-  for (int i = tid; i < P; i += DISPATCH_THREADS) {
-    const int64_t e = idx[i];
-    if (e >= 0 && e < E) atomicAdd(&s_cnt[(int)e], 1);
-  }
-  __syncthreads();
-
-  // 2. inclusive scans of counts and of tile counts (E <= 1024 = one entry
-  //    per thread): a shuffle scan within each wave, then the wave totals
-  const int my_cnt = tid < E ? s_cnt[tid] : 0;
   const int my_tiles = (my_cnt + BM - 1) / BM;
   int incl_rows = my_cnt, incl_tiles = my_tiles;
 #pragma unroll
@@ -73,10 +54,8 @@ __global__ __launch_bounds__(DISPATCH_THREADS) void moe_dispatch_kernel(
     incl_rows += s_scan[w];
     incl_tiles += s_scan[DISPATCH_WAVES + w];
   }
-  if (tid < E) {
-    const int start = incl_rows - my_cnt;
-    s_off[tid] = start;
-    s_tile[tid] = incl_tiles - my_tiles;
+  const int start = incl_rows - my_cnt;
+  if (write && tid < E) {
     counts[tid] = my_cnt;
     offsets[tid] = start;
     if (tid == E - 1) {
@@ -85,14 +64,25 @@ __global__ __launch_bounds__(DISPATCH_THREADS) void moe_dispatch_kernel(
     }
     for (int j = 0; j < my_tiles; ++j) tiles[incl_tiles - my_tiles + j] = make_int2(tid, start + j * BM);
   }
-  __syncthreads();
+  return start;
+}
 
-  // 3. stable placement, DISPATCH_THREADS pairs per round
+// Stable placement of pairs [begin, end): pair i with expert e goes to row
+// s_base[e] + (pairs of expert e before i in the range).  DISPATCH_THREADS
+// pairs per round: ranks within a wave from ballots, across waves from the
+// per-wave counts, across rounds from s_run.
+__device__ __forceinline__ void dispatch_place(const int64_t* __restrict__ idx, int begin, int end, int E,
+                                               const int* s_base, int* s_run,
+                                               uint8_t (*s_wc)[DISPATCH_MAX_E], int* __restrict__ row_pair,
+                                               int* __restrict__ pair_pos) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int base = 0; base < P; base += DISPATCH_THREADS) {
+  for (int base = begin; base < end; base += DISPATCH_THREADS) {
     const int i = base + tid;
     int e = -1;
-    if (i < P) {
+    if (i < end) {
       const int64_t v = idx[i];
       e = (v >= 0 && v < E) ? (int)v : -1;
     }
@@ -111,11 +101,11 @@ __global__ __launch_bounds__(DISPATCH_THREADS) void moe_dispatch_kernel(
     __syncthreads();
     if (e >= 0 && local_rank == 0) s_wc[wave][e] = (uint8_t)wave_cnt;
     __syncthreads();
-    if (i < P) {
+    if (i < end) {
       if (e >= 0) {
         int prefix = 0;
         for (int w = 0; w < wave; ++w) prefix += s_wc[w][e];
-        const int pos = s_off[e] + s_run[e] + prefix + local_rank;
+        const int pos = s_base[e] + s_run[e] + prefix + local_rank;
         row_pair[pos] = i;
         pair_pos[i] = pos;
       } else {
@@ -130,6 +120,85 @@ __global__ __launch_bounds__(DISPATCH_THREADS) void moe_dispatch_kernel(
     }
     __syncthreads();
   }
+}
+
+// Small batches: one workgroup does everything.
+__global__ __launch_bounds__(DISPATCH_THREADS) void moe_dispatch_kernel(
+    const int64_t* __restrict__ idx, int P, int E, int BM, int* __restrict__ counts,
+    int* __restrict__ offsets, int* __restrict__ row_pair, int* __restrict__ pair_pos,
+    int2* __restrict__ tiles, int* __restrict__ num_tiles) {
+  __shared__ int s_cnt[DISPATCH_MAX_E];
+  __shared__ int s_off[DISPATCH_MAX_E];
+  __shared__ int s_run[DISPATCH_MAX_E];
+  __shared__ int s_scan[2 * DISPATCH_WAVES];
+  __shared__ uint8_t s_wc[DISPATCH_WAVES][DISPATCH_MAX_E];
+
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += DISPATCH_THREADS) {
+    s_cnt[e] = 0;
+    s_run[e] = 0;
+  }
+  __syncthreads();
+  for (int i = tid; i < P; i += DISPATCH_THREADS) {
+    const int64_t e = idx[i];
+    if (e >= 0 && e < E) atomicAdd(&s_cnt[(int)e], 1);
+  }
+  __syncthreads();
+  const int start = dispatch_scan(tid < E ? s_cnt[tid] : 0, E, BM, s_scan, true, counts, offsets, tiles,
+                                  num_tiles);
+  if (tid < E) s_off[tid] = start;
+  __syncthreads();
+  dispatch_place(idx, 0, P, E, s_off, s_run, s_wc, row_pair, pair_pos);
+}
+
+// Large batches, in two launches over chunks of DISPATCH_CHUNK pairs: the
+// per-chunk expert histograms, then each chunk's workgroup derives every
+// expert's first row (all chunks' histograms) and its own chunk's base within
+// each expert (the earlier chunks'), and places its pairs.  The result is the
+// single-workgroup kernel's, entry for entry.
+constexpr int DISPATCH_CHUNK = 2048;
+
+__global__ __launch_bounds__(DISPATCH_THREADS) void moe_dispatch_hist_kernel(const int64_t* __restrict__ idx,
+                                                                              int P, int E,
+                                                                              int* __restrict__ hist) {
+  __shared__ int s_cnt[DISPATCH_MAX_E];
+  const int tid = threadIdx.x;
+  const int begin = blockIdx.x * DISPATCH_CHUNK;
+  const int end = min(P, begin + DISPATCH_CHUNK);
+  for (int e = tid; e < E; e += DISPATCH_THREADS) s_cnt[e] = 0;
+  __syncthreads();
+  for (int i = begin + tid; i < end; i += DISPATCH_THREADS) {
+    const int64_t e = idx[i];
+    if (e >= 0 && e < E) atomicAdd(&s_cnt[(int)e], 1);
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += DISPATCH_THREADS) hist[(int64_t)blockIdx.x * E + e] = s_cnt[e];
+}
+
+__global__ __launch_bounds__(DISPATCH_THREADS) void moe_dispatch_place_kernel(
+    const int64_t* __restrict__ idx, int P, int E, int BM, const int* __restrict__ hist,
+    int* __restrict__ counts, int* __restrict__ offsets, int* __restrict__ row_pair,
+    int* __restrict__ pair_pos, int2* __restrict__ tiles, int* __restrict__ num_tiles) {
+  __shared__ int s_off[DISPATCH_MAX_E];
+  __shared__ int s_run[DISPATCH_MAX_E];
+  __shared__ int s_scan[2 * DISPATCH_WAVES];
+  __shared__ uint8_t s_wc[DISPATCH_WAVES][DISPATCH_MAX_E];
+  const int tid = threadIdx.x;
+  const int chunk = blockIdx.x;
+  int total = 0, before = 0;
+  if (tid < E) {
+    for (int c = 0; c < (int)gridDim.x; ++c) {
+      const int h = hist[(int64_t)c * E + tid];
+      total += h;
+      if (c < chunk) before += h;
+    }
+    s_run[tid] = 0;
+  }
+  const int start = dispatch_scan(total, E, BM, s_scan, chunk == 0, counts, offsets, tiles, num_tiles);
+  if (tid < E) s_off[tid] = start + before;
+  __syncthreads();
+  const int begin = chunk * DISPATCH_CHUNK;
+  dispatch_place(idx, begin, min(P, begin + DISPATCH_CHUNK), E, s_off, s_run, s_wc, row_pair, pair_pos);
 }
 
 __device__ __forceinline__ float load_f32(const void* p, int64_t i, int dtype) {
@@ -417,7 +486,17 @@ int launch_bwd_prep(const void* dout, int dout_dtype, const float* y, const void
 }
 
 int launch_dispatch(const int64_t* idx, int P, int E, int BM, int* counts, int* offsets,
-                    int* row_pair, int* pair_pos, int2* tiles, int* num_tiles, hipStream_t st) {
+                    int* row_pair, int* pair_pos, int2* tiles, int* num_tiles, int* hist,
+                    hipStream_t st) {
+  if (hist && P > 2 * DISPATCH_CHUNK) {
+    const int nc = (P + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK;
+    hipLaunchKernelGGL(moe_dispatch_hist_kernel, dim3(nc), dim3(DISPATCH_THREADS), 0, st, idx, P, E, hist);
+    BSA_LAUNCH_CHECK("dispatch launch");
+    hipLaunchKernelGGL(moe_dispatch_place_kernel, dim3(nc), dim3(DISPATCH_THREADS), 0, st, idx, P, E, BM,
+                       hist, counts, offsets, row_pair, pair_pos, tiles, num_tiles);
+    BSA_LAUNCH_CHECK("dispatch launch");
+    return BSA_OK;
+  }
   hipLaunchKernelGGL(moe_dispatch_kernel, dim3(1), dim3(DISPATCH_THREADS), 0, st, idx, P, E, BM,
                      counts, offsets, row_pair, pair_pos, tiles, num_tiles);
   BSA_LAUNCH_CHECK("dispatch launch");
