@@ -271,8 +271,11 @@ extern "C" int bsa_router_fwd(const void* hidden, int dtype, int64_t T, int64_t 
   if (mfma) {
     // logits tiles, then top-k + softmax from the (L2-resident) logits
     if (T >= 4096) {
-      const int64_t nblk = ((T + 31) / 32) * ((E + 31) / 32);
-      hipLaunchKernelGGL((logits_bf16_kernel<2, 2, 4>), dim3((unsigned)nblk), dim3(256), 0, st,
+      // 32 tokens x 64 experts per workgroup (measured at 8192 tokens: 48.6 us
+      // for the router against 56-57 us with 32 x 32 and 65-67 us with 16 x 64
+      // or 16 x 128; the sums, and so the logits, do not depend on the tile)
+      const int64_t nblk = ((T + 31) / 32) * ((E + 63) / 64);
+      hipLaunchKernelGGL((logits_bf16_kernel<2, 4, 4>), dim3((unsigned)nblk), dim3(256), 0, st,
                          static_cast<const uint16_t*>(hidden), static_cast<const uint16_t*>(weight),
                          static_cast<const uint16_t*>(bias), (int)T, (int)H, (int)E,
                          static_cast<uint16_t*>(logits));
