@@ -1,8 +1,8 @@
 """The oracle: a CPU restatement of BlockStreamer's gpt-oss MoE expert path.
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
-``bench.py``'s ``cpu_baseline`` leg may import this package, and only as the
-checker (or, for ``cpu_baseline``, as the timed CPU port).  The product
+``bench.py``'s ``cpu_baseline`` leg may import this package, and only to check
+results against (or, for ``cpu_baseline``, as the timed CPU port).  The product
 package ``blockstreamer_amd`` never imports it.
 """
 

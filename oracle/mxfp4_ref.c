@@ -1,7 +1,7 @@
 /*
  * TEST INFRASTRUCTURE ONLY -- the oracle.  Nothing in the product links this
  * file; only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
- * load it, and only as the checker.
+ * load it, and only to check results against.
  *
  * CPU restatement of the MXFP4 expert-weight dequantisation that BlockStreamer
  * reaches through block_streamer/gptoss.py:24-42 (dequantize_expert), which
