@@ -351,7 +351,7 @@ def focused(args) -> int:
     if args.workload == "copy":
         res = bench_copy(args.steps, args.warmup)
     elif args.workload == "moe_decode":
-        res = bench_moe(64, args.steps, args.warmup, 0.5, seed=4, path=args.path)
+        res = bench_moe(args.tokens, args.steps, args.warmup, 0.5, seed=4, path=args.path)
     else:
         res = bench_moe(8192, args.steps, args.warmup, 0.0, seed=5, path=args.path)
     print(json.dumps({"workload": args.workload, "steps": args.steps, "warmup": args.warmup, **res}),
@@ -371,6 +371,8 @@ def main() -> int:
                          "that calibrates the HBM byte counters")
     ap.add_argument("--path", default="auto", choices=["auto", "stream", "tiled", "mx"],
                     help="expert GEMM kernel for the moe_decode / moe_prefill workloads")
+    ap.add_argument("--tokens", type=int, default=64, choices=[1, 8, 64],
+                    help="token batch of the moe_decode workload (the decode batches 1, 8 and 64)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE layer measurements")
     args = ap.parse_args()
@@ -403,6 +405,8 @@ def main() -> int:
     }
     if not args.no_moe:
         moe = {
+            "decode_t1": bench_moe(1, max(args.steps, 20), args.warmup, 0.5, seed=4),
+            "decode_t8": bench_moe(8, max(args.steps, 20), args.warmup, 0.5, seed=4),
             "decode_t64": bench_moe(64, max(args.steps, 20), args.warmup, 0.5, seed=4),
             "prefill_t8192": bench_moe(8192, max(args.steps // 4, 5), args.warmup, 0.0, seed=5),
         }
