@@ -54,6 +54,7 @@ CASES = [
     (8, 2, 256, 256, 64, 116, 120),
     (16, 4, 512, 256, 129, 116, 120),
     (4, 1, 128, 192, 77, 117, 121),
+    (4, 2, 64, 32, 5, 117, 121),   # one k-tile in both products, one column block
 ]
 
 
