@@ -13,20 +13,26 @@
 // tensor holds output column n with K contiguous, which is exactly the
 // per-lane layout of an MFMA B operand, so no transpose is ever needed.
 //
-// Three kernels:
-//  * moe_stream_kernel (decode, few rows per expert): one workgroup per
-//    (expert, 32-column slice).  The slice's packed bytes are one contiguous
-//    32*K/2-byte span; it is copied to LDS with 16-byte loads, then four
-//    waves split K and run v_mfma_f32_16x16x32_bf16 on 16-row blocks, with A
-//    rows prefetched 8 steps ahead.  Partial sums are reduced through LDS.
+// Kernels:
+//  * moe_stream_persist_kernel (decode, K = 2880): persistent workgroups,
+//    two per CU, walking (expert, 16-row pass, 16-weight-row slice) items
+//    through LDS DMA rings; the packed weights go to the block-scaled MFMA
+//    as they are, against the activations split into two MXFP8 terms.
 //    Bound: HBM (each hit expert's weights are read exactly once).
+//  * moe_stream_kernel (decode, other K, or operands the persistent kernel
+//    cannot DMA): one workgroup per (expert, 32-column slice), weights
+//    decoded to bf16 for v_mfma_f32_16x16x32_bf16.
 //  * moe_tiled2_kernel (prefill, 16-byte aligned operands): 128x256 output
-//    tiles of one expert, BK=64, three LDS stages filled by global_load_lds
+//    tiles of one expert, BK=64, two LDS stages filled by global_load_lds
 //    DMA, packed B decoded from LDS into MFMA operands by the one wave that
-//    uses them, v_mfma_f32_32x32x16_bf16.  Bound: MFMA.
-//  * moe_tiled_kernel (prefill for operands aligned to less than 16 bytes,
-//    and the backward products over dense bf16 weights): 128x128 tiles,
-//    BK=64, register-staged LDS double buffering, 2x2 waves of 64x64.
+//    uses them, v_mfma_f32_32x32x16_bf16.  Bound: MFMA, in practice L1->L2
+//    requests.
+//  * moe_mx_kernel (prefill, opt-in): the same tiles on the block-scaled
+//    v_mfma_scale_f32_32x32x64_f8f6f4 with MXFP8 activations.
+//  * moe_tiled_kernel (prefill for operands aligned to less than 16 bytes):
+//    128x128 tiles, BK=64, register-staged LDS double buffering.
+//  * moe_bwd_packed_kernel (the input-gradient backward): the packed weights
+//    read along their rows (the reduction index) and decoded in registers.
 // Weights are decoded with the gfx950 converter (v_cvt_scalef32_pk_bf16_fp4),
 // which follows OCP MX: a block whose E8M0 scale byte is 255 (the NaN code)
 // decodes to NaN, so the outputs it touches are NaN.  The reference's
@@ -35,8 +41,9 @@
 // reproduces the reference bit for bit, this case included.
 //
 // For the gate_up projection the weight rows interleave gate (even) and up
-// (odd) columns (gptoss.py:131).  Both kernels place gate column j and up
-// column j in the same lane, so the clamped SwiGLU runs in registers.
+// (odd) columns (gptoss.py:131).  Every forward kernel places gate column j
+// and up column j in the same lane (or adjacent lanes), so the clamped SwiGLU
+// runs in registers.
 #include "bsa_common.h"
 
 namespace bsa {
