@@ -19,9 +19,10 @@
 //    through LDS DMA rings; the packed weights go to the block-scaled MFMA
 //    as they are, against the activations split into two MXFP8 terms.
 //    Bound: HBM (each hit expert's weights are read exactly once).
-//  * moe_stream_kernel (decode, other K, or operands the persistent kernel
-//    cannot DMA): one workgroup per (expert, 32-column slice), weights
-//    decoded to bf16 for v_mfma_f32_16x16x32_bf16.
+//  * moe_stream_parts_kernel (decode, K = 2880 with operands the persistent
+//    kernel cannot DMA) and moe_stream_kernel (decode, any other K): one
+//    workgroup per (expert, column slice), weights decoded to bf16 for
+//    v_mfma_f32_16x16x32_bf16.
 //  * moe_tiled2_kernel (prefill, 16-byte aligned operands): 128x256 output
 //    tiles of one expert, BK=64, two LDS stages filled by global_load_lds
 //    DMA, packed B decoded from LDS into MFMA operands by the one wave that
