@@ -330,6 +330,88 @@ def cpu_baseline_moe(T: int = 64, sample: int = 64) -> dict:
                       f"({tm:.2f} s each)"}
 
 
+def bench_norm(T: int, reps: int = 50) -> dict:
+    """The post-attention RMSNorm of one gpt-oss layer (H = 2880, bf16
+    activations, float32 weight as transformers loads it): the fused kernels
+    against the eager transformers module.
+
+    ``fused_*_gpu_us``: GPU time per call of the fused kernels, from ``reps``
+    calls captured in one HIP graph and replayed between two HIP events (no
+    host launch cost).  ``*_fwd_us`` / ``*_fwd_bwd_us``: the module's forward,
+    and forward plus autograd input gradient, launched from the host as a
+    model issues them (launch cost included), mean of ``reps`` calls.  The
+    eager module stays out of graph capture (its reductions may record
+    memset nodes)."""
+    from blockstreamer_amd import gptoss, kernels
+
+    dev = torch.device("cuda", 0)
+    H, eps = GPTOSS_120B["H"], 1e-5
+    gen = torch.Generator().manual_seed(11)
+    w = (torch.randn(H, generator=gen) * 0.3 + 1.0).to(dev)
+    x = torch.randn(T, H, generator=gen).to(torch.bfloat16).to(dev)
+    dy = (torch.randn(T, H, generator=gen) * 0.1).to(torch.bfloat16).to(dev)
+    fused = gptoss.FusedRMSNorm(H, eps, torch.float32, dev)
+    with torch.no_grad():
+        fused.weight.copy_(w)
+    fused.weight.requires_grad_(False)
+    try:
+        from transformers.models.gpt_oss.modeling_gpt_oss import GptOssRMSNorm
+        eager = GptOssRMSNorm(H, eps=eps).to(dev)
+        with torch.no_grad():
+            eager.weight.copy_(w)
+        eager.weight.requires_grad_(False)
+    except ImportError:
+        eager = None
+
+    def graph_us(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        graph.replay()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        return round(a.elapsed_time(b) / reps * 1e3, 2)
+
+    def host_us(fn):
+        for _ in range(3):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return round(a.elapsed_time(b) / reps * 1e3, 2)
+
+    def fwd_bwd(mod):
+        xr = x.detach().requires_grad_(True)
+        return lambda: torch.autograd.grad(mod(xr), [xr], dy)
+
+    res = {"tokens": T, "hidden": H}
+    with torch.no_grad():
+        res["fused_fwd_gpu_us"] = graph_us(lambda: kernels.rmsnorm_forward(x, w, eps))
+        res["fused_bwd_gpu_us"] = graph_us(lambda: kernels.rmsnorm_backward(dy, x, w, eps))
+        res["fused_fwd_us"] = host_us(lambda: fused(x))
+        if eager is not None:
+            res["eager_fwd_us"] = host_us(lambda: eager(x))
+    res["fused_fwd_bwd_us"] = host_us(fwd_bwd(fused))
+    if eager is not None:
+        res["eager_fwd_bwd_us"] = host_us(fwd_bwd(eager))
+    # algorithmic HBM bytes: forward reads x and writes y, the input gradient
+    # reads x and dy and writes dx; the weight is read once
+    fwd_bytes, bwd_bytes = 2 * T * H * 2 + 4 * H, 3 * T * H * 2 + 4 * H
+    res["fused_fwd_GB_per_s"] = round(fwd_bytes / (res["fused_fwd_gpu_us"] * 1e-6) / 1e9, 1)
+    res["fused_bwd_GB_per_s"] = round(bwd_bytes / (res["fused_bwd_gpu_us"] * 1e-6) / 1e9, 1)
+    return res
+
+
 def bench_copy(steps: int, warmup: int) -> dict:
     """torch device-to-device copy of 2 GiB: 4 GiB of HBM traffic per step."""
     dev = torch.device("cuda", 0)
@@ -350,6 +432,8 @@ def bench_copy(steps: int, warmup: int) -> dict:
 def focused(args) -> int:
     if args.workload == "copy":
         res = bench_copy(args.steps, args.warmup)
+    elif args.workload == "norm":
+        res = {"norm": [bench_norm(t, reps=max(args.steps, 20)) for t in (64, 8192)]}
     elif args.workload == "moe_decode":
         res = bench_moe(args.tokens, args.steps, args.warmup, 0.5, seed=4, path=args.path)
     else:
@@ -365,10 +449,11 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="dequant",
-                    choices=["dequant", "moe_decode", "moe_prefill", "copy"],
+                    choices=["dequant", "moe_decode", "moe_prefill", "copy", "norm"],
                     help="dequant: the headline line (plus MoE layer results); moe_decode / "
                          "moe_prefill: one MoE workload alone; copy: a plain 2 GiB device copy "
-                         "that calibrates the HBM byte counters")
+                         "that calibrates the HBM byte counters; norm: the post-attention "
+                         "RMSNorm, fused and eager")
     ap.add_argument("--path", default="auto", choices=["auto", "stream", "tiled", "mx"],
                     help="expert GEMM kernel for the moe_decode / moe_prefill workloads")
     ap.add_argument("--tokens", type=int, default=64, choices=[1, 8, 64],
@@ -413,6 +498,7 @@ def main() -> int:
         if not args.no_cpu_baseline:
             moe["decode_t64"]["cpu_baseline"] = cpu_baseline_moe()
         line["moe_layer"] = moe
+        line["post_attention_norm"] = {"t64": bench_norm(64), "t8192": bench_norm(8192)}
     print(json.dumps(line), flush=True)
     return 0
 

@@ -54,6 +54,8 @@ _SIGNATURES = {
         _ptr, _i64, _ptr, _ptr, _i64,              # ws, ws bytes, save, bwd ws, bwd bytes
         _ptr, _int, _ptr, _ptr,                    # grad_hidden, dtype, grad_weights, stream
     ],
+    "bsa_rmsnorm_fwd": [_ptr, _int, _i64, _i64, _ptr, _int, _f32, _ptr, _ptr],
+    "bsa_rmsnorm_bwd": [_ptr, _ptr, _int, _i64, _i64, _ptr, _int, _f32, _ptr, _ptr],
 }
 _RESTYPE = {"bsa_last_error": ctypes.c_char_p}
 

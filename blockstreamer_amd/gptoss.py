@@ -245,6 +245,74 @@ class MXFP4MLP(nn.Module):
         return out.reshape(batch_size, sequence_length, hidden_dim), router_scores
 
 
+class _RMSNorm(torch.autograd.Function):
+    """One-launch RMSNorm; the input gradient in one launch as well.  The
+    weight gradient (frozen in LoRA training) is formed with torch ops only
+    when it is asked for."""
+
+    @staticmethod
+    def forward(ctx, hidden, weight, eps):
+        out = kernels.rmsnorm_forward(hidden, weight, eps)
+        ctx.save_for_backward(hidden, weight)
+        ctx.eps = eps
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        hidden, weight = ctx.saved_tensors
+        dh = kernels.rmsnorm_backward(grad, hidden, weight, ctx.eps) if ctx.needs_input_grad[0] else None
+        dw = None
+        if ctx.needs_input_grad[1]:
+            h32 = hidden.float()
+            normed = h32 * torch.rsqrt(h32.pow(2).mean(-1, keepdim=True) + ctx.eps)
+            dw = (grad.float() * normed).reshape(-1, hidden.shape[-1]).sum(0).to(weight.dtype)
+        return dh, dw, None
+
+
+class FusedRMSNorm(nn.Module):
+    """Drop-in for ``GptOssRMSNorm`` (TF/models/gpt_oss/modeling_gpt_oss.py:47-62):
+    same parameter (``weight [H]``), attribute (``variance_epsilon``) and
+    result dtype (that of the input), computed in one HIP launch instead of
+    the eager module's chain of elementwise kernels."""
+
+    def __init__(self, hidden_size: int, eps: float = 1e-6, dtype: torch.dtype = torch.float32,
+                 device=None) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden_size, dtype=dtype, device=device))
+        self.variance_epsilon = eps
+
+    def forward(self, hidden_states: Tensor) -> Tensor:
+        return _RMSNorm.apply(hidden_states, self.weight, self.variance_epsilon)
+
+    def extra_repr(self) -> str:
+        return f"{tuple(self.weight.shape)}, eps={self.variance_epsilon}"
+
+
+def install_fused_post_attention_norm(model: nn.Module) -> int:
+    """Swap every layer's ``post_attention_layernorm`` (the norm in front of
+    the router and experts, modeling_gpt_oss.py:373) for ``FusedRMSNorm``.
+
+    No counterpart in the reference, which keeps the transformers module; the
+    parameter name, dtype and device are kept, so checkpoints and shards bind
+    as before.  Returns the number of layers changed.
+    """
+    from transformers.models.gpt_oss import modeling_gpt_oss as gpt_oss
+
+    replaced = 0
+    for layer in model.model.layers:
+        old = layer.post_attention_layernorm
+        if isinstance(old, gpt_oss.GptOssRMSNorm):
+            new = FusedRMSNorm(old.weight.shape[0], old.variance_epsilon, old.weight.dtype,
+                               None if old.weight.device.type == "meta" else old.weight.device)
+            if old.weight.device.type != "meta":
+                with torch.no_grad():
+                    new.weight.copy_(old.weight)
+            new.weight.requires_grad_(old.weight.requires_grad)
+            layer.post_attention_layernorm = new
+            replaced += 1
+    return replaced
+
+
 def install_mxfp4_router(model: nn.Module, config, dtype=torch.bfloat16) -> int:
     """Swap every ``GptOssTopKRouter`` for the fused ``MXFP4TopKRouter``.
 

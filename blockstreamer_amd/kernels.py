@@ -319,3 +319,42 @@ def router_topk(logits: Tensor, top_k: int):
         _lib.call("bsa_router_topk", lg.data_ptr(), _lib.dtype_code(lg.dtype), T, E, top_k,
                   scores.data_ptr(), idx.data_ptr(), _lib.stream_handle(dev))
     return scores, idx
+
+
+def _norm_args(x: Tensor, weight: Tensor):
+    H = x.shape[-1]
+    if weight.dim() != 1 or weight.shape[0] != H:
+        raise ValueError(f"norm weight must be [{H}], got {tuple(weight.shape)}")
+    if x.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise ValueError(f"norm input dtype {x.dtype} is not bf16, f16 or f32")
+    w = weight if weight.dtype in (torch.bfloat16, torch.float16, torch.float32) else weight.float()
+    return H, x.numel() // H if H else 0, w.contiguous()
+
+
+def rmsnorm_forward(x: Tensor, weight: Tensor, eps: float) -> Tensor:
+    """GptOssRMSNorm.forward (TF/models/gpt_oss/modeling_gpt_oss.py:57-62) in
+    one launch: ``dtype(float32(weight) * x32 * rsqrt(mean(x32^2) + eps))``
+    over the last dimension, in the dtype of ``x``."""
+    dev = _lib.require_gpu(x, weight)
+    H, T, w = _norm_args(x, weight)
+    xc = x.contiguous()
+    out = torch.empty_like(xc)
+    with torch.cuda.device(dev):
+        _lib.call("bsa_rmsnorm_fwd", xc.data_ptr(), _lib.dtype_code(xc.dtype), T, H, w.data_ptr(),
+                  _lib.dtype_code(w.dtype), float(eps), out.data_ptr(), _lib.stream_handle(dev))
+    return out
+
+
+def rmsnorm_backward(grad_out: Tensor, x: Tensor, weight: Tensor, eps: float) -> Tensor:
+    """Input gradient of ``rmsnorm_forward`` in the dtype of ``x``."""
+    dev = _lib.require_gpu(grad_out, x, weight)
+    H, T, w = _norm_args(x, weight)
+    if grad_out.shape != x.shape:
+        raise ValueError(f"grad_out shape {tuple(grad_out.shape)} != input shape {tuple(x.shape)}")
+    xc = x.contiguous()
+    g = grad_out.to(xc.dtype).contiguous()
+    dx = torch.empty_like(xc)
+    with torch.cuda.device(dev):
+        _lib.call("bsa_rmsnorm_bwd", g.data_ptr(), xc.data_ptr(), _lib.dtype_code(xc.dtype), T, H,
+                  w.data_ptr(), _lib.dtype_code(w.dtype), float(eps), dx.data_ptr(), _lib.stream_handle(dev))
+    return dx

@@ -234,6 +234,36 @@ int bsa_moe_experts_bwd(
     int64_t bwd_workspace_bytes, void *grad_hidden, int grad_hidden_dtype,
     float *grad_weights, void *stream);
 
+/*
+ * RMSNorm of a decoder layer, in one launch: the post-attention norm that
+ * feeds the router and the experts (and any other GptOssRMSNorm).
+ *
+ * Replaces transformers models/gpt_oss/modeling_gpt_oss.py:57-62
+ * (GptOssRMSNorm.forward; the post-attention call is at :373), in its
+ * operation order:
+ *   x32 = float32(x); r = 1 / sqrt(sum(x32^2) / H + eps)
+ *   out dtype [T, H] = dtype(float32(weight) * (x32 * r))
+ *   x       dtype [T, H]
+ *   weight  weight_dtype [H] (transformers keeps this module in float32 when
+ *           loading a checkpoint, modeling_gpt_oss.py:398)
+ * The sum runs in a fixed order, so the result is reproducible; it differs
+ * from torch's by float32 rounding of the sum only.  Any T >= 0, H >= 1.
+ */
+int bsa_rmsnorm_fwd(const void *x, int dtype, int64_t T, int64_t H,
+                    const void *weight, int weight_dtype, float eps,
+                    void *out, void *stream);
+
+/*
+ * Input gradient of bsa_rmsnorm_fwd (what autograd computes for
+ * modeling_gpt_oss.py:57-62 with respect to hidden_states), rounded once:
+ *   g = float32(weight) * float32(grad_out)
+ *   grad_x dtype [T, H] = dtype(r * g - x32 * (r^3 * sum(g * x32) / H))
+ * The weight gradient is not computed (the LoRA path keeps it frozen).
+ */
+int bsa_rmsnorm_bwd(const void *grad_out, const void *x, int dtype, int64_t T,
+                    int64_t H, const void *weight, int weight_dtype,
+                    float eps, void *grad_x, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

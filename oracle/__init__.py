@@ -20,6 +20,8 @@ from .oracle import (  # noqa: F401
     mlp_ref,
     mxfp8_dequant_ref,
     mxfp8_quant_ref,
+    rmsnorm_bwd_ref,
+    rmsnorm_ref,
     router_ref,
     topk_softmax_ref,
 )

@@ -22,6 +22,10 @@ Pinning (how each function is checked, see ``tests/test_oracle.py``):
   float8_e4m3fn cast for in-range values (a library routine, RNE), closed
   forms at the format's boundaries (max 448, min normal 2^-6, min subnormal
   2^-9, ties), and exact round trips of representable inputs.
+* RMSNorm (the post-attention norm in front of the path): the installed
+  transformers ``GptOssRMSNorm`` in float64, forward and its autograd
+  backward (against the closed-form gradient), plus scale invariance and the
+  eps-dominated regime.
 * experts: the installed transformers dense twin ``GptOssExperts``
   (TF/models/gpt_oss/modeling_gpt_oss.py:68-114) fed the dequantised
   weights, plus invariants (zero routing weight contributes nothing, token
@@ -162,6 +166,28 @@ def router_ref(h: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, k: int
     logits = F.linear(h.to(dtype), weight.to(dtype), bias.to(dtype))
     _, scores, idx = topk_softmax_ref(logits, k)
     return logits, scores, idx
+
+
+def rmsnorm_ref(x: torch.Tensor, weight: torch.Tensor, eps: float,
+                dtype: torch.dtype = torch.float64) -> torch.Tensor:
+    """TF/models/gpt_oss/modeling_gpt_oss.py:57-62 (GptOssRMSNorm.forward)
+    over the last dimension, computed in ``dtype`` and not rounded back to the
+    input dtype (float64 for the parity reference)."""
+    x = x.to(dtype)
+    r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+    return weight.to(dtype) * (x * r)
+
+
+def rmsnorm_bwd_ref(grad: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, eps: float,
+                    dtype: torch.dtype = torch.float64) -> torch.Tensor:
+    """Input gradient of ``rmsnorm_ref`` in closed form: with g = weight * grad
+    and r = rsqrt(mean(x^2) + eps), dx = r g - x r^3 sum(g x) / H (the
+    derivative of modeling_gpt_oss.py:60-62 with respect to hidden_states)."""
+    x = x.to(dtype)
+    g = weight.to(dtype) * grad.to(dtype)
+    H = x.shape[-1]
+    r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+    return r * g - x * (r ** 3 * (g * x).sum(-1, keepdim=True) / H)
 
 
 def apply_gate_ref(gate_up: torch.Tensor, alpha: float = 1.702,

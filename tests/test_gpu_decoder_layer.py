@@ -1,5 +1,6 @@
 """The drop-in inside transformers' own GptOssDecoderLayer, called the way a
-layer-streaming runner calls it.
+layer-streaming runner calls it: packed experts and the fused post-attention
+norm installed (the fused router as well in the whole-model test).
 
 Per layer: the layer's parameters arrive through
 ``torch.func.functional_call(layer, state, args, kwargs, strict=True)`` with
@@ -74,6 +75,7 @@ def _build(device):
                                                         torch.float32))
     ours = copy.deepcopy(ref)
     assert gptoss.install_mxfp4_experts(ours, cfg, torch.bfloat16) == L
+    assert gptoss.install_fused_post_attention_norm(ours) == L
     return cfg, ref, ref32, ours, packs
 
 
@@ -99,9 +101,11 @@ def _capture_layer_inputs(model, x):
 
 def _run_layer(layer, state, args, kwargs, grad=False):
     """functional_call as the runner does; returns the output, the MLP's input,
-    the router's (scores, indices) and the experts' output."""
+    the router's (scores, indices), the experts' output and the post-attention
+    norm's input."""
     seen = {}
     hooks = [
+        layer.post_attention_layernorm.register_forward_hook(lambda m, a, o: seen.__setitem__("norm_in", a[0])),
         layer.mlp.register_forward_hook(lambda m, a, o: seen.__setitem__("mlp_in", a[0])),
         layer.mlp.router.register_forward_hook(lambda m, a, o: seen.__setitem__("route", (o[1], o[2]))),
         layer.mlp.experts.register_forward_hook(lambda m, a, o: seen.__setitem__("experts", o)),
@@ -126,6 +130,12 @@ def test_decoder_layers_forward_vs_float32_transformers(device):
         state = _layer_state(ref.model.layers[i], packs[i])
         out, seen = _run_layer(ours.model.layers[i], state, args, kwargs)
         assert out.shape == args[0].shape and out.dtype == torch.bfloat16 and torch.isfinite(out).all()
+        # the fused post-attention norm against the transformers module it
+        # replaced, on the same input: at most one bf16 ulp apart
+        want_norm = ref.model.layers[i].post_attention_layernorm(seen["norm_in"])
+        a, b = seen["mlp_in"].float(), want_norm.float()
+        assert ((a - b).abs() <= 2.0 ** -7 * b.abs() * (1 + 1e-5) + 1e-30).all()
+        print(f"layer {i}: norm differs from transformers on {(a != b).float().mean().item():.3%}")
         scores, idx = seen["route"]
         tokens = seen["mlp_in"].reshape(-1, H)
         want = ref32.model.layers[i].mlp.experts(tokens.float(), idx, scores.float())

@@ -169,6 +169,58 @@ def test_router_matches_transformers():
     assert torch.equal(got[1], want[1])
 
 
+# ----------------------------------------------------------------------------- rmsnorm
+
+def _tf_norm(H, eps, weight):
+    gpt_oss = pytest.importorskip("transformers.models.gpt_oss.modeling_gpt_oss")
+    m = gpt_oss.GptOssRMSNorm(H, eps=eps)
+    with torch.no_grad():
+        m.weight.copy_(weight)
+    return m
+
+
+@pytest.mark.parametrize("H,eps,scale", [(2880, 1e-5, 1.0), (100, 1e-5, 1e-3), (64, 1e-6, 30.0)])
+def test_rmsnorm_ref_matches_transformers_forward_and_autograd(H, eps, scale):
+    """The module upcasts its input to float32 itself, so it is pinned in
+    float32 (bit-exact, same operations) and the float64 reference within
+    float32 rounding; the closed-form gradient against float64 autograd of
+    the restated forward and against the module's own float32 autograd."""
+    g = torch.Generator().manual_seed(H)
+    x = torch.randn(9, H, generator=g) * scale
+    w = torch.randn(H, generator=g) * 0.5 + 1.0
+    dy = torch.randn(9, H, generator=g)
+    m = _tf_norm(H, eps, w)
+    xr = x.clone().requires_grad_(True)
+    want = m(xr)
+    (want_dx,) = torch.autograd.grad(want, [xr], dy)
+    assert torch.equal(oracle.rmsnorm_ref(x, w, eps, dtype=torch.float32), want.detach())
+    got = oracle.rmsnorm_ref(x, w, eps)
+    assert torch.allclose(got, want.detach().double(), rtol=2e-6, atol=0)
+    x64 = x.double().requires_grad_(True)
+    (auto_dx,) = torch.autograd.grad(oracle.rmsnorm_ref(x64, w, eps), [x64], dy.double())
+    got_dx = oracle.rmsnorm_bwd_ref(dy, x, w, eps)
+    assert (got_dx - auto_dx).abs().max() <= 1e-12 * auto_dx.abs().max()
+    assert (got_dx - want_dx.double()).abs().max() <= 1e-5 * auto_dx.abs().max()
+
+
+def test_rmsnorm_ref_invariants():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(4, 256, generator=g, dtype=torch.float64)
+    w = torch.ones(256, dtype=torch.float64)
+    # scale invariance without eps; unit RMS output with unit weight
+    a = oracle.rmsnorm_ref(x, w, 0.0)
+    b = oracle.rmsnorm_ref(x * 37.5, w, 0.0)
+    assert torch.allclose(a, b, rtol=1e-14, atol=0)
+    assert torch.allclose(a.pow(2).mean(-1), torch.ones(4, dtype=torch.float64), rtol=1e-14)
+    # eps-dominated rows: x * rsqrt(eps)
+    tiny = x * 1e-9
+    assert torch.allclose(oracle.rmsnorm_ref(tiny, w, 1e-2), tiny * 10.0, rtol=1e-9)
+    # the gradient is orthogonal to x when eps = 0 (scale invariance)
+    dy = torch.randn(4, 256, generator=g, dtype=torch.float64)
+    dx = oracle.rmsnorm_bwd_ref(dy, x, w, 0.0)
+    assert (dx * x).sum(-1).abs().max() <= 1e-12 * dx.abs().max() * x.abs().max() * 256
+
+
 # ----------------------------------------------------------------------------- experts
 
 def _tiny():
