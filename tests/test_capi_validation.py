@@ -1,0 +1,131 @@
+"""Argument checking of every C-ABI entry point (CPU).
+
+Each case breaks one rule that the entry point checks on the host before any
+HIP call, so it returns BSA_EINVAL with a message naming the rule; empty
+problems (T = 0 or R = 0) return BSA_OK without touching memory.  The
+pointers passed are never dereferenced: every case fails (or returns) in the
+host-side checks, which this file also asserts on a machine without a GPU,
+where a call that got past them would fail with BSA_EHIP instead.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+
+from blockstreamer_amd import _lib
+
+FAKE = 1 << 20          # a 1 MiB-aligned address, never dereferenced
+BF16, F16, F32 = 0, 1, 2
+GPTOSS = dict(T=4, H=2880, I=2880, E=128, k=4)
+_OUT = ctypes.c_int64(0)
+OUT = ctypes.byref(_OUT)  # the size functions' output
+
+
+def _ws_bytes(T, H, I, E, k, fn="bsa_moe_workspace_bytes"):
+    n = ctypes.c_int64(0)
+    assert getattr(_lib.lib(), fn)(T, H, I, E, k, ctypes.byref(n)) == _lib.BSA_OK
+    return n.value
+
+
+def _fwd_args(T=4, H=2880, I=2880, E=128, k=4, hidden=FAKE, wdt=BF16, bdt=BF16, odt=BF16, path=0,
+              ptr=FAKE, ws=FAKE, ws_bytes=None):
+    if ws_bytes is None:
+        ws_bytes = _ws_bytes(max(T, 0), H, I, E, k) if min(H, I, E, k) > 0 and T >= 0 else 0
+    return (hidden, T, H, I, E, k, ptr, ptr, wdt, ptr, ptr, ptr, ptr, ptr, ptr, bdt, 1.702, 7.0, ptr, odt,
+            ws, ws_bytes, None, path, None)
+
+
+def _bwd_args(T=4, H=2880, I=2880, E=128, k=4, gdt=BF16, blocks=FAKE, save=FAKE, bwd_ws=FAKE,
+              bwd_bytes=None, ghdt=BF16):
+    ws_bytes = _ws_bytes(T, H, I, E, k) if min(H, I, E, k) > 0 and T >= 0 else 0
+    if bwd_bytes is None:
+        bwd_bytes = _ws_bytes(T, H, I, E, k, "bsa_moe_bwd_workspace_bytes") if ws_bytes else 0
+    return (FAKE, gdt, T, H, I, E, k, FAKE, FAKE, BF16, blocks, FAKE, FAKE, FAKE, 1.702, 7.0, FAKE, ws_bytes,
+            save, bwd_ws, bwd_bytes, FAKE, ghdt, FAKE, None)
+
+
+CASES = [
+    # name, entry point, arguments, expected status, message fragment
+    ("ws size null", "bsa_moe_workspace_bytes", (4, 64, 64, 8, 2, None), _lib.BSA_EINVAL, b"null"),
+    ("ws size shape", "bsa_moe_workspace_bytes", (4, 0, 64, 8, 2, OUT), _lib.BSA_EINVAL, b"bad shape"),
+    ("bwd ws size shape", "bsa_moe_bwd_workspace_bytes", (-1, 64, 64, 8, 2, OUT), _lib.BSA_EINVAL,
+     b"bad shape"),
+    ("fwd k = 0", "bsa_moe_experts_fwd", _fwd_args(k=0), _lib.BSA_EINVAL, b"bad shape"),
+    ("fwd H % 32", "bsa_moe_experts_fwd", _fwd_args(H=48), _lib.BSA_EINVAL, b"multiples of 32"),
+    ("fwd E > 1024", "bsa_moe_experts_fwd", _fwd_args(E=2000), _lib.BSA_EINVAL, b"1024 experts"),
+    ("fwd k > 16", "bsa_moe_experts_fwd", _fwd_args(k=17), _lib.BSA_EINVAL, b"top-k"),
+    ("fwd T = 0", "bsa_moe_experts_fwd", _fwd_args(T=0, ptr=None, hidden=None), _lib.BSA_OK, None),
+    ("fwd dtype", "bsa_moe_experts_fwd", _fwd_args(odt=7), _lib.BSA_EINVAL, b"dtype"),
+    ("fwd path", "bsa_moe_experts_fwd", _fwd_args(path=9), _lib.BSA_EINVAL, b"path"),
+    ("fwd null", "bsa_moe_experts_fwd", _fwd_args(ptr=None), _lib.BSA_EINVAL, b"null"),
+    ("fwd hidden alignment", "bsa_moe_experts_fwd", _fwd_args(hidden=FAKE + 2), _lib.BSA_EINVAL,
+     b"16-byte aligned"),
+    ("fwd workspace too small", "bsa_moe_experts_fwd", _fwd_args(ws_bytes=1024), _lib.BSA_EINVAL, b"workspace"),
+    ("fwd workspace alignment", "bsa_moe_experts_fwd", _fwd_args(ws=FAKE + 16), _lib.BSA_EINVAL, b"aligned"),
+    ("bwd H % 64", "bsa_moe_experts_bwd", _bwd_args(H=96), _lib.BSA_EINVAL, b"hidden % 64"),
+    ("bwd T = 0", "bsa_moe_experts_bwd", _bwd_args(T=0), _lib.BSA_OK, None),
+    ("bwd dtype", "bsa_moe_experts_bwd", _bwd_args(ghdt=5), _lib.BSA_EINVAL, b"dtype"),
+    ("bwd blocks alignment", "bsa_moe_experts_bwd", _bwd_args(blocks=FAKE + 2), _lib.BSA_EINVAL,
+     b"4-byte aligned"),
+    ("bwd save alignment", "bsa_moe_experts_bwd", _bwd_args(save=FAKE + 4), _lib.BSA_EINVAL, b"16-byte"),
+    ("bwd workspace too small", "bsa_moe_experts_bwd", _bwd_args(bwd_bytes=256), _lib.BSA_EINVAL,
+     b"backward workspace"),
+    ("bwd workspace alignment", "bsa_moe_experts_bwd", _bwd_args(bwd_ws=FAKE + 64), _lib.BSA_EINVAL,
+     b"256-byte"),
+    ("router E > 256", "bsa_router_fwd", (FAKE, BF16, 4, 64, 300, 4, FAKE, None, FAKE, FAKE, FAKE, None),
+     _lib.BSA_EINVAL, b"E <= 256"),
+    ("router k > E", "bsa_router_fwd", (FAKE, BF16, 4, 64, 4, 8, FAKE, None, FAKE, FAKE, FAKE, None),
+     _lib.BSA_EINVAL, b"k <= min(E"),
+    ("router dtype", "bsa_router_fwd", (FAKE, 3, 4, 64, 8, 2, FAKE, None, FAKE, FAKE, FAKE, None),
+     _lib.BSA_EINVAL, b"dtype"),
+    ("router T = 0", "bsa_router_fwd", (None, BF16, 0, 64, 8, 2, None, None, None, None, None, None),
+     _lib.BSA_OK, None),
+    ("router null", "bsa_router_fwd", (FAKE, BF16, 4, 64, 8, 2, None, None, FAKE, FAKE, FAKE, None),
+     _lib.BSA_EINVAL, b"null"),
+    ("topk k > 16", "bsa_router_topk", (FAKE, F32, 4, 64, 17, FAKE, FAKE, None), _lib.BSA_EINVAL, b"k <= min"),
+    ("topk T = 0", "bsa_router_topk", (None, F32, 0, 64, 4, None, None, None), _lib.BSA_OK, None),
+    ("mxfp8 K % 32", "bsa_quant_mxfp8", (FAKE, BF16, 4, 48, FAKE, FAKE, 2, None), _lib.BSA_EINVAL, b"K % 32"),
+    ("mxfp8 scale stride", "bsa_quant_mxfp8", (FAKE, BF16, 4, 128, FAKE, FAKE, 2, None), _lib.BSA_EINVAL,
+     b"stride"),
+    ("mxfp8 alignment", "bsa_quant_mxfp8", (FAKE + 8, BF16, 4, 128, FAKE, FAKE, 4, None), _lib.BSA_EINVAL,
+     b"aligned"),
+    ("mxfp8 R = 0", "bsa_quant_mxfp8", (None, BF16, 0, 128, None, None, 4, None), _lib.BSA_OK, None),
+    ("norm H = 0", "bsa_rmsnorm_fwd", (FAKE, BF16, 4, 0, FAKE, F32, 1e-5, FAKE, None), _lib.BSA_EINVAL,
+     b"bad shape"),
+    ("norm dtype", "bsa_rmsnorm_fwd", (FAKE, 4, 4, 64, FAKE, F32, 1e-5, FAKE, None), _lib.BSA_EINVAL,
+     b"dtype"),
+    ("norm T = 0", "bsa_rmsnorm_fwd", (None, BF16, 0, 64, None, F32, 1e-5, None, None), _lib.BSA_OK, None),
+    ("norm null", "bsa_rmsnorm_fwd", (FAKE, BF16, 4, 64, None, F32, 1e-5, FAKE, None), _lib.BSA_EINVAL,
+     b"null"),
+    ("norm bwd weight dtype", "bsa_rmsnorm_bwd", (FAKE, FAKE, BF16, 4, 64, FAKE, 9, 1e-5, FAKE, None),
+     _lib.BSA_EINVAL, b"dtype"),
+    ("norm bwd null", "bsa_rmsnorm_bwd", (None, FAKE, BF16, 4, 64, FAKE, F32, 1e-5, FAKE, None),
+     _lib.BSA_EINVAL, b"null"),
+]
+
+
+@pytest.mark.parametrize("name,fn,args,rc,msg", CASES, ids=[c[0] for c in CASES])
+def test_entry_point_rejects_before_any_gpu_call(name, fn, args, rc, msg):
+    lib = _lib.lib()
+    got = getattr(lib, fn)(*args)
+    err = lib.bsa_last_error()
+    assert got == rc, f"{name}: status {got}, message {err!r}"
+    if msg is not None:
+        assert msg in err, f"{name}: message {err!r} lacks {msg!r}"
+    else:
+        assert err in (b"", None), f"{name}: unexpected message {err!r}"
+
+
+def test_workspace_sizes_grow_with_tokens():
+    a = _ws_bytes(64, **{k: v for k, v in GPTOSS.items() if k != "T"})
+    b = _ws_bytes(8192, **{k: v for k, v in GPTOSS.items() if k != "T"})
+    assert 0 < a < b and a % 256 == 0 and b % 256 == 0
+    c = _ws_bytes(64, **{k: v for k, v in GPTOSS.items() if k != "T"}, fn="bsa_moe_bwd_workspace_bytes")
+    assert c > 0
+
+
+def test_python_call_raises_value_error_with_the_message():
+    with pytest.raises(ValueError, match="top-k"):
+        _lib.call("bsa_moe_experts_fwd", *_fwd_args(k=17))
