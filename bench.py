@@ -494,6 +494,9 @@ def main() -> int:
             "decode_t8": bench_moe(8, max(args.steps, 20), args.warmup, 0.5, seed=4),
             "decode_t64": bench_moe(64, max(args.steps, 20), args.warmup, 0.5, seed=4),
             "prefill_t8192": bench_moe(8192, max(args.steps // 4, 5), args.warmup, 0.0, seed=5),
+            # the same prefill on the native block-scaled MXFP4 matrix cores
+            # (MXFP8 activations), beside the dequant-to-bf16 path above
+            "prefill_t8192_mx": bench_moe(8192, max(args.steps // 4, 5), args.warmup, 0.0, seed=5, path="mx"),
         }
         if not args.no_cpu_baseline:
             moe["decode_t64"]["cpu_baseline"] = cpu_baseline_moe()
