@@ -185,7 +185,7 @@ def _median_ms(pairs):
 
 
 def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int,
-              path: str = "auto") -> dict:
+              path: str = "auto", layout: str = "checkpoint") -> dict:
     from blockstreamer_amd import kernels, synthetic
 
     dev = torch.device("cuda", 0)
@@ -195,6 +195,10 @@ def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int
     x = t["hidden"]
     args = tuple(t[n] for n in ("gate_up_proj_blocks", "gate_up_proj_scales", "gate_up_proj_bias",
                                 "down_proj_blocks", "down_proj_scales", "down_proj_bias"))
+    if layout == "kpair":
+        # the k-pair shard layout is an on-disk format: repacked once, before
+        # anything is timed
+        args = (kernels.to_kpair(args[0]),) + args[1:3] + (kernels.to_kpair(args[3]),) + args[4:]
 
     def route():
         # fused router kernel (logits, top-k, softmax over the top-k)
@@ -251,6 +255,7 @@ def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int
     hbm = wbytes / (gemm_ms / 1e3) / 1e9
     tfl = flops / (gemm_ms / 1e3) / 1e12
     res["path"] = path
+    res["layout"] = layout
     if T >= 4096 and path != "mx":
         # the LoRA training use: forward saving the gate_up pre-activations,
         # then the input-gradient backward (expert weights frozen)
@@ -291,7 +296,7 @@ def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int
                            "unit": "GB/s", "frac": round(hbm / HBM_PEAK_GBS, 4),
                            "kernel": "moe_stream_persist_kernel gate_up + down",
                            "algorithmic_bytes": wbytes}
-        if T == 64:
+        if T == 64 and layout == "checkpoint":
             gu_b = traffic_record("moe_layer_gptoss120b_decode_t64", "gate_up_hbm_bytes")
             dn_b = traffic_record("moe_layer_gptoss120b_decode_t64", "down_hbm_bytes")
             res["roofline"]["traffic"] = gu_b + dn_b if gu_b and dn_b else None
@@ -435,9 +440,9 @@ def focused(args) -> int:
     elif args.workload == "norm":
         res = {"norm": [bench_norm(t, reps=max(args.steps, 20)) for t in (64, 8192)]}
     elif args.workload == "moe_decode":
-        res = bench_moe(args.tokens, args.steps, args.warmup, 0.5, seed=4, path=args.path)
+        res = bench_moe(args.tokens, args.steps, args.warmup, 0.5, seed=4, path=args.path, layout=args.layout)
     else:
-        res = bench_moe(8192, args.steps, args.warmup, 0.0, seed=5, path=args.path)
+        res = bench_moe(8192, args.steps, args.warmup, 0.0, seed=5, path=args.path, layout=args.layout)
     print(json.dumps({"workload": args.workload, "steps": args.steps, "warmup": args.warmup, **res}),
           flush=True)
     return 0
@@ -458,6 +463,8 @@ def main() -> int:
                     help="expert GEMM kernel for the moe_decode / moe_prefill workloads")
     ap.add_argument("--tokens", type=int, default=64, choices=[1, 8, 64],
                     help="token batch of the moe_decode workload (the decode batches 1, 8 and 64)")
+    ap.add_argument("--layout", default="checkpoint", choices=["checkpoint", "kpair"],
+                    help="layout of the packed blocks for the moe_decode / moe_prefill workloads")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE layer measurements")
     args = ap.parse_args()
@@ -497,6 +504,12 @@ def main() -> int:
             # the same prefill on the native block-scaled MXFP4 matrix cores
             # (MXFP8 activations), beside the dequant-to-bf16 path above
             "prefill_t8192_mx": bench_moe(8192, max(args.steps // 4, 5), args.warmup, 0.0, seed=5, path="mx"),
+            # the same workloads with the blocks in the k-pair shard layout
+            "decode_t64_kpair": bench_moe(64, max(args.steps, 20), args.warmup, 0.5, seed=4, layout="kpair"),
+            "prefill_t8192_kpair": bench_moe(8192, max(args.steps // 4, 5), args.warmup, 0.0, seed=5,
+                                             layout="kpair"),
+            "prefill_t8192_mx_kpair": bench_moe(8192, max(args.steps // 4, 5), args.warmup, 0.0, seed=5,
+                                                path="mx", layout="kpair"),
         }
         if not args.no_cpu_baseline:
             moe["decode_t64"]["cpu_baseline"] = cpu_baseline_moe()

@@ -28,18 +28,23 @@ _SIGNATURES = {
     "bsa_version": [],
     "bsa_dequant_mxfp4": [_ptr, _ptr, _ptr, _int, _i64, _i64, _i64, _ptr],
     "bsa_dequant_mxfp4_mode": [_ptr, _ptr, _ptr, _int, _i64, _i64, _i64, _int, _ptr],
+    "bsa_dequant_mxfp4_layout": [_ptr, _ptr, _ptr, _int, _i64, _i64, _i64, _int, _int, _ptr],
+    "bsa_mxfp4_to_kpair": [_ptr, _ptr, _i64, _i64, _i64, _ptr],
+    "bsa_mxfp4_from_kpair": [_ptr, _ptr, _i64, _i64, _i64, _ptr],
     "bsa_moe_workspace_bytes": [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_i64)],
     "bsa_moe_experts_fwd": [
         _ptr, _i64, _i64, _i64, _i64, _i64,      # hidden, T, H, I, E, k
         _ptr, _ptr, _int,                        # indices, weights, weight dtype
         _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _int,  # gate_up b/s/bias, down b/s/bias, bias dtype
         _f32, _f32,                              # alpha, limit
-        _ptr, _int, _ptr, _i64, _ptr, _int, _ptr,  # out, out dtype, ws, ws bytes, save, path, stream
+        _ptr, _int, _ptr, _i64, _ptr, _int,       # out, out dtype, ws, ws bytes, save, path
+        _int, _ptr,                               # blocks layout, stream
     ],
     "bsa_moe_dispatch": [_ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr],
     "bsa_moe_gate_up": [_ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr, _int, _f32, _f32,
-                        _ptr, _i64, _ptr, _int, _ptr],
-    "bsa_moe_down": [_i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr, _int, _ptr, _i64, _int, _ptr],
+                        _ptr, _i64, _ptr, _int, _int, _ptr],
+    "bsa_moe_down": [_i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr, _int, _ptr, _i64, _int, _int,
+                     _ptr],
     "bsa_moe_combine": [_ptr, _ptr, _int, _i64, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _int,
                         _ptr],
     "bsa_router_fwd": [_ptr, _int, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr],
@@ -52,7 +57,7 @@ _SIGNATURES = {
         _ptr, _ptr, _ptr, _ptr,                    # gate_up b/s, down b/s
         _f32, _f32,                                # alpha, limit
         _ptr, _i64, _ptr, _ptr, _i64,              # ws, ws bytes, save, bwd ws, bwd bytes
-        _ptr, _int, _ptr, _ptr,                    # grad_hidden, dtype, grad_weights, stream
+        _ptr, _int, _ptr, _int, _ptr,              # grad_hidden, dtype, grad_weights, layout, stream
     ],
     "bsa_rmsnorm_fwd": [_ptr, _int, _i64, _i64, _ptr, _int, _f32, _ptr, _ptr],
     "bsa_rmsnorm_bwd": [_ptr, _ptr, _int, _i64, _i64, _ptr, _int, _f32, _ptr, _ptr],

@@ -159,6 +159,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 
+// Byte offset of 16-byte group g of packed row n from the start of row n0 of
+// the tensor (n0 a multiple of 16, rows counted across experts), G groups per
+// row.  Checkpoint layout [rows][G][16]; k-pair layout [rows/16][G/2][16][2]
+// [16]: 16-row bands, inside a band the groups two by two, each pair holding
+// the band's 16 rows.  A band occupies the same bytes in both layouts.
+__device__ __forceinline__ int64_t bq_off(int kp, int64_t n, int g, int G) {
+  return kp ? ((((n >> 4) * (G >> 1) + (g >> 1)) * 32 + (n & 15) * 2 + (g & 1)) * 16) : ((n * G + g) * 16);
+}
+
 // Activation / weight element types accepted by the kernels.
 enum DType : int { DT_BF16 = BSA_DTYPE_BF16, DT_F16 = BSA_DTYPE_F16, DT_F32 = BSA_DTYPE_F32 };
 

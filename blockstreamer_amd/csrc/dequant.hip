@@ -14,6 +14,8 @@
 // stores the 8 adjacent columns r..r+7 as one 16-byte store (for a fixed k,
 // 8 lanes write 128 contiguous bytes).  Everything is HBM-bound: 2.53 bytes
 // of traffic per bf16 output element.
+#include <algorithm>
+
 #include "bsa_common.h"
 
 namespace bsa {
@@ -87,7 +89,7 @@ template <int OUT, bool ALIGN16>
 __global__ __launch_bounds__(256) void dequant_vec_kernel(const uint8_t* __restrict__ blocks,
                                                           const uint8_t* __restrict__ scales,
                                                           void* __restrict__ out, int R, int G,
-                                                          int row_tiles, int mode) {
+                                                          int row_tiles, int mode, int kp) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int e = blockIdx.x / row_tiles;
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(256) void dequant_vec_kernel(const uint8_t* __restr
     for (int i = 0; i < 8; ++i) {
       if (active) {
         const size_t rg = (row0 + i) * G + g;
-        const uint8_t* p = blocks + rg * 16;
+        const uint8_t* p = blocks + bq_off(kp, (int64_t)(row0 + i), g, G);
         if constexpr (ALIGN16) {
           pk[i] = *reinterpret_cast<const u32x4_t*>(p);
         } else {
@@ -172,13 +174,18 @@ __global__ __launch_bounds__(256) void dequant_generic_kernel(const uint8_t* __r
 
 template <int OUT>
 static int launch_dequant(const uint8_t* blocks, const uint8_t* scales, void* out, int64_t E,
-                          int64_t R, int64_t G, int mode, hipStream_t stream) {
+                          int64_t R, int64_t G, int mode, int kp, hipStream_t stream) {
   const uintptr_t bp = reinterpret_cast<uintptr_t>(blocks);
   const uintptr_t op = reinterpret_cast<uintptr_t>(out);
   // The vectorised kernel decodes in whichever way `mode` asks (mode 1 makes
   // it take the integer decoder for every wave).
   const bool vec = (R % 8 == 0) && (op % 16 == 0) && (bp % 8 == 0) && R <= INT32_MAX / 2 &&
                    G <= INT32_MAX / 64;
+  // the k-pair layout is read by the vectorised kernel only
+  if (kp && !(vec && bp % 16 == 0)) {
+    set_error("dequant: the k-pair layout needs 16-byte aligned blocks and output");
+    return BSA_EINVAL;
+  }
   if (vec) {
     const int row_tiles = (int)((R + DQ_ROWS - 1) / DQ_ROWS);
     const int64_t nblk = E * row_tiles;
@@ -188,10 +195,10 @@ static int launch_dequant(const uint8_t* blocks, const uint8_t* scales, void* ou
     }
     if (bp % 16 == 0)
       hipLaunchKernelGGL((dequant_vec_kernel<OUT, true>), dim3((unsigned)nblk), dim3(256), 0,
-                         stream, blocks, scales, out, (int)R, (int)G, row_tiles, mode);
+                         stream, blocks, scales, out, (int)R, (int)G, row_tiles, mode, kp);
     else
       hipLaunchKernelGGL((dequant_vec_kernel<OUT, false>), dim3((unsigned)nblk), dim3(256), 0,
-                         stream, blocks, scales, out, (int)R, (int)G, row_tiles, mode);
+                         stream, blocks, scales, out, (int)R, (int)G, row_tiles, mode, 0);
   } else {
     const int64_t n = E * R * G * 16;
     int64_t nb = (n + 255) / 256;
@@ -203,11 +210,58 @@ static int launch_dequant(const uint8_t* blocks, const uint8_t* scales, void* ou
   return BSA_OK;
 }
 
+// Checkpoint <-> k-pair layout of packed blocks: one 16-byte group per
+// thread, i = row * G + g in checkpoint order (rows counted across experts;
+// R % 16 == 0 makes every band lie inside one expert).  Reads of the
+// checkpoint side are coalesced; the k-pair side is written (read) in
+// 32-byte pairs.
+template <bool TO_KP>
+__global__ __launch_bounds__(256) void kpair_repack_kernel(const u32x4_t* __restrict__ in,
+                                                           u32x4_t* __restrict__ out, int64_t rows, int G) {
+  const int64_t n = rows * G;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / G;
+    const int g = (int)(i - r * G);
+    const int64_t k = bq_off(1, r, g, G) >> 4;
+    if constexpr (TO_KP)
+      out[k] = in[i];
+    else
+      out[i] = in[k];
+  }
+}
+
+static int kpair_repack(const void* blocks, void* out, int64_t E, int64_t R, int64_t G, void* stream,
+                        bool to_kp, const char* what) {
+  clear_error();
+  BSA_REQUIRE(E >= 0 && R >= 0 && G >= 0, "%s: negative shape E=%lld R=%lld G=%lld", what, (long long)E,
+              (long long)R, (long long)G);
+  BSA_REQUIRE(R % 16 == 0 && G % 2 == 0 && G <= INT32_MAX,
+              "%s: needs rows %% 16 == 0 and an even group count (R=%lld G=%lld)", what, (long long)R,
+              (long long)G);
+  if (E == 0 || R == 0 || G == 0) return BSA_OK;
+  BSA_REQUIRE(blocks && out, "%s: null pointer", what);
+  BSA_REQUIRE(blocks != out, "%s: input and output must be distinct buffers", what);
+  BSA_REQUIRE(reinterpret_cast<uintptr_t>(blocks) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0,
+              "%s: blocks and out must be 16-byte aligned", what);
+  BSA_REQUIRE(E <= INT64_MAX / 16 / (R * G), "%s: size overflow", what);
+  const int64_t n = E * R * G;
+  const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, 65536);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const u32x4_t* in = static_cast<const u32x4_t*>(blocks);
+  u32x4_t* o = static_cast<u32x4_t*>(out);
+  if (to_kp)
+    hipLaunchKernelGGL(kpair_repack_kernel<true>, dim3(grid), dim3(256), 0, st, in, o, E * R, (int)G);
+  else
+    hipLaunchKernelGGL(kpair_repack_kernel<false>, dim3(grid), dim3(256), 0, st, in, o, E * R, (int)G);
+  BSA_LAUNCH_CHECK("k-pair repack launch");
+  return BSA_OK;
+}
+
 }  // namespace bsa
 
-extern "C" int bsa_dequant_mxfp4_mode(const void* blocks, const void* scales, void* out,
-                                      int out_dtype, int64_t E, int64_t R, int64_t G, int mode,
-                                      void* stream) {
+extern "C" int bsa_dequant_mxfp4_layout(const void* blocks, const void* scales, void* out,
+                                        int out_dtype, int64_t E, int64_t R, int64_t G, int mode,
+                                        int blocks_layout, void* stream) {
   using namespace bsa;
   clear_error();
   BSA_REQUIRE(E >= 0 && R >= 0 && G >= 0, "dequant: negative shape E=%lld R=%lld G=%lld",
@@ -215,20 +269,40 @@ extern "C" int bsa_dequant_mxfp4_mode(const void* blocks, const void* scales, vo
   BSA_REQUIRE(mode >= 0 && mode <= 2, "dequant: mode must be 0, 1 or 2 (got %d)", mode);
   BSA_REQUIRE(out_dtype == DT_BF16 || out_dtype == DT_F16 || out_dtype == DT_F32,
               "dequant: unsupported output dtype %d", out_dtype);
+  BSA_REQUIRE(blocks_layout == BSA_LAYOUT_CHECKPOINT || blocks_layout == BSA_LAYOUT_KPAIR,
+              "dequant: unknown blocks layout %d", blocks_layout);
+  BSA_REQUIRE(blocks_layout == BSA_LAYOUT_CHECKPOINT || (R % 16 == 0 && G % 2 == 0),
+              "dequant: the k-pair layout needs rows %% 16 == 0 and an even group count (R=%lld G=%lld)",
+              (long long)R, (long long)G);
   if (E == 0 || R == 0 || G == 0) return BSA_OK;
   BSA_REQUIRE(blocks && scales && out, "dequant: null pointer");
   BSA_REQUIRE(E <= INT64_MAX / 16 / (R * G) , "dequant: size overflow");
   const uint8_t* b = static_cast<const uint8_t*>(blocks);
   const uint8_t* s = static_cast<const uint8_t*>(scales);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const int kp = blocks_layout == BSA_LAYOUT_KPAIR;
   switch (out_dtype) {
-    case DT_BF16: return launch_dequant<DT_BF16>(b, s, out, E, R, G, mode, st);
-    case DT_F16: return launch_dequant<DT_F16>(b, s, out, E, R, G, mode, st);
-    default: return launch_dequant<DT_F32>(b, s, out, E, R, G, mode, st);
+    case DT_BF16: return launch_dequant<DT_BF16>(b, s, out, E, R, G, mode, kp, st);
+    case DT_F16: return launch_dequant<DT_F16>(b, s, out, E, R, G, mode, kp, st);
+    default: return launch_dequant<DT_F32>(b, s, out, E, R, G, mode, kp, st);
   }
+}
+
+extern "C" int bsa_dequant_mxfp4_mode(const void* blocks, const void* scales, void* out,
+                                      int out_dtype, int64_t E, int64_t R, int64_t G, int mode,
+                                      void* stream) {
+  return bsa_dequant_mxfp4_layout(blocks, scales, out, out_dtype, E, R, G, mode, BSA_LAYOUT_CHECKPOINT, stream);
 }
 
 extern "C" int bsa_dequant_mxfp4(const void* blocks, const void* scales, void* out,
                                  int out_dtype, int64_t E, int64_t R, int64_t G, void* stream) {
   return bsa_dequant_mxfp4_mode(blocks, scales, out, out_dtype, E, R, G, 0, stream);
+}
+
+extern "C" int bsa_mxfp4_to_kpair(const void* blocks, void* out, int64_t E, int64_t R, int64_t G, void* stream) {
+  return bsa::kpair_repack(blocks, out, E, R, G, stream, true, "to k-pair layout");
+}
+
+extern "C" int bsa_mxfp4_from_kpair(const void* blocks, void* out, int64_t E, int64_t R, int64_t G, void* stream) {
+  return bsa::kpair_repack(blocks, out, E, R, G, stream, false, "from k-pair layout");
 }

@@ -12,6 +12,9 @@
 // weight [E][N][K/32][16] (+ E8M0 scales [E][N][K/32]): row n of the packed
 // tensor holds output column n with K contiguous, which is exactly the
 // per-lane layout of an MFMA B operand, so no transpose is ever needed.
+// The same blocks may come in the k-pair shard layout (GemmArgs::kp,
+// bq_off): every kernel only changes where it reads each 16-byte group from,
+// the LDS contents and the results are the same bit for bit.
 //
 // Kernels:
 //  * moe_stream_persist_kernel (decode, K = 2880): persistent workgroups,
@@ -74,7 +77,7 @@ struct GemmArgs {
   int64_t lda;
   const int* row_pair;   // non-null: A row of sorted row pos is row_pair[pos] / topk
   int topk;
-  const uint8_t* Bq;     // packed [E][N][K/32][16]
+  const uint8_t* Bq;     // packed [E][N][K/32][16], or the k-pair layout when kp (below)
   const uint8_t* Bs;     // scales [E][N][K/32]
   const void* bias;      // [E][N] or null
   int bias_dtype;
@@ -92,7 +95,9 @@ struct GemmArgs {
   const uint8_t* Aq;     // MX path: E4M3 activations, row stride ldq bytes
   const uint8_t* As;     // MX path: E8M0 activation scales, row stride ldas bytes (% 4 == 0)
   int64_t ldq, ldas;
+  int kp;                // Bq in the k-pair layout [E][N/16][K/64][16][2][16]
 };
+
 
 typedef __attribute__((ext_vector_type(8))) short s16x8_t;
 typedef __attribute__((ext_vector_type(8))) int i32x8_t;
@@ -407,9 +412,11 @@ __device__ __forceinline__ void st_kloop(const GemmArgs& a, const uint8_t* sB, c
 #pragma unroll
     for (int m = 0; m < 4; ++m) dst[m] = p[m];
   };
-  // LDS byte offsets of this lane's two weight rows, group c
-  const uint32_t boff0 = (uint32_t)((col * G + c) * 16);
-  const uint32_t boff1 = (uint32_t)(((16 + col) * G + c) * 16);
+  // LDS byte offsets of this lane's two weight rows, group c (the slice is
+  // the tensor's bytes as they are), and the advance per 4-group step
+  const uint32_t boff0 = (uint32_t)bq_off(a.kp, col, c, G);
+  const uint32_t boff1 = (uint32_t)bq_off(a.kp, 16 + col, c, G);
+  const uint32_t bstep = a.kp ? 1024u : 64u;
   const uint32_t soff0 = (uint32_t)(col * G + c);
   const uint32_t soff1 = (uint32_t)((16 + col) * G + c);
   if (wave < nsteps) loadA(wave, an);
@@ -419,8 +426,8 @@ __device__ __forceinline__ void st_kloop(const GemmArgs& a, const uint8_t* sB, c
     for (int m = 0; m < 4; ++m) ac[m] = an[m];
     if (step + 4 < nsteps) loadA(step + 4, an);
     const uint32_t gofs = (uint32_t)(step * 4);
-    u32x4_t q0 = *reinterpret_cast<const u32x4_t*>(sB + boff0 + gofs * 16);
-    u32x4_t q1 = *reinterpret_cast<const u32x4_t*>(sB + boff1 + gofs * 16);
+    u32x4_t q0 = *reinterpret_cast<const u32x4_t*>(sB + boff0 + step * bstep);
+    u32x4_t q1 = *reinterpret_cast<const u32x4_t*>(sB + boff1 + step * bstep);
     uint32_t s0 = sS[soff0 + gofs];
     uint32_t s1 = sS[soff1 + gofs];
     if (!full_last && step == nsteps - 1 && 4 * step + c >= G) {
@@ -604,18 +611,18 @@ __global__ __launch_bounds__(256, 3) void moe_stream_parts_kernel(GemmArgs a) {
   // part p, piece i (2 per wave): rows 4i .. 4i+3, lane -> row 4i + lane/16,
   // slot lane%16 holding group 16p + ((lane%16) ^ (row%16)); groups past G
   // read group 0 (never used)
-  auto issue_part = [](const uint8_t* gb, uint8_t* sb, int p, int wv, int ln) {
+  auto issue_part = [](const uint8_t* gb, uint8_t* sb, int p, int wv, int ln, int kp) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int i = 2 * wv + j;
       const int row = 4 * i + (ln >> 4);
       const int g = 16 * p + ((ln & 15) ^ (row & 15));
-      __builtin_amdgcn_global_load_lds(gb + ((int64_t)row * G + (g < G ? g : 0)) * 16,
+      __builtin_amdgcn_global_load_lds(gb + bq_off(kp, row, g < G ? g : 0, G),
                                        (lds_void*)(sb + p * PART + i * 1024), 16, 0, 0);
     }
   };
 #pragma unroll
-  for (int p = 0; p < NPART; ++p) issue_part(gB, sB, p, wave, lane);
+  for (int p = 0; p < NPART; ++p) issue_part(gB, sB, p, wave, lane, a.kp);
 
   // LDS offsets of this lane's two rows (col, 16 + col) for its step of any
   // part: slot (4*wave + c) ^ col
@@ -626,7 +633,7 @@ __global__ __launch_bounds__(256, 3) void moe_stream_parts_kernel(GemmArgs a) {
     if (pass0 > 0) {
       // part 0 held the reduction: reload it, and the A rows of this pass
       load_a(a, row0, cnt, pass0, col, c, wave, an);
-      issue_part(gB, sB, 0, wave, lane);
+      issue_part(gB, sB, 0, wave, lane, a.kp);
       wait_vmcnt<0>();
       asm volatile("s_barrier" ::: "memory");
     }
@@ -778,7 +785,7 @@ __device__ __forceinline__ void ps_issue(const GemmArgs& a, uint8_t* sb, int e, 
   const int sl = (lane & 15) ^ row;
 #pragma unroll
   for (int p = 0; p < C::NP; ++p) {
-    const uint8_t* src = gB + (row * G + 16 * p + sl) * 16;
+    const uint8_t* src = gB + bq_off(a.kp, row, 16 * p + sl, G);
     if (p == C::NP - 1 && 16 * p + sl >= G) {
       // a spare slot: scale chunk j, then the bias chunks, else anything valid
       const int j = row * C::UN + (16 * p + sl - G);
@@ -1257,7 +1264,8 @@ __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
   const int brr = tid >> 1;
   const int bgs = tid & 1;
   const bool bok = n0 + brr < a.N;
-  const uint8_t* bq = a.Bq + ((int64_t)e * a.N + (bok ? n0 + brr : 0)) * G * 16 + bgs * 16;
+  const uint8_t* bq = a.Bq + (int64_t)e * a.N * G * 16 + bq_off(a.kp, bok ? n0 + brr : 0, bgs, G);
+  const int bkt = a.kp ? 512 : 32;  // bytes per k-tile (two groups) along a row
   const uint8_t* bs = a.Bs + ((int64_t)e * a.N + (bok ? n0 + brr : 0)) * G + bgs;
   const int bcol = (EPI == EPI_SWIGLU) ? ((brr & 1) ? 64 + (brr >> 1) : (brr >> 1)) : brr;
 
@@ -1269,7 +1277,7 @@ __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
     for (int i = 0; i < 4; ++i)
       ra[i] = aok[i] ? *reinterpret_cast<const u32x4_t*>(aptr[i] + kt * TL_BK)
                      : u32x4_t{0u, 0u, 0u, 0u};
-    rb = bok ? load16<ALIGN16>(bq + kt * 32) : u32x4_t{0u, 0u, 0u, 0u};
+    rb = bok ? load16<ALIGN16>(bq + kt * bkt) : u32x4_t{0u, 0u, 0u, 0u};
     rs = bok ? (uint32_t)bs[kt * 2] : 127u;
   };
   auto lstore = [&](int buf) {
@@ -1502,8 +1510,9 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
     const int q = 32 * (2 * wave + h2) + (lane >> 1);
     const bool ok = n0 + q < a.N;
     const int grp = (lane & 1) ^ ((q >> 3) & 1);
-    bsrc[h2] = a.Bq + ((int64_t)e * a.N + (ok ? n0 + q : n0)) * G * 16 + grp * 16;
+    bsrc[h2] = a.Bq + (int64_t)e * a.N * G * 16 + bq_off(a.kp, ok ? n0 + q : n0, grp, G);
   }
+  const int bkt = a.kp ? 512 : 32;  // bytes per k-tile (two groups) along a row
   uint8_t* sbs = smem + T2_NS * T2_STAGE;
   preload_b_scales<SB16, T2_BN, 4>(a.Bs, e, a.N, n0, G, sbs, wave, lane);
 
@@ -1515,7 +1524,7 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
                                        (lds_void*)(st + (4 * wave + i) * 1024), 16, 0, 0);
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2)
-      __builtin_amdgcn_global_load_lds(bsrc[h2] + kt * 32,
+      __builtin_amdgcn_global_load_lds(bsrc[h2] + kt * bkt,
                                        (lds_void*)(st + T2_A_BYTES + (2 * wave + h2) * 1024), 16, 0, 0);
   };
 
@@ -1649,8 +1658,8 @@ __device__ __forceinline__ int64_t tile_src_row(const GemmArgs& a, int m0, int r
 // host-side handle of these kernel templates when their bodies call a
 // capturing lambda.
 template <int WN, int NBW, int MX_NS>
-__device__ __forceinline__ void mx_issue(uint8_t* smem, int kt, int wave,
-                                         const uint8_t* const* asrc, const uint8_t* const* bsrc) {
+__device__ __forceinline__ void mx_issue(uint8_t* smem, int kt, int wave, const uint8_t* const* asrc,
+                                         const uint8_t* const* bsrc, int bkt) {
   using C = MxCfg<WN, NBW>;
   uint8_t* st = smem + (kt % MX_NS) * C::STAGE;
 #pragma unroll
@@ -1659,7 +1668,7 @@ __device__ __forceinline__ void mx_issue(uint8_t* smem, int kt, int wave,
                                      16, 0, 0);
 #pragma unroll
   for (int h = 0; h < C::B_DMA; ++h)
-    __builtin_amdgcn_global_load_lds(bsrc[h] + kt * 32,
+    __builtin_amdgcn_global_load_lds(bsrc[h] + kt * bkt,
                                      (lds_void*)(st + MX_A_BYTES + (C::B_DMA * wave + h) * 1024), 16, 0, 0);
 }
 
@@ -1735,8 +1744,9 @@ __global__ __launch_bounds__(64 * WN, NBW == 2 ? 2 : 1) void moe_mx_kernel(GemmA
     const int q = 32 * (C::B_DMA * wave + h) + (lane >> 1);
     const bool ok = n0 + q < a.N;
     const int grp = (lane & 1) ^ ((q >> 3) & 1);
-    bsrc[h] = a.Bq + ((int64_t)e * a.N + (ok ? n0 + q : n0)) * G * 16 + grp * 16;
+    bsrc[h] = a.Bq + (int64_t)e * a.N * G * 16 + bq_off(a.kp, ok ? n0 + q : n0, grp, G);
   }
+  const int bkt = a.kp ? 512 : 32;  // bytes per k-tile (two groups) along a row
 
   // this lane's B rows (one per 32-column block) and their bias
   int bq[NBW];
@@ -1766,13 +1776,13 @@ __global__ __launch_bounds__(64 * WN, NBW == 2 ? 2 : 1) void moe_mx_kernel(GemmA
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
   for (int i = 0; i < MX_NS - 1; ++i)
-    if (i < KT) mx_issue<WN, NBW, MX_NS>(smem, i, wave, asrc, bsrc);
+    if (i < KT) mx_issue<WN, NBW, MX_NS>(smem, i, wave, asrc, bsrc, bkt);
   for (int kt = 0; kt < KT; ++kt) {
     // tile kt (and, on the first pass, the scales issued before it) has
     // landed once at most the tiles issued after it are in flight
     wait_tiles_ahead<C::DMA_PER_TILE, MX_NS - 2>(min(MX_NS - 2, KT - 1 - kt));
     asm volatile("s_barrier" ::: "memory");
-    if (kt + MX_NS - 1 < KT) mx_issue<WN, NBW, MX_NS>(smem, kt + MX_NS - 1, wave, asrc, bsrc);
+    if (kt + MX_NS - 1 < KT) mx_issue<WN, NBW, MX_NS>(smem, kt + MX_NS - 1, wave, asrc, bsrc, bkt);
     const uint8_t* st = smem + (kt % MX_NS) * C::STAGE;
     int sb[NBW];
     i32x8_t bop[NBW];
@@ -1941,7 +1951,7 @@ struct BtSrc {
       for (int j = 0; j < 4; ++j) {
         const int r = 4 * (4 * wave + j) + (lane >> 4);
         const int c = (lane & 15) ^ (r & 15);
-        q[j] = ((wrow0 + r) * NB + nt * 16 + (c < qvalid ? c : 0)) * 16;  // past N: any chunk
+        q[j] = bq_off(a.kp, wrow0 + r, nt * 16 + (c < qvalid ? c : 0), NB);  // past N: any chunk
       }
       // rows 16 wave .. +15, two chunks each; lanes 32..63 repeat 0..31
       const int r = 16 * wave + ((lane & 31) >> 1);
@@ -2437,10 +2447,26 @@ static int stage_dispatch(const MoeShape& m, const int64_t* idx, const Workspace
                          w.pair_pos, w.tiles, w.num_tiles, reinterpret_cast<int*>(w.act), st);
 }
 
+// blocks_layout of one packed weight with `rows` rows of K/32 groups.
+static int check_layout(int layout, const void* blocks, const void* scales, int64_t rows, int64_t K,
+                        const char* what) {
+  BSA_REQUIRE(layout == BSA_LAYOUT_CHECKPOINT || layout == BSA_LAYOUT_KPAIR, "%s: unknown blocks layout %d", what,
+              layout);
+  if (layout == BSA_LAYOUT_KPAIR) {
+    BSA_REQUIRE(rows % 16 == 0 && (K / 32) % 2 == 0,
+                "%s: the k-pair layout needs rows %% 16 == 0 and an even group count (rows=%lld K=%lld)", what,
+                (long long)rows, (long long)K);
+    BSA_REQUIRE(reinterpret_cast<uintptr_t>(blocks) % 16 == 0 && reinterpret_cast<uintptr_t>(scales) % 16 == 0,
+                "%s: the k-pair layout needs 16-byte aligned blocks and scales", what);
+  }
+  return BSA_OK;
+}
+
 static int stage_gate_up(const MoeShape& m, const void* hidden, const void* blocks, const void* scales,
                          const void* bias, int bias_dtype, float alpha, float limit, const Workspace& w,
-                         void* save_gate_up, int path, hipStream_t st) {
+                         void* save_gate_up, int path, int layout, hipStream_t st) {
   GemmArgs g{};
+  g.kp = layout == BSA_LAYOUT_KPAIR;
   g.A = static_cast<const uint16_t*>(hidden);
   g.lda = m.H;
   g.row_pair = w.row_pair;
@@ -2479,8 +2505,9 @@ static int stage_gate_up(const MoeShape& m, const void* hidden, const void* bloc
 }
 
 static int stage_down(const MoeShape& m, const void* blocks, const void* scales, const void* bias,
-                      int bias_dtype, const Workspace& w, int path, hipStream_t st) {
+                      int bias_dtype, const Workspace& w, int path, int layout, hipStream_t st) {
   GemmArgs g{};
+  g.kp = layout == BSA_LAYOUT_KPAIR;
   g.A = w.act;
   g.lda = m.I;
   g.row_pair = nullptr;
@@ -2538,7 +2565,8 @@ extern "C" int bsa_moe_dispatch(const int64_t* router_indices, int64_t T, int64_
 extern "C" int bsa_moe_gate_up(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E,
                                int64_t k, const void* blocks, const void* scales, const void* bias,
                                int bias_dtype, float alpha, float limit, void* workspace,
-                               int64_t workspace_bytes, void* save_gate_up, int path, void* stream) {
+                               int64_t workspace_bytes, void* save_gate_up, int path, int blocks_layout,
+                               void* stream) {
   clear_error();
   const MoeShape m{T, H, I, E, k};
   int rc = check_shape(m, "gate_up");
@@ -2547,16 +2575,17 @@ extern "C" int bsa_moe_gate_up(const void* hidden, int64_t T, int64_t H, int64_t
   BSA_REQUIRE(dtype_ok(bias_dtype) && path >= 0 && path <= 3, "gate_up: bad dtype or path");
   BSA_REQUIRE(reinterpret_cast<uintptr_t>(hidden) % 16 == 0 && reinterpret_cast<uintptr_t>(blocks) % 8 == 0,
               "gate_up: hidden must be 16-byte and blocks 8-byte aligned");
+  if ((rc = check_layout(blocks_layout, blocks, scales, 2 * I, H, "gate_up"))) return rc;
   Workspace w;
   if ((rc = check_ws(m, workspace, workspace_bytes, &w, "gate_up"))) return rc;
   return stage_gate_up(m, hidden, blocks, scales, bias, bias_dtype, alpha, limit, w, save_gate_up,
-                       path, static_cast<hipStream_t>(stream));
+                       path, blocks_layout, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int bsa_moe_down(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
                             const void* blocks, const void* scales, const void* bias,
                             int bias_dtype, void* workspace, int64_t workspace_bytes, int path,
-                            void* stream) {
+                            int blocks_layout, void* stream) {
   clear_error();
   const MoeShape m{T, H, I, E, k};
   int rc = check_shape(m, "down");
@@ -2564,9 +2593,10 @@ extern "C" int bsa_moe_down(int64_t T, int64_t H, int64_t I, int64_t E, int64_t 
   BSA_REQUIRE(blocks && scales, "down: null pointer");
   BSA_REQUIRE(dtype_ok(bias_dtype) && path >= 0 && path <= 3, "down: bad dtype or path");
   BSA_REQUIRE(reinterpret_cast<uintptr_t>(blocks) % 8 == 0, "down: blocks must be 8-byte aligned");
+  if ((rc = check_layout(blocks_layout, blocks, scales, H, I, "down"))) return rc;
   Workspace w;
   if ((rc = check_ws(m, workspace, workspace_bytes, &w, "down"))) return rc;
-  return stage_down(m, blocks, scales, bias, bias_dtype, w, path, static_cast<hipStream_t>(stream));
+  return stage_down(m, blocks, scales, bias, bias_dtype, w, path, blocks_layout, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int bsa_moe_combine(const int64_t* router_indices, const void* routing_weights,
@@ -2591,7 +2621,7 @@ extern "C" int bsa_moe_experts_fwd(
     const void* gate_up_blocks, const void* gate_up_scales, const void* gate_up_bias,
     const void* down_blocks, const void* down_scales, const void* down_bias, int bias_dtype,
     float alpha, float limit, void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
-    void* save_gate_up, int path, void* stream) {
+    void* save_gate_up, int path, int blocks_layout, void* stream) {
   clear_error();
   const MoeShape m{T, H, I, E, k};
   int rc = check_shape(m, "experts fwd");
@@ -2606,14 +2636,18 @@ extern "C" int bsa_moe_experts_fwd(
   BSA_REQUIRE(reinterpret_cast<uintptr_t>(gate_up_blocks) % 8 == 0 &&
                   reinterpret_cast<uintptr_t>(down_blocks) % 8 == 0,
               "experts fwd: packed blocks must be 8-byte aligned");
+  if ((rc = check_layout(blocks_layout, gate_up_blocks, gate_up_scales, 2 * I, H, "experts fwd (gate_up)")) ||
+      (rc = check_layout(blocks_layout, down_blocks, down_scales, H, I, "experts fwd (down)")))
+    return rc;
   Workspace w;
   if ((rc = check_ws(m, workspace, workspace_bytes, &w, "experts fwd"))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if ((rc = stage_dispatch(m, router_indices, w, st))) return rc;
   if ((rc = stage_gate_up(m, hidden, gate_up_blocks, gate_up_scales, gate_up_bias, bias_dtype, alpha,
-                          limit, w, save_gate_up, path, st)))
+                          limit, w, save_gate_up, path, blocks_layout, st)))
     return rc;
-  if ((rc = stage_down(m, down_blocks, down_scales, down_bias, bias_dtype, w, path, st))) return rc;
+  if ((rc = stage_down(m, down_blocks, down_scales, down_bias, bias_dtype, w, path, blocks_layout, st)))
+    return rc;
   return launch_combine(w.y, router_indices, routing_weights, weight_dtype, w.pair_pos, (int)T,
                         (int)k, (int)H, out, out_dtype, st);
 }
@@ -2663,7 +2697,7 @@ extern "C" int bsa_moe_experts_bwd(
     const void* gate_up_blocks, const void* gate_up_scales, const void* down_blocks,
     const void* down_scales, float alpha, float limit, void* workspace, int64_t workspace_bytes,
     const void* save_gate_up, void* bwd_workspace, int64_t bwd_workspace_bytes, void* grad_hidden,
-    int grad_hidden_dtype, float* grad_weights, void* stream) {
+    int grad_hidden_dtype, float* grad_weights, int blocks_layout, void* stream) {
   clear_error();
   const MoeShape m{T, H, I, E, k};
   int rc = check_shape(m, "experts bwd");
@@ -2685,6 +2719,9 @@ extern "C" int bsa_moe_experts_bwd(
   BSA_REQUIRE(al(gate_up_blocks, 4) && al(gate_up_scales, 4) && al(down_blocks, 4) && al(down_scales, 4),
               "experts bwd: gate_up/down blocks and scales must be 4-byte aligned");
   BSA_REQUIRE(al(save_gate_up, 16), "experts bwd: save_gate_up must be 16-byte aligned");
+  if ((rc = check_layout(blocks_layout, gate_up_blocks, gate_up_scales, 2 * I, H, "experts bwd (gate_up)")) ||
+      (rc = check_layout(blocks_layout, down_blocks, down_scales, H, I, "experts bwd (down)")))
+    return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t P = T * k;
 
@@ -2732,6 +2769,7 @@ extern "C" int bsa_moe_experts_bwd(
   g.Bs = static_cast<const uint8_t*>(down_scales);
   g2.Bq = static_cast<const uint8_t*>(gate_up_blocks);
   g2.Bs = static_cast<const uint8_t*>(gate_up_scales);
+  g.kp = g2.kp = blocks_layout == BSA_LAYOUT_KPAIR;
   BSA_REQUIRE(bwd_packed_ok(g) && bwd_packed_ok(g2), "experts bwd: unsupported operand layout");
   if ((rc = launch_gemm_packed_rows<EPI_SWIGLU_BWD>(g, P, st))) return rc;
   if ((rc = launch_gemm_packed_rows<EPI_STORE>(g2, P, st))) return rc;

@@ -20,31 +20,86 @@ def _as_u8(t: Tensor) -> Tensor:
     return t if t.is_contiguous() else t.contiguous()
 
 
+# Layouts of packed MXFP4 blocks (scales are always [E, rows, groups]):
+# checkpoint [E, rows, groups, 16], and the k-pair shard layout
+# [E, rows/16, groups/2, 16, 2, 16] (group g of row r at [e][r/16][g/2][r%16][g%2]).
+LAYOUT_CHECKPOINT, LAYOUT_KPAIR = 0, 1
+
+
+def blocks_layout(blocks: Tensor) -> int:
+    """The layout of a packed blocks tensor, from its shape."""
+    if blocks.dim() == 4 and blocks.shape[-1] == 16:
+        return LAYOUT_CHECKPOINT
+    if blocks.dim() == 6 and tuple(blocks.shape[3:]) == (16, 2, 16):
+        return LAYOUT_KPAIR
+    raise ValueError(
+        f"packed blocks must be [E, rows, groups, 16] or the k-pair layout "
+        f"[E, rows/16, groups/2, 16, 2, 16], got {tuple(blocks.shape)}"
+    )
+
+
+def packed_shape(blocks: Tensor) -> tuple[int, int, int]:
+    """``(E, rows, groups)`` of a packed blocks tensor in either layout."""
+    if blocks_layout(blocks) == LAYOUT_CHECKPOINT:
+        E, R, G, _ = blocks.shape
+        return E, R, G
+    E, bands, pairs = blocks.shape[:3]
+    return E, bands * 16, pairs * 2
+
+
+def to_kpair(blocks: Tensor) -> Tensor:
+    """Checkpoint-layout blocks ``[E, R, G, 16]`` in the k-pair layout
+    ``[E, R/16, G/2, 16, 2, 16]`` (R % 16 == 0, G even), bit for bit."""
+    return _repack(blocks, to_kp=True)
+
+
+def from_kpair(blocks: Tensor) -> Tensor:
+    """The inverse of ``to_kpair``."""
+    return _repack(blocks, to_kp=False)
+
+
+def _repack(blocks: Tensor, to_kp: bool) -> Tensor:
+    want = LAYOUT_CHECKPOINT if to_kp else LAYOUT_KPAIR
+    if blocks_layout(blocks) != want:
+        raise ValueError(f"expected {'checkpoint' if to_kp else 'k-pair'} layout blocks, got {tuple(blocks.shape)}")
+    E, R, G = packed_shape(blocks)
+    if R % 16 or G % 2:
+        raise ValueError(f"the k-pair layout needs rows % 16 == 0 and an even group count (rows={R}, groups={G})")
+    dev = _lib.require_gpu(blocks)
+    src = _aligned(_as_u8(blocks), 16)
+    shape = (E, R // 16, G // 2, 16, 2, 16) if to_kp else (E, R, G, 16)
+    out = torch.empty(shape, dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("bsa_mxfp4_to_kpair" if to_kp else "bsa_mxfp4_from_kpair", src.data_ptr(), out.data_ptr(),
+                  E, R, G, _lib.stream_handle(dev))
+    return out
+
+
 def dequantize_mxfp4(blocks: Tensor, scales: Tensor, dtype: torch.dtype = torch.bfloat16,
                      out: Tensor | None = None, mode: int = 0) -> Tensor:
-    """Dense ``[E, G*32, R]`` weights from packed ``[E, R, G, 16]`` MXFP4.
+    """Dense ``[E, G*32, R]`` weights from packed ``[E, R, G, 16]`` MXFP4
+    (or the same blocks in the k-pair layout).
 
     The transformers ``convert_moe_packed_tensors`` contract for a 4-D input
     (TF/integrations/mxfp4.py:257-313): bit-exact in bf16/f16/f32.
     """
-    if blocks.dim() != 4 or blocks.shape[-1] != 16:
-        raise ValueError(f"packed blocks must be [E, rows, groups, 16], got {tuple(blocks.shape)}")
-    if tuple(scales.shape) != tuple(blocks.shape[:-1]):
-        raise ValueError(
-            f"scales shape {tuple(scales.shape)} does not match blocks {tuple(blocks.shape[:-1])}"
-        )
+    layout = blocks_layout(blocks)
+    E, R, G = packed_shape(blocks)
+    if tuple(scales.shape) != (E, R, G):
+        raise ValueError(f"scales shape {tuple(scales.shape)} does not match blocks {(E, R, G)}")
     code = _lib.dtype_code(dtype)
     dev = _lib.require_gpu(blocks, scales)
     blocks = _as_u8(blocks)
     scales = _as_u8(scales)
-    E, R, G, _ = blocks.shape
+    if layout == LAYOUT_KPAIR:
+        blocks = _aligned(blocks, 16)
     if out is None:
         out = torch.empty((E, G * 32, R), dtype=dtype, device=dev)
     elif out.shape != (E, G * 32, R) or out.dtype != dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous [E, G*32, R] tensor of the requested dtype")
     with torch.cuda.device(dev):
-        _lib.call("bsa_dequant_mxfp4_mode", blocks.data_ptr(), scales.data_ptr(), out.data_ptr(),
-                  code, E, R, G, mode, _lib.stream_handle(dev))
+        _lib.call("bsa_dequant_mxfp4_layout", blocks.data_ptr(), scales.data_ptr(), out.data_ptr(),
+                  code, E, R, G, mode, layout, _lib.stream_handle(dev))
     return out
 
 
@@ -94,12 +149,26 @@ def _aligned_bytes(nbytes: int, device, align: int = 256) -> Tensor:
     return buf[off:off + nbytes]
 
 
-def _check_packed(blocks: Tensor, scales: Tensor, E: int, rows: int, K: int, what: str) -> None:
-    want = (E, rows, K // 32, 16)
-    if tuple(blocks.shape) != want:
-        raise ValueError(f"{what}_blocks must be {list(want)}, got {list(blocks.shape)}")
-    if tuple(scales.shape) != want[:3]:
-        raise ValueError(f"{what}_scales must be {list(want[:3])}, got {list(scales.shape)}")
+def _check_packed(blocks: Tensor, scales: Tensor, E: int, rows: int, K: int, what: str) -> int:
+    """Checks the shapes; returns the blocks' layout."""
+    want = (E, rows, K // 32)
+    try:
+        layout = blocks_layout(blocks)
+        got = packed_shape(blocks)
+    except ValueError:
+        layout, got = -1, None
+    if got != want:
+        raise ValueError(f"{what}_blocks must be {list(want) + [16]} (or that in the k-pair layout), "
+                         f"got {list(blocks.shape)}")
+    if tuple(scales.shape) != want:
+        raise ValueError(f"{what}_scales must be {list(want)}, got {list(scales.shape)}")
+    return layout
+
+
+def _experts_dims(gate_up_blocks: Tensor) -> tuple[int, int]:
+    """``(E, I)`` from the gate_up blocks in either layout."""
+    E, rows, _ = packed_shape(gate_up_blocks)
+    return E, rows // 2
 
 
 def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights: Tensor,
@@ -123,10 +192,10 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
         raise ValueError("routing_weights must match router_indices in shape")
     T, H = hidden.shape
     k = router_indices.shape[1]
-    E = gate_up_blocks.shape[0]
-    I = gate_up_blocks.shape[1] // 2
-    _check_packed(gate_up_blocks, gate_up_scales, E, 2 * I, H, "gate_up_proj")
-    _check_packed(down_blocks, down_scales, E, H, I, "down_proj")
+    E, I = _experts_dims(gate_up_blocks)
+    layout = _check_packed(gate_up_blocks, gate_up_scales, E, 2 * I, H, "gate_up_proj")
+    if _check_packed(down_blocks, down_scales, E, H, I, "down_proj") != layout:
+        raise ValueError("gate_up and down blocks must be in the same layout")
     dev = _lib.require_gpu(hidden, router_indices, routing_weights, gate_up_blocks,
                            gate_up_scales, down_blocks, down_scales, gate_up_bias, down_bias)
     out_dtype = hidden.dtype
@@ -140,8 +209,9 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
     bias_code = _lib.dtype_code(bias_dtype.dtype) if bias_dtype is not None else 0
     gub = gate_up_bias.to(bias_dtype.dtype).contiguous() if gate_up_bias is not None else None
     dnb = down_bias.to(bias_dtype.dtype).contiguous() if down_bias is not None else None
-    gu_b, gu_s = _as_u8(gate_up_blocks), _as_u8(gate_up_scales)
-    dn_b, dn_s = _as_u8(down_blocks), _as_u8(down_scales)
+    gu_b, gu_s, dn_b, dn_s = (_as_u8(x) for x in (gate_up_blocks, gate_up_scales, down_blocks, down_scales))
+    if layout == LAYOUT_KPAIR:  # the k-pair layout moves in 16-byte pieces only
+        gu_b, gu_s, dn_b, dn_s = (_aligned(x, 16) for x in (gu_b, gu_s, dn_b, dn_s))
     out = torch.empty((T, H), dtype=out_dtype, device=dev)
     ws_bytes = moe_workspace_bytes(T, H, I, E, k)
     ws = _aligned_bytes(ws_bytes, dev)
@@ -155,7 +225,7 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
                   w.data_ptr(), w_code, gu_b.data_ptr(), gu_s.data_ptr(), ptr(gub),
                   dn_b.data_ptr(), dn_s.data_ptr(), ptr(dnb), bias_code, float(alpha),
                   float(limit), out.data_ptr(), out_code, ws.data_ptr(), ws_bytes,
-                  ptr(save_pre), PATHS[path], _lib.stream_handle(dev))
+                  ptr(save_pre), PATHS[path], layout, _lib.stream_handle(dev))
     if save:
         return out, ws, save_pre
     return out
@@ -174,10 +244,10 @@ class MoEStages:
                  down_bias, alpha: float = 1.702, limit: float = 7.0, path: str = "auto"):
         self.T, self.H = hidden.shape
         self.k = router_indices.shape[1]
-        self.E = gate_up_blocks.shape[0]
-        self.I = gate_up_blocks.shape[1] // 2
-        _check_packed(gate_up_blocks, gate_up_scales, self.E, 2 * self.I, self.H, "gate_up_proj")
-        _check_packed(down_blocks, down_scales, self.E, self.H, self.I, "down_proj")
+        self.E, self.I = _experts_dims(gate_up_blocks)
+        self.layout = _check_packed(gate_up_blocks, gate_up_scales, self.E, 2 * self.I, self.H, "gate_up_proj")
+        if _check_packed(down_blocks, down_scales, self.E, self.H, self.I, "down_proj") != self.layout:
+            raise ValueError("gate_up and down blocks must be in the same layout")
         self.dev = _lib.require_gpu(hidden, router_indices, routing_weights, gate_up_blocks)
         if hidden.dtype != torch.bfloat16 or not hidden.is_contiguous():
             raise ValueError("MoEStages takes contiguous bfloat16 hidden states")
@@ -205,13 +275,13 @@ class MoEStages:
         _lib.call("bsa_moe_gate_up", self.hidden.data_ptr(), *self.shape, b.data_ptr(),
                   s.data_ptr(), bias.data_ptr() if bias is not None else None, self.bias_code,
                   self.alpha, self.limit, self.ws.data_ptr(), self.ws_bytes, None, self.path,
-                  self._stream())
+                  self.layout, self._stream())
 
     def down(self):
         b, s, bias = self.dn
         _lib.call("bsa_moe_down", *self.shape, b.data_ptr(), s.data_ptr(),
                   bias.data_ptr() if bias is not None else None, self.bias_code,
-                  self.ws.data_ptr(), self.ws_bytes, self.path, self._stream())
+                  self.ws.data_ptr(), self.ws_bytes, self.path, self.layout, self._stream())
 
     def combine(self):
         _lib.call("bsa_moe_combine", self.idx.data_ptr(), self.w.data_ptr(),
@@ -246,8 +316,10 @@ def moe_experts_backward(grad_out: Tensor, hidden: Tensor, router_indices: Tenso
     """
     T, H = hidden.shape
     k = router_indices.shape[1]
-    E = gate_up_blocks.shape[0]
-    I = gate_up_blocks.shape[1] // 2
+    E, I = _experts_dims(gate_up_blocks)
+    layout = blocks_layout(gate_up_blocks)
+    if blocks_layout(down_blocks) != layout:
+        raise ValueError("gate_up and down blocks must be in the same layout")
     dev = _lib.require_gpu(grad_out, hidden, router_indices, routing_weights, workspace)
     if T == 0:
         return (torch.zeros_like(hidden) if need_hidden else None,
@@ -257,9 +329,11 @@ def moe_experts_backward(grad_out: Tensor, hidden: Tensor, router_indices: Tenso
     idx = router_indices.to(torch.int64).contiguous()
     w = routing_weights.contiguous()
     # the backward kernels DMA the packed weights in 16- or 4-byte pieces
-    # (staging-blob views are 8-byte aligned) and the pre-activations in 16
-    gub, gus, dnb, dns = (_aligned(_as_u8(x), 4) for x in (gate_up_blocks, gate_up_scales,
-                                                            down_blocks, down_scales))
+    # (staging-blob views are 8-byte aligned; the k-pair layout moves in
+    # 16-byte pieces only) and the pre-activations in 16
+    wal = 16 if layout == LAYOUT_KPAIR else 4
+    gub, gus, dnb, dns = (_aligned(_as_u8(x), wal) for x in (gate_up_blocks, gate_up_scales,
+                                                              down_blocks, down_scales))
     pre = _aligned(gate_up_pre.contiguous(), 16)
     bwd_bytes = moe_bwd_workspace_bytes(T, H, I, E, k)
     bws = _aligned_bytes(bwd_bytes, dev)
@@ -272,7 +346,7 @@ def moe_experts_backward(grad_out: Tensor, hidden: Tensor, router_indices: Tenso
                   workspace.data_ptr(), workspace.numel(), pre.data_ptr(), bws.data_ptr(),
                   bwd_bytes, grad_h.data_ptr() if grad_h is not None else None,
                   _lib.dtype_code(hidden.dtype),
-                  grad_w.data_ptr() if grad_w is not None else None, _lib.stream_handle(dev))
+                  grad_w.data_ptr() if grad_w is not None else None, layout, _lib.stream_handle(dev))
     if grad_w is not None:
         grad_w = grad_w.to(routing_weights.dtype)
     return grad_h, grad_w

@@ -31,6 +31,27 @@ extern "C" {
 #define BSA_DTYPE_F16 1
 #define BSA_DTYPE_F32 2
 
+/*
+ * Layouts of the packed MXFP4 blocks (scales always keep the checkpoint
+ * layout [E, R, G]).
+ *
+ * BSA_LAYOUT_CHECKPOINT  uint8 [E, R, G, 16]: the checkpoint's own layout
+ *                        (gate_up_proj_blocks / down_proj_blocks).
+ * BSA_LAYOUT_KPAIR       uint8 [E, R/16, G/2, 16, 2, 16]: group g of row r at
+ *                        [e][r / 16][g / 2][r % 16][g % 2] -- 16-row bands,
+ *                        inside a band the groups two by two, each pair
+ *                        holding the band's 16 rows (512 contiguous bytes).
+ *                        A band occupies the same bytes in both layouts.  An
+ *                        on-disk shard format for the prefill kernels, whose
+ *                        weight tiles become 512-byte runs instead of 32-byte
+ *                        ones; no counterpart in the reference (its shards
+ *                        store the checkpoint layout, shards.py:148-165).
+ *                        Needs R % 16 == 0, G even, and 16-byte aligned
+ *                        blocks and scales.
+ */
+#define BSA_LAYOUT_CHECKPOINT 0
+#define BSA_LAYOUT_KPAIR 1
+
 /* Thread-local message describing the last failure of this thread. */
 const char *bsa_last_error(void);
 
@@ -72,6 +93,28 @@ int bsa_dequant_mxfp4_mode(const void *blocks, const void *scales, void *out,
                            int mode, void *stream);
 
 /*
+ * As bsa_dequant_mxfp4_mode, for blocks in either layout (blocks_layout
+ * BSA_LAYOUT_CHECKPOINT or BSA_LAYOUT_KPAIR); the output is the same.  The
+ * k-pair layout also needs a 16-byte aligned out.
+ */
+int bsa_dequant_mxfp4_layout(const void *blocks, const void *scales,
+                             void *out, int out_dtype, int64_t E, int64_t R,
+                             int64_t G, int mode, int blocks_layout,
+                             void *stream);
+
+/*
+ * Repack checkpoint-layout blocks uint8 [E, R, G, 16] into the k-pair layout
+ * (bsa_mxfp4_to_kpair) and back (bsa_mxfp4_from_kpair): a permutation of
+ * 16-byte groups, bit for bit.  R % 16 == 0, G even, both buffers 16-byte
+ * aligned and distinct.  The conversion a shard writer runs once, before
+ * writing (block_streamer/shards.py:167-176 writes tensors as they are).
+ */
+int bsa_mxfp4_to_kpair(const void *blocks, void *out, int64_t E, int64_t R,
+                       int64_t G, void *stream);
+int bsa_mxfp4_from_kpair(const void *blocks, void *out, int64_t E, int64_t R,
+                         int64_t G, void *stream);
+
+/*
  * Bytes of workspace bsa_moe_experts_fwd needs for T tokens, hidden H,
  * intermediate I, E experts and top-k k (written to *bytes).  No reference
  * counterpart: the reference allocates per expert inside its loop.
@@ -107,6 +150,9 @@ int bsa_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
  *                   blocks, 4-byte aligned scales; not bit-compatible with
  *                   paths 0-2: the activation quantisation adds a relative
  *                   error of a few 1e-2)
+ *   blocks_layout   layout of gate_up_blocks and down_blocks:
+ *                   BSA_LAYOUT_CHECKPOINT or BSA_LAYOUT_KPAIR (the results
+ *                   are the same bit for bit)
  *
  * Gate and up columns are interleaved (gate = even, up = odd), alpha and
  * limit parameterise the clamped SwiGLU.  Each token's k contributions are
@@ -119,7 +165,7 @@ int bsa_moe_experts_fwd(
     const void *gate_up_bias, const void *down_blocks, const void *down_scales,
     const void *down_bias, int bias_dtype, float alpha, float limit, void *out,
     int out_dtype, void *workspace, int64_t workspace_bytes,
-    void *save_gate_up, int path, void *stream);
+    void *save_gate_up, int path, int blocks_layout, void *stream);
 
 /*
  * The four stages bsa_moe_experts_fwd runs, callable one by one (same
@@ -134,6 +180,7 @@ int bsa_moe_experts_fwd(
  *                    workspace's float32 [T*k, H] rows.
  * bsa_moe_combine    replaces gptoss.py:175-176: routing-weight scale and the
  *                    per-token sum (ascending expert order) into out.
+ * blocks_layout is that of the blocks argument, as for bsa_moe_experts_fwd.
  */
 int bsa_moe_dispatch(const int64_t *router_indices, int64_t T, int64_t H,
                      int64_t I, int64_t E, int64_t k, void *workspace,
@@ -143,11 +190,11 @@ int bsa_moe_gate_up(const void *hidden, int64_t T, int64_t H, int64_t I,
                     const void *scales, const void *bias, int bias_dtype,
                     float alpha, float limit, void *workspace,
                     int64_t workspace_bytes, void *save_gate_up, int path,
-                    void *stream);
+                    int blocks_layout, void *stream);
 int bsa_moe_down(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
                  const void *blocks, const void *scales, const void *bias,
                  int bias_dtype, void *workspace, int64_t workspace_bytes,
-                 int path, void *stream);
+                 int path, int blocks_layout, void *stream);
 int bsa_moe_combine(const int64_t *router_indices, const void *routing_weights,
                     int weight_dtype, int64_t T, int64_t H, int64_t I,
                     int64_t E, int64_t k, void *workspace,
@@ -222,7 +269,7 @@ int bsa_moe_bwd_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
  * H must be a multiple of 64.  The packed blocks and scales must be 4-byte
  * aligned (16-byte aligned ones move in 16-byte DMA pieces, others in 4-byte
  * pieces) and save_gate_up 16-byte aligned; otherwise BSA_EINVAL.  Dropped (token, slot) pairs get a zero
- * routing-weight gradient.
+ * routing-weight gradient.  blocks_layout is that of both blocks tensors.
  */
 int bsa_moe_experts_bwd(
     const void *grad_out, int grad_dtype, int64_t T, int64_t H, int64_t I,
@@ -232,7 +279,7 @@ int bsa_moe_experts_bwd(
     const void *down_scales, float alpha, float limit, void *workspace,
     int64_t workspace_bytes, const void *save_gate_up, void *bwd_workspace,
     int64_t bwd_workspace_bytes, void *grad_hidden, int grad_hidden_dtype,
-    float *grad_weights, void *stream);
+    float *grad_weights, int blocks_layout, void *stream);
 
 /*
  * RMSNorm of a decoder layer, in one launch: the post-attention norm that

@@ -23,5 +23,6 @@ from .oracle import (  # noqa: F401
     rmsnorm_bwd_ref,
     rmsnorm_ref,
     router_ref,
+    to_kpair_ref,
     topk_softmax_ref,
 )

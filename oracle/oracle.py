@@ -26,6 +26,8 @@ Pinning (how each function is checked, see ``tests/test_oracle.py``):
   transformers ``GptOssRMSNorm`` in float64, forward and its autograd
   backward (against the closed-form gradient), plus scale invariance and the
   eps-dominated regime.
+* k-pair layout (this build's shard format, no reference counterpart): its
+  defining index map checked element by element on small inputs.
 * experts: the installed transformers dense twin ``GptOssExperts``
   (TF/models/gpt_oss/modeling_gpt_oss.py:68-114) fed the dequantised
   weights, plus invariants (zero routing weight contributes nothing, token
@@ -188,6 +190,15 @@ def rmsnorm_bwd_ref(grad: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, e
     H = x.shape[-1]
     r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
     return r * g - x * (r ** 3 * (g * x).sum(-1, keepdim=True) / H)
+
+
+def to_kpair_ref(blocks: torch.Tensor) -> torch.Tensor:
+    """The k-pair shard layout of checkpoint blocks ``[E, R, G, 16]``: group g
+    of row r at ``[e][r // 16][g // 2][r % 16][g % 2]`` (no reference
+    counterpart; the definition the HIP repacking and every kernel reading
+    that layout are checked against)."""
+    E, R, G, _ = blocks.shape
+    return blocks.reshape(E, R // 16, 16, G // 2, 2, 16).permute(0, 1, 3, 2, 4, 5).contiguous()
 
 
 def apply_gate_ref(gate_up: torch.Tensor, alpha: float = 1.702,

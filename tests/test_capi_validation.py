@@ -30,20 +30,21 @@ def _ws_bytes(T, H, I, E, k, fn="bsa_moe_workspace_bytes"):
 
 
 def _fwd_args(T=4, H=2880, I=2880, E=128, k=4, hidden=FAKE, wdt=BF16, bdt=BF16, odt=BF16, path=0,
-              ptr=FAKE, ws=FAKE, ws_bytes=None):
+              ptr=FAKE, ws=FAKE, ws_bytes=None, layout=0, scales=None):
     if ws_bytes is None:
         ws_bytes = _ws_bytes(max(T, 0), H, I, E, k) if min(H, I, E, k) > 0 and T >= 0 else 0
-    return (hidden, T, H, I, E, k, ptr, ptr, wdt, ptr, ptr, ptr, ptr, ptr, ptr, bdt, 1.702, 7.0, ptr, odt,
-            ws, ws_bytes, None, path, None)
+    sc = ptr if scales is None else scales
+    return (hidden, T, H, I, E, k, ptr, ptr, wdt, ptr, sc, ptr, ptr, sc, ptr, bdt, 1.702, 7.0, ptr, odt,
+            ws, ws_bytes, None, path, layout, None)
 
 
 def _bwd_args(T=4, H=2880, I=2880, E=128, k=4, gdt=BF16, blocks=FAKE, save=FAKE, bwd_ws=FAKE,
-              bwd_bytes=None, ghdt=BF16):
+              bwd_bytes=None, ghdt=BF16, layout=0):
     ws_bytes = _ws_bytes(T, H, I, E, k) if min(H, I, E, k) > 0 and T >= 0 else 0
     if bwd_bytes is None:
         bwd_bytes = _ws_bytes(T, H, I, E, k, "bsa_moe_bwd_workspace_bytes") if ws_bytes else 0
     return (FAKE, gdt, T, H, I, E, k, FAKE, FAKE, BF16, blocks, FAKE, FAKE, FAKE, 1.702, 7.0, FAKE, ws_bytes,
-            save, bwd_ws, bwd_bytes, FAKE, ghdt, FAKE, None)
+            save, bwd_ws, bwd_bytes, FAKE, ghdt, FAKE, layout, None)
 
 
 CASES = [
@@ -64,6 +65,19 @@ CASES = [
      b"16-byte aligned"),
     ("fwd workspace too small", "bsa_moe_experts_fwd", _fwd_args(ws_bytes=1024), _lib.BSA_EINVAL, b"workspace"),
     ("fwd workspace alignment", "bsa_moe_experts_fwd", _fwd_args(ws=FAKE + 16), _lib.BSA_EINVAL, b"aligned"),
+    ("fwd unknown layout", "bsa_moe_experts_fwd", _fwd_args(layout=5), _lib.BSA_EINVAL, b"layout"),
+    ("fwd k-pair odd groups", "bsa_moe_experts_fwd", _fwd_args(H=96, layout=1), _lib.BSA_EINVAL,
+     b"even group count"),
+    ("fwd k-pair scales alignment", "bsa_moe_experts_fwd", _fwd_args(layout=1, scales=FAKE + 8), _lib.BSA_EINVAL,
+     b"16-byte aligned blocks and scales"),
+    ("gate_up unknown layout", "bsa_moe_gate_up",
+     (FAKE, 4, 64, 64, 8, 2, FAKE, FAKE, None, BF16, 1.702, 7.0, FAKE, 1 << 20, None, 0, 3, None),
+     _lib.BSA_EINVAL, b"layout"),
+    ("down k-pair alignment", "bsa_moe_down",
+     (4, 64, 64, 8, 2, FAKE + 8, FAKE, None, BF16, FAKE, 1 << 20, 0, 1, None), _lib.BSA_EINVAL,
+     b"16-byte aligned"),
+    ("bwd k-pair alignment", "bsa_moe_experts_bwd", _bwd_args(blocks=FAKE + 4, layout=1), _lib.BSA_EINVAL,
+     b"16-byte aligned blocks"),
     ("bwd H % 64", "bsa_moe_experts_bwd", _bwd_args(H=96), _lib.BSA_EINVAL, b"hidden % 64"),
     ("bwd T = 0", "bsa_moe_experts_bwd", _bwd_args(T=0), _lib.BSA_OK, None),
     ("bwd dtype", "bsa_moe_experts_bwd", _bwd_args(ghdt=5), _lib.BSA_EINVAL, b"dtype"),
@@ -92,6 +106,18 @@ CASES = [
     ("mxfp8 alignment", "bsa_quant_mxfp8", (FAKE + 8, BF16, 4, 128, FAKE, FAKE, 4, None), _lib.BSA_EINVAL,
      b"aligned"),
     ("mxfp8 R = 0", "bsa_quant_mxfp8", (None, BF16, 0, 128, None, None, 4, None), _lib.BSA_OK, None),
+    ("dequant unknown layout", "bsa_dequant_mxfp4_layout", (FAKE, FAKE, FAKE, BF16, 1, 32, 4, 0, 2, None),
+     _lib.BSA_EINVAL, b"layout"),
+    ("dequant k-pair rows", "bsa_dequant_mxfp4_layout", (FAKE, FAKE, FAKE, BF16, 1, 24, 4, 0, 1, None),
+     _lib.BSA_EINVAL, b"rows % 16"),
+    ("dequant k-pair unaligned", "bsa_dequant_mxfp4_layout", (FAKE + 8, FAKE, FAKE, BF16, 1, 32, 4, 0, 1, None),
+     _lib.BSA_EINVAL, b"16-byte aligned"),
+    ("to k-pair odd groups", "bsa_mxfp4_to_kpair", (FAKE, FAKE * 2, 1, 32, 3, None), _lib.BSA_EINVAL,
+     b"even group count"),
+    ("to k-pair in place", "bsa_mxfp4_to_kpair", (FAKE, FAKE, 1, 32, 4, None), _lib.BSA_EINVAL, b"distinct"),
+    ("from k-pair unaligned", "bsa_mxfp4_from_kpair", (FAKE + 4, FAKE * 2, 1, 32, 4, None), _lib.BSA_EINVAL,
+     b"16-byte aligned"),
+    ("to k-pair empty", "bsa_mxfp4_to_kpair", (None, None, 0, 32, 4, None), _lib.BSA_OK, None),
     ("norm H = 0", "bsa_rmsnorm_fwd", (FAKE, BF16, 4, 0, FAKE, F32, 1e-5, FAKE, None), _lib.BSA_EINVAL,
      b"bad shape"),
     ("norm dtype", "bsa_rmsnorm_fwd", (FAKE, 4, 4, 64, FAKE, F32, 1e-5, FAKE, None), _lib.BSA_EINVAL,

@@ -221,6 +221,24 @@ def test_rmsnorm_ref_invariants():
     assert (dx * x).sum(-1).abs().max() <= 1e-12 * dx.abs().max() * x.abs().max() * 256
 
 
+# ----------------------------------------------------------------------------- k-pair layout
+
+def test_to_kpair_ref_index_map():
+    g = torch.Generator().manual_seed(3)
+    E, R, G = 2, 32, 6
+    blocks = torch.randint(0, 256, (E, R, G, 16), generator=g, dtype=torch.uint8)
+    kp = oracle.to_kpair_ref(blocks)
+    assert kp.shape == (E, R // 16, G // 2, 16, 2, 16)
+    for e in range(E):
+        for r in range(R):
+            for gg in range(G):
+                assert torch.equal(kp[e, r // 16, gg // 2, r % 16, gg % 2], blocks[e, r, gg])
+    # a band occupies the same bytes in both layouts
+    flat_b = blocks.reshape(E, R // 16, -1)
+    flat_k = kp.reshape(E, R // 16, -1)
+    assert torch.equal(flat_b.sort(dim=-1).values, flat_k.sort(dim=-1).values)
+
+
 # ----------------------------------------------------------------------------- experts
 
 def _tiny():
