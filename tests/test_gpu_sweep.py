@@ -8,6 +8,8 @@ partial, experts go unhit, and rows, columns and k-tiles end at every kind of
 boundary.  Bars: the layer bar for the forward (tests/moe_util.py), the
 gradient bar for the backward (relative L2 <= 1e-2).  The MX path is checked
 against the oracle's emulation of its own arithmetic (MXFP8 activations).
+Where both projections have an even group count, the forward is also run on
+the blocks in the k-pair shard layout and must give the same bits.
 """
 
 from __future__ import annotations
@@ -55,10 +57,19 @@ def test_sweep_forward(device, shape):
     t, idx, w = _inputs(shape, device)
     want = oracle.experts_ref(t["hidden"], idx, w, *expert_args(t))
     g = {n: (v.to(device) if torch.is_tensor(v) else v) for n, v in t.items()}
+    # the k-pair shard layout where the shape allows it (both projections with an
+    # even group count): the same bits as the checkpoint layout
+    kp = (I // 32) % 2 == 0
+    kp_args = list(expert_args(g))
+    if kp:
+        kp_args[0], kp_args[3] = kernels.to_kpair(kp_args[0]), kernels.to_kpair(kp_args[3])
     for path in ("auto", "stream", "tiled"):
         announce(f"sweep forward {shape} {path}")
         got = kernels.moe_experts_forward(g["hidden"], idx.to(device), w.to(device), *expert_args(g), path=path)
         assert_layer_close(got, want, f"{shape} {path}", absolute=True)
+        if kp:
+            got_kp = kernels.moe_experts_forward(g["hidden"], idx.to(device), w.to(device), *kp_args, path=path)
+            assert torch.equal(got_kp.view(torch.int16), got.view(torch.int16)), f"{shape} {path} k-pair"
     if H % 64 == 0 and I % 64 == 0:
         announce(f"sweep forward {shape} mx")
         want_mx = oracle.experts_mx_ref(t["hidden"], idx, w, *expert_args(t))
