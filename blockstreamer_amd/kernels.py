@@ -92,7 +92,7 @@ def dequantize_mxfp4(blocks: Tensor, scales: Tensor, dtype: torch.dtype = torch.
     blocks = _as_u8(blocks)
     scales = _as_u8(scales)
     if layout == LAYOUT_KPAIR:
-        blocks = _aligned(blocks, 16)
+        blocks = _aligned_kpair(blocks)
     if out is None:
         out = torch.empty((E, G * 32, R), dtype=dtype, device=dev)
     elif out.shape != (E, G * 32, R) or out.dtype != dtype or not out.is_contiguous():
@@ -141,6 +141,24 @@ def moe_workspace_bytes(T: int, H: int, I: int, E: int, k: int) -> int:
 def _aligned(t: Tensor, n: int) -> Tensor:
     """``t`` itself when its storage starts on an n-byte boundary, else a copy."""
     return t if t.data_ptr() % n == 0 else t.clone()
+
+
+_warned_kpair_copy = False
+
+
+def _aligned_kpair(t: Tensor) -> Tensor:
+    """A k-pair layout tensor on a 16-byte boundary; a misaligned one is
+    copied, with a warning the first time (a shard writer that adopts the
+    layout aligns these tensors to 16 bytes, so the copy is the exception)."""
+    global _warned_kpair_copy
+    if t.data_ptr() % 16 == 0:
+        return t
+    if not _warned_kpair_copy:
+        import warnings
+        warnings.warn("k-pair layout blocks or scales are not 16-byte aligned and are copied on every call; "
+                      "align them to 16 bytes when writing the shards", RuntimeWarning, stacklevel=3)
+        _warned_kpair_copy = True
+    return t.clone()
 
 
 def _aligned_bytes(nbytes: int, device, align: int = 256) -> Tensor:
@@ -211,7 +229,7 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
     dnb = down_bias.to(bias_dtype.dtype).contiguous() if down_bias is not None else None
     gu_b, gu_s, dn_b, dn_s = (_as_u8(x) for x in (gate_up_blocks, gate_up_scales, down_blocks, down_scales))
     if layout == LAYOUT_KPAIR:  # the k-pair layout moves in 16-byte pieces only
-        gu_b, gu_s, dn_b, dn_s = (_aligned(x, 16) for x in (gu_b, gu_s, dn_b, dn_s))
+        gu_b, gu_s, dn_b, dn_s = (_aligned_kpair(x) for x in (gu_b, gu_s, dn_b, dn_s))
     out = torch.empty((T, H), dtype=out_dtype, device=dev)
     ws_bytes = moe_workspace_bytes(T, H, I, E, k)
     ws = _aligned_bytes(ws_bytes, dev)
@@ -331,9 +349,12 @@ def moe_experts_backward(grad_out: Tensor, hidden: Tensor, router_indices: Tenso
     # the backward kernels DMA the packed weights in 16- or 4-byte pieces
     # (staging-blob views are 8-byte aligned; the k-pair layout moves in
     # 16-byte pieces only) and the pre-activations in 16
-    wal = 16 if layout == LAYOUT_KPAIR else 4
-    gub, gus, dnb, dns = (_aligned(_as_u8(x), wal) for x in (gate_up_blocks, gate_up_scales,
-                                                              down_blocks, down_scales))
+    if layout == LAYOUT_KPAIR:
+        gub, gus, dnb, dns = (_aligned_kpair(_as_u8(x)) for x in (gate_up_blocks, gate_up_scales,
+                                                                   down_blocks, down_scales))
+    else:
+        gub, gus, dnb, dns = (_aligned(_as_u8(x), 4) for x in (gate_up_blocks, gate_up_scales,
+                                                                down_blocks, down_scales))
     pre = _aligned(gate_up_pre.contiguous(), 16)
     bwd_bytes = moe_bwd_workspace_bytes(T, H, I, E, k)
     bws = _aligned_bytes(bwd_bytes, dev)

@@ -153,3 +153,26 @@ def test_module_binds_k_pair_tensors(device):
     want = torch.func.functional_call(mod, ck, (t["hidden"], idx, w), strict=True)
     got = torch.func.functional_call(mod, kp, (t["hidden"], idx, w), strict=True)
     assert _same(got, want)
+
+
+def test_misaligned_k_pair_view_is_copied_with_a_warning(device):
+    """A k-pair tensor at an 8-byte offset (a blob written with the
+    checkpoint's 8-byte alignment) is copied, with a warning, and gives the
+    same bits."""
+    E, k, H, I, T = 8, 2, 256, 256, 16
+    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=12, scale_lo=116, scale_hi=122,
+                            device=device)
+    idx, w = synthetic.random_routing(T, E, k, seed=6, dtype=torch.float32)
+    idx, w = idx.to(device), w.to(device)
+    kp = _kp_args(t)
+    buf = torch.empty(kp[0].numel() + 8, dtype=torch.uint8, device=device)
+    view = buf[8:].view(kp[0].shape)
+    view.copy_(kp[0])
+    kp[0] = view
+    assert view.data_ptr() % 16 == 8
+    kernels._warned_kpair_copy = False
+    announce("k-pair misaligned view")
+    with pytest.warns(RuntimeWarning, match="16-byte aligned"):
+        got = kernels.moe_experts_forward(t["hidden"], idx, w, *kp)
+    want = kernels.moe_experts_forward(t["hidden"], idx, w, *[t[n] for n in NAMES])
+    assert _same(got, want)
