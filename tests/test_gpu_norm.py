@@ -169,3 +169,30 @@ def test_rmsnorm_in_cuda_graph(device):
         torch.cuda.synchronize()
         want = kernels.rmsnorm_forward(x, w, eps)
         assert torch.equal(y, want), f"replay {i} differs from eager"
+
+
+def test_rmsnorm_special_rows_match_transformers(device):
+    """Rows of zeros (the result is 0: r = eps^-1/2 times 0), values whose
+    squares overflow float32 (r = 0, so 0 out), and rows holding inf or NaN
+    (NaN out): the same as transformers' module, NaN for NaN."""
+    gpt_oss = pytest.importorskip("transformers.models.gpt_oss.modeling_gpt_oss")
+    H, eps = 2880, 1e-5
+    ref = gpt_oss.GptOssRMSNorm(H, eps=eps).to(device)
+    ours = gptoss.FusedRMSNorm(H, eps, torch.float32, device)
+    rows = torch.randn(6, H, generator=torch.Generator().manual_seed(8))
+    rows[0] = 0.0
+    rows[1] = 3e38
+    rows[2, 5] = float("inf")
+    rows[3, 7] = float("nan")
+    rows[4] *= 1e-30
+    for dt in (torch.float32, torch.bfloat16):
+        x = rows.to(dt).to(device)
+        announce(f"rmsnorm special rows {dt}")
+        with torch.no_grad():
+            got, want = ours(x), ref(x)
+        assert torch.equal(torch.isnan(got), torch.isnan(want)), f"{dt}: NaN positions differ"
+        fin = ~torch.isnan(want)
+        g, w = got[fin].float(), want[fin].float()
+        assert torch.equal(torch.isinf(g), torch.isinf(w))
+        ok = torch.isfinite(w)
+        assert ((g[ok] - w[ok]).abs() <= 2.0 ** -7 * w[ok].abs() + 1e-30).all(), f"{dt}: finite values differ"
