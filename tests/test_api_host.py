@@ -28,3 +28,35 @@ def test_scale_shape_mismatch():
     scales = torch.zeros(1, 8, 3, dtype=torch.uint8)
     with pytest.raises(ValueError, match="does not match"):
         gptoss.dequantize_expert(blocks, scales)
+
+
+def test_blocks_layout_and_shape_from_rank():
+    from blockstreamer_amd import kernels
+    ck = torch.zeros(3, 32, 6, 16, dtype=torch.uint8)
+    kp = torch.zeros(3, 2, 3, 16, 2, 16, dtype=torch.uint8)
+    assert kernels.blocks_layout(ck) == kernels.LAYOUT_CHECKPOINT
+    assert kernels.blocks_layout(kp) == kernels.LAYOUT_KPAIR
+    assert kernels.packed_shape(ck) == kernels.packed_shape(kp) == (3, 32, 6)
+    for bad in (torch.zeros(3, 32, 6, 8, dtype=torch.uint8), torch.zeros(3, 2, 3, 16, 4, 16, dtype=torch.uint8),
+                torch.zeros(32, 6, 16, dtype=torch.uint8)):
+        with pytest.raises(ValueError, match="k-pair layout"):
+            kernels.blocks_layout(bad)
+
+
+def test_experts_refuse_mixed_layouts_before_the_gpu():
+    """gate_up in one layout and down in the other is a shape error, raised
+    before any device check."""
+    from blockstreamer_amd import kernels
+    E, k, H, I, T = 2, 1, 64, 64, 4
+    h = torch.zeros(T, H, dtype=torch.bfloat16)
+    idx = torch.zeros(T, k, dtype=torch.int64)
+    w = torch.ones(T, k)
+    gub = torch.zeros(E, 2 * I // 16, H // 64, 16, 2, 16, dtype=torch.uint8)   # k-pair
+    gus = torch.zeros(E, 2 * I, H // 32, dtype=torch.uint8)
+    dnb = torch.zeros(E, H, I // 32, 16, dtype=torch.uint8)                     # checkpoint
+    dns = torch.zeros(E, H, I // 32, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="same layout"):
+        kernels.moe_experts_forward(h, idx, w, gub, gus, None, dnb, dns, None)
+    wrong_k = torch.zeros(E, 2 * I, H // 32 + 1, 16, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="gate_up_proj_blocks must be"):
+        kernels.moe_experts_forward(h, idx, w, wrong_k, gus, None, dnb, dns, None)
