@@ -55,7 +55,8 @@ extern "C" {
 /* Thread-local message describing the last failure of this thread. */
 const char *bsa_last_error(void);
 
-/* ABI version of this library (major * 100 + minor). */
+/* ABI version of this library (major * 100 + minor); 101 added the blocks
+ * layout argument and the k-pair entry points. */
 int bsa_version(void);
 
 /*
