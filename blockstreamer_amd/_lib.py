@@ -15,6 +15,7 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "libbsamd.so"
 
 BSA_OK, BSA_EINVAL, BSA_EHIP = 0, 1, 2
+ABI_MAJOR = 2  # BSA_VERSION_MAJOR of include/bsamd.h: the signatures declared below
 DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 _i64 = ctypes.c_int64
@@ -80,6 +81,10 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.argtypes = args
             fn.restype = _RESTYPE.get(name, ctypes.c_int)
+        version = handle.bsa_version()
+        if version // 100 != ABI_MAJOR:
+            raise RuntimeError(f"{LIB_PATH} has ABI version {version}; this binding needs major version "
+                               f"{ABI_MAJOR} (rebuild with `python -m blockstreamer_amd.build`)")
         _lib = handle
     return _lib
 

@@ -1904,20 +1904,21 @@ constexpr int BT_STAGE = BT_A_BYTES + BT_Q_BYTES + BT_S_BYTES;
 constexpr int BT_NS = 4;
 
 // DMA sources of one workgroup tile.  The activations (this library's own
-// buffers) always move in 16-byte pieces; the packed weights and scales move
-// in 16-byte pieces when both tensors are 16-byte aligned (W4 = false: 4 + 1
-// instructions per wave per stage) and in 4-byte pieces otherwise (W4 = true:
-// 16 + 2; views into a staging blob are only 8-byte aligned).  Either way the
-// stage layout is the one described above.
-template <bool W4>
+// buffers) always move in 16-byte pieces.  The packed weights move in 16-byte
+// pieces when they are 16-byte aligned (QW4 = false: 4 instructions per wave
+// per stage) and in 4-byte pieces otherwise (QW4 = true: 16; views into a
+// staging blob are only 8-byte aligned); the scales likewise (SW4 = false: 1
+// instruction, true: 2).  Either way the stage layout is the one described
+// above.  The k-pair blocks layout takes the 16-byte weight pieces only.
+template <bool QW4, bool SW4>
 struct BtSrc {
-  static constexpr int DMA_PER_TILE = 4 + (W4 ? 16 + 2 : 4 + 1);  // per wave: A, Q, S
+  static constexpr int DMA_PER_TILE = 4 + (QW4 ? 16 : 4) + (SW4 ? 2 : 1);  // per wave: A, Q, S
   const uint16_t* asrc[4];
   const uint8_t* bq;
   const uint8_t* bs;
-  int64_t q[W4 ? 1 : 4];   // byte offsets into bq (W4: of this lane's word in instruction 0)
-  int64_t sc[W4 ? 2 : 1];  // byte offsets into bs of this lane's chunk
-  int qsw, qvalid;         // W4: the lane's chunk position, valid chunks of the tile
+  int64_t q[QW4 ? 1 : 4];   // byte offsets into bq (QW4: of this lane's word in instruction 0)
+  int64_t sc[SW4 ? 2 : 1];  // byte offsets into bs of this lane's chunk
+  int qsw, qvalid;          // QW4: the lane's chunk position; valid chunks of the tile
   int64_t qrow, qstep, sstep, slast;
 
   __device__ __forceinline__ void init(const GemmArgs& a, int m0, int rows, int nt, int64_t wrow0, int NB,
@@ -1935,10 +1936,20 @@ struct BtSrc {
     qstep = (int64_t)BT_BK * NB * 16;
     sstep = (int64_t)BT_BK * NB;
     slast = (int64_t)a.E * a.K * NB - 16;  // last whole chunk (the size is a multiple of 16)
-    if constexpr (W4) {
-      // instruction j: weight row 16 wave + j, lane = 4-byte word of the row's 256 bytes
+    if constexpr (QW4) {
+      // instruction j: weight row 16 wave + j, lane = 4-byte word of the row's
+      // 256 bytes (checkpoint layout only)
       qsw = lane >> 2;
       q[0] = ((wrow0 + 16 * wave) * NB + nt * 16) * 16 + (lane & 3) * 4;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 4 * (4 * wave + j) + (lane >> 4);
+        const int c = (lane & 15) ^ (r & 15);
+        q[j] = bq_off(a.kp, wrow0 + r, nt * 16 + (c < qvalid ? c : 0), NB);  // past N: any chunk
+      }
+    }
+    if constexpr (SW4) {
       // instruction i: rows 16 wave + 8 i + lane / 8, word lane % 8 of the two chunks
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
@@ -1947,12 +1958,6 @@ struct BtSrc {
         sc[i] = (o & ~(int64_t)15) + 16 * ((lane & 7) >> 2);
       }
     } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 4 * (4 * wave + j) + (lane >> 4);
-        const int c = (lane & 15) ^ (r & 15);
-        q[j] = bq_off(a.kp, wrow0 + r, nt * 16 + (c < qvalid ? c : 0), NB);  // past N: any chunk
-      }
       // rows 16 wave .. +15, two chunks each; lanes 32..63 repeat 0..31
       const int r = 16 * wave + ((lane & 31) >> 1);
       const int64_t o = (wrow0 + r) * NB + nt * 16;
@@ -1969,22 +1974,25 @@ struct BtSrc {
     uint8_t* ss = st + BT_A_BYTES + BT_Q_BYTES + wave * 1024;
     // the second chunk of the tensor's last rows may start past its end: read
     // the last whole chunk instead (those bytes are not used)
-    if constexpr (W4) {
+    if constexpr (QW4) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int c = qsw ^ j;  // row 16 wave + j keeps source chunk c at position qsw
         const int64_t off = q[0] + kt * qstep + j * qrow + (c < qvalid ? c : 0) * 16;
         __builtin_amdgcn_global_load_lds(bq + off, (lds_void*)(sq + (16 * wave + j) * 256), 4, 0, 0);
       }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        __builtin_amdgcn_global_load_lds(bs + min(sc[i] + kt * sstep, slast) + (lane & 3) * 4,
-                                         (lds_void*)(ss + i * 256), 4, 0, 0);
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         __builtin_amdgcn_global_load_lds(bq + q[j] + kt * qstep, (lds_void*)(sq + (4 * wave + j) * 1024), 16, 0,
                                          0);
+    }
+    if constexpr (SW4) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        __builtin_amdgcn_global_load_lds(bs + min(sc[i] + kt * sstep, slast) + (lane & 3) * 4,
+                                         (lds_void*)(ss + i * 256), 4, 0, 0);
+    } else {
       __builtin_amdgcn_global_load_lds(bs + min(sc[0] + kt * sstep, slast), (lds_void*)ss, 16, 0, 0);
     }
   }
@@ -2048,7 +2056,7 @@ __device__ __forceinline__ void bt_store4(const GemmArgs& a, int64_t pos, int n,
   }
 }
 
-template <int EPI, bool W4>
+template <int EPI, bool QW4, bool SW4>
 __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
   extern __shared__ __align__(1024) uint8_t smem[];  // BT_NS stages
   const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
@@ -2068,9 +2076,9 @@ __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
   const int NB = a.N >> 5;               // scale bytes (and 16-byte chunks) per weight row
   const int64_t wrow0 = (int64_t)e * a.K;  // first weight row of the expert
 
-  BtSrc<W4> src;
+  BtSrc<QW4, SW4> src;
   src.init(a, m0, rows, nt, wrow0, NB, wave, lane);
-  constexpr int DPT = BtSrc<W4>::DMA_PER_TILE;
+  constexpr int DPT = BtSrc<QW4, SW4>::DMA_PER_TILE;
 
   // --- fragment addresses (step s adds 4096 s to Q, 1024 s to S) -------------
   uint32_t aoff[4];
@@ -2198,10 +2206,12 @@ static int allow_big_lds(const void* fn, int kind, int epi, int bytes);
 
 // Explicit instantiations: the host compiler otherwise drops the handle of
 // the first of these named in the launcher below.
-template __global__ void moe_bwd_packed_kernel<EPI_STORE, false>(GemmArgs);
-template __global__ void moe_bwd_packed_kernel<EPI_STORE, true>(GemmArgs);
-template __global__ void moe_bwd_packed_kernel<EPI_SWIGLU_BWD, false>(GemmArgs);
-template __global__ void moe_bwd_packed_kernel<EPI_SWIGLU_BWD, true>(GemmArgs);
+template __global__ void moe_bwd_packed_kernel<EPI_STORE, false, false>(GemmArgs);
+template __global__ void moe_bwd_packed_kernel<EPI_STORE, false, true>(GemmArgs);
+template __global__ void moe_bwd_packed_kernel<EPI_STORE, true, true>(GemmArgs);
+template __global__ void moe_bwd_packed_kernel<EPI_SWIGLU_BWD, false, false>(GemmArgs);
+template __global__ void moe_bwd_packed_kernel<EPI_SWIGLU_BWD, false, true>(GemmArgs);
+template __global__ void moe_bwd_packed_kernel<EPI_SWIGLU_BWD, true, true>(GemmArgs);
 
 // Grouped GEMM on the packed weights read along their rows (the backward
 // products): a.Bq [E][K][N/32][16], a.Bs [E][K][N/32].
@@ -2222,9 +2232,18 @@ static int launch_gemm_packed_rows(const GemmArgs& a, int64_t P, hipStream_t st)
     return BSA_EINVAL;
   }
   const size_t smem = (size_t)BT_NS * BT_STAGE;
-  const bool w16 = reinterpret_cast<uintptr_t>(a.Bq) % 16 == 0 && reinterpret_cast<uintptr_t>(a.Bs) % 16 == 0;
-  void (*fn)(GemmArgs) = w16 ? moe_bwd_packed_kernel<EPI, false> : moe_bwd_packed_kernel<EPI, true>;
-  int rc = allow_big_lds(reinterpret_cast<const void*>(fn), w16 ? 3 : 2, EPI, (int)smem);
+  // the k-pair layout is read in 16-byte weight pieces only (its blocks are
+  // 16-byte aligned by contract); scales take 4-byte pieces below 16
+  const bool q16 = reinterpret_cast<uintptr_t>(a.Bq) % 16 == 0;
+  const bool s16 = q16 && reinterpret_cast<uintptr_t>(a.Bs) % 16 == 0;
+  if (a.kp && !q16) {
+    set_error("packed-weight grouped GEMM: k-pair blocks must be 16-byte aligned");
+    return BSA_EINVAL;
+  }
+  void (*fn)(GemmArgs) = s16 ? moe_bwd_packed_kernel<EPI, false, false>
+                         : q16 ? moe_bwd_packed_kernel<EPI, false, true>
+                               : moe_bwd_packed_kernel<EPI, true, true>;
+  int rc = allow_big_lds(reinterpret_cast<const void*>(fn), s16 ? 3 : (q16 ? 1 : 2), EPI, (int)smem);
   if (rc) return rc;
   hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), smem, st, b);
   BSA_LAUNCH_CHECK("packed-weight grouped GEMM launch");
@@ -2241,7 +2260,7 @@ static int allow_big_lds(const void* fn, int kind, int epi, int bytes = 160 * 10
     set_error("no current HIP device");
     return BSA_EHIP;
   }
-  // kinds: 2-3 packed-weight backward kernel, 4-5 tiled kernel, 6 persistent
+  // kinds: 1-3 packed-weight backward kernel, 4-5 tiled kernel, 6 persistent
   // decode kernel, 8-15 MX kernel configurations
   static bool allowed[64][16][4];
   if (!allowed[dev][kind][epi]) {
@@ -2448,16 +2467,15 @@ static int stage_dispatch(const MoeShape& m, const int64_t* idx, const Workspace
 }
 
 // blocks_layout of one packed weight with `rows` rows of K/32 groups.
-static int check_layout(int layout, const void* blocks, const void* scales, int64_t rows, int64_t K,
-                        const char* what) {
+static int check_layout(int layout, const void* blocks, int64_t rows, int64_t K, const char* what) {
   BSA_REQUIRE(layout == BSA_LAYOUT_CHECKPOINT || layout == BSA_LAYOUT_KPAIR, "%s: unknown blocks layout %d", what,
               layout);
   if (layout == BSA_LAYOUT_KPAIR) {
     BSA_REQUIRE(rows % 16 == 0 && (K / 32) % 2 == 0,
                 "%s: the k-pair layout needs rows %% 16 == 0 and an even group count (rows=%lld K=%lld)", what,
                 (long long)rows, (long long)K);
-    BSA_REQUIRE(reinterpret_cast<uintptr_t>(blocks) % 16 == 0 && reinterpret_cast<uintptr_t>(scales) % 16 == 0,
-                "%s: the k-pair layout needs 16-byte aligned blocks and scales", what);
+    BSA_REQUIRE(reinterpret_cast<uintptr_t>(blocks) % 16 == 0, "%s: the k-pair layout needs 16-byte aligned blocks",
+                what);
   }
   return BSA_OK;
 }
@@ -2575,7 +2593,7 @@ extern "C" int bsa_moe_gate_up(const void* hidden, int64_t T, int64_t H, int64_t
   BSA_REQUIRE(dtype_ok(bias_dtype) && path >= 0 && path <= 3, "gate_up: bad dtype or path");
   BSA_REQUIRE(reinterpret_cast<uintptr_t>(hidden) % 16 == 0 && reinterpret_cast<uintptr_t>(blocks) % 8 == 0,
               "gate_up: hidden must be 16-byte and blocks 8-byte aligned");
-  if ((rc = check_layout(blocks_layout, blocks, scales, 2 * I, H, "gate_up"))) return rc;
+  if ((rc = check_layout(blocks_layout, blocks, 2 * I, H, "gate_up"))) return rc;
   Workspace w;
   if ((rc = check_ws(m, workspace, workspace_bytes, &w, "gate_up"))) return rc;
   return stage_gate_up(m, hidden, blocks, scales, bias, bias_dtype, alpha, limit, w, save_gate_up,
@@ -2593,7 +2611,7 @@ extern "C" int bsa_moe_down(int64_t T, int64_t H, int64_t I, int64_t E, int64_t 
   BSA_REQUIRE(blocks && scales, "down: null pointer");
   BSA_REQUIRE(dtype_ok(bias_dtype) && path >= 0 && path <= 3, "down: bad dtype or path");
   BSA_REQUIRE(reinterpret_cast<uintptr_t>(blocks) % 8 == 0, "down: blocks must be 8-byte aligned");
-  if ((rc = check_layout(blocks_layout, blocks, scales, H, I, "down"))) return rc;
+  if ((rc = check_layout(blocks_layout, blocks, H, I, "down"))) return rc;
   Workspace w;
   if ((rc = check_ws(m, workspace, workspace_bytes, &w, "down"))) return rc;
   return stage_down(m, blocks, scales, bias, bias_dtype, w, path, blocks_layout, static_cast<hipStream_t>(stream));
@@ -2636,8 +2654,8 @@ extern "C" int bsa_moe_experts_fwd(
   BSA_REQUIRE(reinterpret_cast<uintptr_t>(gate_up_blocks) % 8 == 0 &&
                   reinterpret_cast<uintptr_t>(down_blocks) % 8 == 0,
               "experts fwd: packed blocks must be 8-byte aligned");
-  if ((rc = check_layout(blocks_layout, gate_up_blocks, gate_up_scales, 2 * I, H, "experts fwd (gate_up)")) ||
-      (rc = check_layout(blocks_layout, down_blocks, down_scales, H, I, "experts fwd (down)")))
+  if ((rc = check_layout(blocks_layout, gate_up_blocks, 2 * I, H, "experts fwd (gate_up)")) ||
+      (rc = check_layout(blocks_layout, down_blocks, H, I, "experts fwd (down)")))
     return rc;
   Workspace w;
   if ((rc = check_ws(m, workspace, workspace_bytes, &w, "experts fwd"))) return rc;
@@ -2719,8 +2737,8 @@ extern "C" int bsa_moe_experts_bwd(
   BSA_REQUIRE(al(gate_up_blocks, 4) && al(gate_up_scales, 4) && al(down_blocks, 4) && al(down_scales, 4),
               "experts bwd: gate_up/down blocks and scales must be 4-byte aligned");
   BSA_REQUIRE(al(save_gate_up, 16), "experts bwd: save_gate_up must be 16-byte aligned");
-  if ((rc = check_layout(blocks_layout, gate_up_blocks, gate_up_scales, 2 * I, H, "experts bwd (gate_up)")) ||
-      (rc = check_layout(blocks_layout, down_blocks, down_scales, H, I, "experts bwd (down)")))
+  if ((rc = check_layout(blocks_layout, gate_up_blocks, 2 * I, H, "experts bwd (gate_up)")) ||
+      (rc = check_layout(blocks_layout, down_blocks, H, I, "experts bwd (down)")))
     return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t P = T * k;

@@ -26,12 +26,14 @@ from . import kernels
 def dequantize_expert(
     blocks: Tensor, scales: Tensor, dtype: torch.dtype = torch.bfloat16
 ) -> Tensor:
-    """Dequantize one expert's packed MXFP4 weight to a dense matrix.
+    """One expert's MXFP4 weight as a dense ``[K, N]`` matrix, in ``dtype``.
 
-    block_streamer/gptoss.py:24-42: ``blocks`` is ``[1, rows, groups, 16]``
-    uint8 and ``scales`` ``[1, rows, groups]``; returns ``[groups * 32, rows]``
-    in ``dtype``.  A missing expert dimension raises ``ValueError`` whose
-    message contains "packed blocks" (tests/test_offload.py:405-414).
+    block_streamer/gptoss.py:24-42.  Input: packed codes ``[1, N, K/32, 16]``
+    (uint8) and E8M0 exponents ``[1, N, K/32]``, with the expert axis present;
+    output ``[K, N]`` (the GEMM's right operand).  Input without the expert
+    axis is refused with a ``ValueError`` naming the expected "packed blocks"
+    shape (tests/test_offload.py:405-414).  Bit-exact with the transformers
+    converter the reference calls.
     """
     if blocks.dim() != 4:
         raise ValueError(
@@ -105,13 +107,14 @@ class _MoEExperts(torch.autograd.Function):
 
 
 class MXFP4Experts(nn.Module):
-    """Drop-in for ``GptOssExperts`` whose weights stay packed until used.
+    """gpt-oss expert block over packed MXFP4 weights (block_streamer/gptoss.py:78-177).
 
-    block_streamer/gptoss.py:78-177.  Parameter names match the checkpoint
-    exactly, so the shard manifest needs no renaming and the streamed state
-    binds straight through.  As in the reference, the meta shapes use
-    ``hidden_size // 32`` groups for both projections (gptoss.py:92); the
-    kernels take their shapes from the bound tensors.
+    Replaces transformers' dense ``GptOssExperts``.  Its six parameters carry
+    the gpt-oss checkpoint's own tensor names, which is what lets a
+    ``functional_call`` bind staged shard tensors to the module by name.
+    The placeholders live on the meta device and use ``hidden_size // 32``
+    groups for both projections, as gptoss.py:92 does; the kernels read every
+    shape from the tensors actually bound at call time.
     """
 
     def __init__(self, config, dtype: torch.dtype = torch.bfloat16) -> None:

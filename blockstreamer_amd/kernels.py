@@ -92,7 +92,7 @@ def dequantize_mxfp4(blocks: Tensor, scales: Tensor, dtype: torch.dtype = torch.
     blocks = _as_u8(blocks)
     scales = _as_u8(scales)
     if layout == LAYOUT_KPAIR:
-        blocks = _aligned_kpair(blocks)
+        _require_kpair_aligned(blocks, "blocks")
     if out is None:
         out = torch.empty((E, G * 32, R), dtype=dtype, device=dev)
     elif out.shape != (E, G * 32, R) or out.dtype != dtype or not out.is_contiguous():
@@ -143,22 +143,17 @@ def _aligned(t: Tensor, n: int) -> Tensor:
     return t if t.data_ptr() % n == 0 else t.clone()
 
 
-_warned_kpair_copy = False
-
-
-def _aligned_kpair(t: Tensor) -> Tensor:
-    """A k-pair layout tensor on a 16-byte boundary; a misaligned one is
-    copied, with a warning the first time (a shard writer that adopts the
-    layout aligns these tensors to 16 bytes, so the copy is the exception)."""
-    global _warned_kpair_copy
-    if t.data_ptr() % 16 == 0:
-        return t
-    if not _warned_kpair_copy:
-        import warnings
-        warnings.warn("k-pair layout blocks or scales are not 16-byte aligned and are copied on every call; "
-                      "align them to 16 bytes when writing the shards", RuntimeWarning, stacklevel=3)
-        _warned_kpair_copy = True
-    return t.clone()
+def _require_kpair_aligned(blocks: Tensor, what: str) -> Tensor:
+    """k-pair layout blocks move in 16-byte pieces only, so they must start
+    on a 16-byte boundary.  The reference's shard planner aligns tensors to
+    8 bytes (block_streamer/shards.py:148-165); a writer that stores the
+    k-pair layout aligns them to 16.  Copying on every call would move the
+    whole tensor each time, so a misaligned tensor is refused instead."""
+    if blocks.data_ptr() % 16:
+        raise ValueError(f"{what} in the k-pair layout must be 16-byte aligned (address % 16 = "
+                         f"{blocks.data_ptr() % 16}); write k-pair shards with 16-byte tensor alignment, "
+                         f"or repack with from_kpair()")
+    return blocks
 
 
 def _aligned_bytes(nbytes: int, device, align: int = 256) -> Tensor:
@@ -181,6 +176,12 @@ def _check_packed(blocks: Tensor, scales: Tensor, E: int, rows: int, K: int, wha
     if tuple(scales.shape) != want:
         raise ValueError(f"{what}_scales must be {list(want)}, got {list(scales.shape)}")
     return layout
+
+
+def _check_bias(bias: Tensor | None, E: int, n: int, what: str) -> None:
+    """The kernels read a bias as ``[E][n]``; anything else would read past it."""
+    if bias is not None and tuple(bias.shape) != (E, n):
+        raise ValueError(f"{what}_bias must be [{E}, {n}], got {list(bias.shape)}")
 
 
 def _experts_dims(gate_up_blocks: Tensor) -> tuple[int, int]:
@@ -214,6 +215,8 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
     layout = _check_packed(gate_up_blocks, gate_up_scales, E, 2 * I, H, "gate_up_proj")
     if _check_packed(down_blocks, down_scales, E, H, I, "down_proj") != layout:
         raise ValueError("gate_up and down blocks must be in the same layout")
+    _check_bias(gate_up_bias, E, 2 * I, "gate_up_proj")
+    _check_bias(down_bias, E, H, "down_proj")
     dev = _lib.require_gpu(hidden, router_indices, routing_weights, gate_up_blocks,
                            gate_up_scales, down_blocks, down_scales, gate_up_bias, down_bias)
     out_dtype = hidden.dtype
@@ -229,7 +232,8 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
     dnb = down_bias.to(bias_dtype.dtype).contiguous() if down_bias is not None else None
     gu_b, gu_s, dn_b, dn_s = (_as_u8(x) for x in (gate_up_blocks, gate_up_scales, down_blocks, down_scales))
     if layout == LAYOUT_KPAIR:  # the k-pair layout moves in 16-byte pieces only
-        gu_b, gu_s, dn_b, dn_s = (_aligned_kpair(x) for x in (gu_b, gu_s, dn_b, dn_s))
+        _require_kpair_aligned(gu_b, "gate_up_proj_blocks")
+        _require_kpair_aligned(dn_b, "down_proj_blocks")
     out = torch.empty((T, H), dtype=out_dtype, device=dev)
     ws_bytes = moe_workspace_bytes(T, H, I, E, k)
     ws = _aligned_bytes(ws_bytes, dev)
@@ -266,6 +270,10 @@ class MoEStages:
         self.layout = _check_packed(gate_up_blocks, gate_up_scales, self.E, 2 * self.I, self.H, "gate_up_proj")
         if _check_packed(down_blocks, down_scales, self.E, self.H, self.I, "down_proj") != self.layout:
             raise ValueError("gate_up and down blocks must be in the same layout")
+        _check_bias(gate_up_bias, self.E, 2 * self.I, "gate_up_proj")
+        _check_bias(down_bias, self.E, self.H, "down_proj")
+        if down_bias is not None and gate_up_bias is not None and down_bias.dtype != gate_up_bias.dtype:
+            raise ValueError("MoEStages takes gate_up and down biases of one dtype")
         self.dev = _lib.require_gpu(hidden, router_indices, routing_weights, gate_up_blocks)
         if hidden.dtype != torch.bfloat16 or not hidden.is_contiguous():
             raise ValueError("MoEStages takes contiguous bfloat16 hidden states")
@@ -332,13 +340,28 @@ def moe_experts_backward(grad_out: Tensor, hidden: Tensor, router_indices: Tenso
     dtypes of ``hidden`` and ``routing_weights``.  Expert weights and biases
     get no gradient (frozen under LoRA, block_streamer/lora.py:138-148).
     """
+    if hidden.dim() != 2:
+        raise ValueError(f"hidden_states must be [tokens, hidden], got {tuple(hidden.shape)}")
     T, H = hidden.shape
+    if tuple(grad_out.shape) != (T, H):
+        raise ValueError(f"grad_out must be [{T}, {H}] like the hidden states, got {list(grad_out.shape)}")
+    if router_indices.dim() != 2 or router_indices.shape[0] != T:
+        raise ValueError("router_indices must be [tokens, top_k]")
+    if tuple(routing_weights.shape) != tuple(router_indices.shape):
+        raise ValueError("routing_weights must match router_indices in shape")
     k = router_indices.shape[1]
     E, I = _experts_dims(gate_up_blocks)
-    layout = blocks_layout(gate_up_blocks)
-    if blocks_layout(down_blocks) != layout:
+    layout = _check_packed(gate_up_blocks, gate_up_scales, E, 2 * I, H, "gate_up_proj")
+    if _check_packed(down_blocks, down_scales, E, H, I, "down_proj") != layout:
         raise ValueError("gate_up and down blocks must be in the same layout")
-    dev = _lib.require_gpu(grad_out, hidden, router_indices, routing_weights, workspace)
+    if gate_up_pre.dtype != torch.float32 or tuple(gate_up_pre.shape) != (T * k, 2 * I):
+        raise ValueError(f"gate_up_pre must be the forward's float32 [{T * k}, {2 * I}] save, "
+                         f"got {gate_up_pre.dtype} {list(gate_up_pre.shape)}")
+    ws_need = moe_workspace_bytes(T, H, I, E, k)
+    if workspace.dtype != torch.uint8 or workspace.numel() < ws_need:
+        raise ValueError(f"workspace must be the forward's uint8 workspace of >= {ws_need} bytes")
+    dev = _lib.require_gpu(grad_out, hidden, router_indices, routing_weights, workspace, gate_up_pre,
+                           gate_up_blocks, gate_up_scales, down_blocks, down_scales)
     if T == 0:
         return (torch.zeros_like(hidden) if need_hidden else None,
                 torch.zeros_like(routing_weights) if need_weights else None)
@@ -349,12 +372,13 @@ def moe_experts_backward(grad_out: Tensor, hidden: Tensor, router_indices: Tenso
     # the backward kernels DMA the packed weights in 16- or 4-byte pieces
     # (staging-blob views are 8-byte aligned; the k-pair layout moves in
     # 16-byte pieces only) and the pre-activations in 16
+    gub, gus, dnb, dns = (_as_u8(x) for x in (gate_up_blocks, gate_up_scales, down_blocks, down_scales))
     if layout == LAYOUT_KPAIR:
-        gub, gus, dnb, dns = (_aligned_kpair(_as_u8(x)) for x in (gate_up_blocks, gate_up_scales,
-                                                                   down_blocks, down_scales))
+        _require_kpair_aligned(gub, "gate_up_proj_blocks")
+        _require_kpair_aligned(dnb, "down_proj_blocks")
     else:
-        gub, gus, dnb, dns = (_aligned(_as_u8(x), 4) for x in (gate_up_blocks, gate_up_scales,
-                                                                down_blocks, down_scales))
+        gub, dnb = _aligned(gub, 4), _aligned(dnb, 4)
+    gus, dns = _aligned(gus, 4), _aligned(dns, 4)
     pre = _aligned(gate_up_pre.contiguous(), 16)
     bwd_bytes = moe_bwd_workspace_bytes(T, H, I, E, k)
     bws = _aligned_bytes(bwd_bytes, dev)

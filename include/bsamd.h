@@ -55,8 +55,12 @@ extern "C" {
 /* Thread-local message describing the last failure of this thread. */
 const char *bsa_last_error(void);
 
-/* ABI version of this library (major * 100 + minor); 101 added the blocks
- * layout argument and the k-pair entry points. */
+/* ABI version of this library (major * 100 + minor).  The major number
+ * changes whenever an existing signature changes: 2 inserted the
+ * blocks_layout argument before the stream in bsa_moe_experts_fwd,
+ * bsa_moe_gate_up, bsa_moe_down and bsa_moe_experts_bwd.  A binding checks
+ * the major number before its first call. */
+#define BSA_VERSION_MAJOR 2
 int bsa_version(void);
 
 /*

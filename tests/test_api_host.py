@@ -60,3 +60,76 @@ def test_experts_refuse_mixed_layouts_before_the_gpu():
     wrong_k = torch.zeros(E, 2 * I, H // 32 + 1, 16, dtype=torch.uint8)
     with pytest.raises(ValueError, match="gate_up_proj_blocks must be"):
         kernels.moe_experts_forward(h, idx, w, wrong_k, gus, None, dnb, dns, None)
+
+
+def _small_experts(E=2, H=64, I=64, layout="checkpoint"):
+    if layout == "kpair":
+        gub = torch.zeros(E, 2 * I // 16, H // 64, 16, 2, 16, dtype=torch.uint8)
+        dnb = torch.zeros(E, H // 16, I // 64, 16, 2, 16, dtype=torch.uint8)
+    else:
+        gub = torch.zeros(E, 2 * I, H // 32, 16, dtype=torch.uint8)
+        dnb = torch.zeros(E, H, I // 32, 16, dtype=torch.uint8)
+    return (gub, torch.zeros(E, 2 * I, H // 32, dtype=torch.uint8), torch.zeros(E, 2 * I, dtype=torch.bfloat16),
+            dnb, torch.zeros(E, H, I // 32, dtype=torch.uint8), torch.zeros(E, H, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("which,shape", [("gate_up_proj", (128,)), ("gate_up_proj", (2, 64)),
+                                         ("down_proj", (2, 32)), ("down_proj", (3, 64))])
+def test_experts_refuse_wrong_bias_shapes_before_the_gpu(which, shape):
+    """The kernels read the biases as [E, 2I] and [E, H]; any other shape is a
+    ValueError on the host (it would read past the tensor on the device)."""
+    from blockstreamer_amd import kernels
+    E, k, H, I, T = 2, 1, 64, 64, 4
+    h = torch.zeros(T, H, dtype=torch.bfloat16)
+    idx = torch.zeros(T, k, dtype=torch.int64)
+    w = torch.ones(T, k)
+    gub, gus, gubias, dnb, dns, dnbias = _small_experts(E, H, I)
+    bad = torch.zeros(shape, dtype=torch.bfloat16)
+    if which == "gate_up_proj":
+        gubias = bad
+    else:
+        dnbias = bad
+    with pytest.raises(ValueError, match=f"{which}_bias must be"):
+        kernels.moe_experts_forward(h, idx, w, gub, gus, gubias, dnb, dns, dnbias)
+    with pytest.raises(ValueError, match=f"{which}_bias must be"):
+        kernels.MoEStages(h, idx, w, gub, gus, gubias, dnb, dns, dnbias)
+
+
+def test_backward_refuses_bad_arguments_before_the_gpu():
+    """Shapes and dtypes of every backward input are checked on the host."""
+    from blockstreamer_amd import kernels
+    E, k, H, I, T = 2, 2, 64, 64, 4
+    h = torch.zeros(T, H, dtype=torch.bfloat16)
+    idx = torch.zeros(T, k, dtype=torch.int64)
+    w = torch.ones(T, k)
+    gub, gus, _, dnb, dns, _ = _small_experts(E, H, I)
+    ws = torch.zeros(1 << 20, dtype=torch.uint8)
+    pre = torch.zeros(T * k, 2 * I, dtype=torch.float32)
+    g = torch.zeros(T, H, dtype=torch.bfloat16)
+
+    def call(**over):
+        args = dict(grad_out=g, hidden=h, router_indices=idx, routing_weights=w, gate_up_blocks=gub,
+                    gate_up_scales=gus, down_blocks=dnb, down_scales=dns, workspace=ws, gate_up_pre=pre)
+        args.update(over)
+        return kernels.moe_experts_backward(**args)
+
+    with pytest.raises(ValueError, match="grad_out must be"):
+        call(grad_out=torch.zeros(T, H + 32, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="gate_up_pre must be"):
+        call(gate_up_pre=pre.to(torch.bfloat16))
+    with pytest.raises(ValueError, match="gate_up_pre must be"):
+        call(gate_up_pre=pre[:-1])
+    with pytest.raises(ValueError, match="down_proj_blocks must be"):
+        call(down_blocks=torch.zeros(E, H, I // 32 + 1, 16, dtype=torch.uint8))
+    with pytest.raises(ValueError, match="gate_up_proj_scales must be"):
+        call(gate_up_scales=gus[:, :-1])
+    with pytest.raises(ValueError, match="routing_weights must match"):
+        call(routing_weights=w[:, :1])
+    with pytest.raises(ValueError, match="workspace"):
+        call(workspace=ws[:16])
+    with pytest.raises(ValueError, match="same layout"):
+        kp = _small_experts(E, H, I, "kpair")
+        call(gate_up_blocks=kp[0])
+    # well-formed arguments get as far as the device check
+    with pytest.raises(ValueError, match="GPU only"):
+        call()

@@ -68,8 +68,8 @@ CASES = [
     ("fwd unknown layout", "bsa_moe_experts_fwd", _fwd_args(layout=5), _lib.BSA_EINVAL, b"layout"),
     ("fwd k-pair odd groups", "bsa_moe_experts_fwd", _fwd_args(H=96, layout=1), _lib.BSA_EINVAL,
      b"even group count"),
-    ("fwd k-pair scales alignment", "bsa_moe_experts_fwd", _fwd_args(layout=1, scales=FAKE + 8), _lib.BSA_EINVAL,
-     b"16-byte aligned blocks and scales"),
+    ("fwd k-pair blocks alignment", "bsa_moe_experts_fwd", _fwd_args(layout=1, ptr=FAKE + 8), _lib.BSA_EINVAL,
+     b"16-byte aligned blocks"),
     ("gate_up unknown layout", "bsa_moe_gate_up",
      (FAKE, 4, 64, 64, 8, 2, FAKE, FAKE, None, BF16, 1.702, 7.0, FAKE, 1 << 20, None, 0, 3, None),
      _lib.BSA_EINVAL, b"layout"),

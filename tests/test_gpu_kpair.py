@@ -155,24 +155,66 @@ def test_module_binds_k_pair_tensors(device):
     assert _same(got, want)
 
 
-def test_misaligned_k_pair_view_is_copied_with_a_warning(device):
-    """A k-pair tensor at an 8-byte offset (a blob written with the
-    checkpoint's 8-byte alignment) is copied, with a warning, and gives the
-    same bits."""
+def _at_offset(x: torch.Tensor, by: int) -> torch.Tensor:
+    """Same bytes, storage starting ``by`` bytes past a 16-byte boundary."""
+    buf = torch.empty(x.numel() + 32, dtype=torch.uint8, device=x.device)
+    off = (by - buf.data_ptr()) % 16
+    v = buf[off:off + x.numel()].view(x.shape)
+    v.copy_(x)
+    assert v.data_ptr() % 16 == by
+    return v
+
+
+def test_misaligned_k_pair_blocks_are_refused(device):
+    """k-pair blocks at an 8-byte offset (a blob written with the checkpoint's
+    8-byte alignment) are a ValueError, not a copy on every call."""
     E, k, H, I, T = 8, 2, 256, 256, 16
     t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=12, scale_lo=116, scale_hi=122,
                             device=device)
-    idx, w = synthetic.random_routing(T, E, k, seed=6, dtype=torch.float32)
-    idx, w = idx.to(device), w.to(device)
+    idx, w = synthetic.random_routing(T, E, k, seed=6, dtype=torch.float32, device=device)
     kp = _kp_args(t)
-    buf = torch.empty(kp[0].numel() + 8, dtype=torch.uint8, device=device)
-    view = buf[8:].view(kp[0].shape)
-    view.copy_(kp[0])
-    kp[0] = view
-    assert view.data_ptr() % 16 == 8
-    kernels._warned_kpair_copy = False
-    announce("k-pair misaligned view")
-    with pytest.warns(RuntimeWarning, match="16-byte aligned"):
-        got = kernels.moe_experts_forward(t["hidden"], idx, w, *kp)
-    want = kernels.moe_experts_forward(t["hidden"], idx, w, *[t[n] for n in NAMES])
-    assert _same(got, want)
+    kp[0] = _at_offset(kp[0], 8)
+    announce("k-pair misaligned blocks refused")
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        kernels.moe_experts_forward(t["hidden"], idx, w, *kp)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        kernels.dequantize_mxfp4(kp[0], kp[1])
+    ws = torch.zeros(kernels.moe_workspace_bytes(T, H, I, E, k), dtype=torch.uint8, device=device)
+    pre = torch.zeros(T * k, 2 * I, dtype=torch.float32, device=device)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        kernels.moe_experts_backward(t["hidden"], t["hidden"], idx, w, kp[0], kp[1], kp[3], kp[4], ws, pre)
+
+
+@pytest.mark.parametrize("dims", [(8, 2, 256, 256, 16), (8, 2, 256, 256, 300), (4, 4, 2880, 2880, 8)],
+                         ids=["small-decode", "small-prefill", "gptoss-decode"])
+@pytest.mark.parametrize("by", [8, 4])
+def test_k_pair_blocks_with_unaligned_scales(device, dims, by):
+    """k-pair blocks on a 16-byte boundary with scales only 8- or 4-byte
+    aligned (the checkpoint's shard alignment): every forward path and the
+    backward give the checkpoint layout's bits.  The checkpoint call gets the
+    same scale alignment, since alignment picks the kernel (at K = 2880 the
+    persistent decode kernel needs 16-byte aligned scales, and the streaming
+    kernel that replaces it rounds differently)."""
+    E, k, H, I, T = dims
+    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=13 + T, scale_lo=116, scale_hi=122,
+                            device=device)
+    idx, w = synthetic.random_routing(T, E, k, seed=7, dtype=torch.float32, device=device)
+    kp = _kp_args(t)
+    kp[1] = _at_offset(kp[1], by)
+    kp[4] = _at_offset(kp[4], by)
+    ck = [t[n] for n in NAMES]
+    ck[1] = _at_offset(ck[1], by)
+    ck[4] = _at_offset(ck[4], by)
+    for path in ("auto", "stream", "tiled", "mx"):
+        announce(f"k-pair blocks, scales {by} bytes off, path={path}, {dims}")
+        want = kernels.moe_experts_forward(t["hidden"], idx, w, *ck, path=path)
+        got = kernels.moe_experts_forward(t["hidden"], idx, w, *kp, path=path)
+        assert _same(got, want), path
+    announce(f"k-pair blocks, scales {by} bytes off, backward, {dims}")
+    g = torch.randn(T, H, device=device).to(torch.bfloat16)
+    outs = []
+    for a in (ck, kp):
+        _, ws, pre = kernels.moe_experts_forward(t["hidden"], idx, w, *a, save=True)
+        outs.append(kernels.moe_experts_backward(g, t["hidden"], idx, w, a[0], a[1], a[3], a[4], ws, pre))
+    torch.cuda.synchronize()
+    assert _same(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])

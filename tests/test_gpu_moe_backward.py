@@ -114,7 +114,7 @@ def test_no_grad_forward_saves_nothing(device):
 def _gpu_fp32_reference_grads(t, idx, w, g):
     """float32 torch autograd on the GPU, dense weights from the dequant kernel."""
     h = t["hidden"].float().requires_grad_(True)
-    wr = w.float().requires_grad_(True)
+    wr = w.detach().float().clone().requires_grad_(True)
     out = torch.zeros_like(h)
     for e in torch.unique(idx).tolist():
         tok, pos = torch.where(idx == e)

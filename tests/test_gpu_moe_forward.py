@@ -103,7 +103,7 @@ def test_gptoss_120b_decode_vs_oracle(device, T):
     announce(f"moe 120b decode T={T}")
     got = kernels.moe_experts_forward(t["hidden"], idx.to(device), scores.to(device),
                                       *expert_args(t))
-    tokens = torch.arange(min(T, 8))
+    tokens = torch.arange(T)  # every token of the batch
     want = oracle_tokens(t, idx, scores, tokens)
     assert_layer_close(got.cpu()[tokens], want, f"120b decode T={T}")
 
@@ -116,7 +116,7 @@ def test_gptoss_120b_decode_realistic_scales_absolute(device):
     announce("moe 120b decode realistic scales")
     got = kernels.moe_experts_forward(t["hidden"], idx.to(device), scores.to(device),
                                       *expert_args(t))
-    tokens = torch.tensor([0, 9, 33, 63])
+    tokens = torch.arange(64)
     want = oracle_tokens(t, idx, scores, tokens)
     assert_layer_close(got.cpu()[tokens], want, "120b decode realistic", absolute=True)
 
@@ -135,7 +135,7 @@ def test_gptoss_20b_full_layer(device, path):
     got = kernels.moe_experts_forward(t["hidden"], idx, scores, *expert_args(t), path=path)
     ref = gpu_reference(t, idx, scores)
     assert_layer_close(got, ref, f"20b all tokens {path}")
-    tokens = torch.tensor([0, 1, 1000, 2047])
+    tokens = torch.randperm(2048, generator=torch.Generator().manual_seed(20))[:64]
     assert_layer_close(got.cpu()[tokens], oracle_tokens(t, idx, scores, tokens), f"20b oracle {path}")
 
 
