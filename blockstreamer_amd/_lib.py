@@ -41,6 +41,14 @@ _SIGNATURES = {
         _ptr, _int, _ptr, _i64, _ptr, _int,       # out, out dtype, ws, ws bytes, save, path
         _int, _ptr,                               # blocks layout, stream
     ],
+    "bsa_moe_experts_fwd_noalloc": [
+        _ptr, _i64, _i64, _i64, _i64, _i64,      # hidden, T, H, I, E, k
+        _ptr, _ptr, _int,                        # indices, weights, weight dtype
+        _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _int,  # gate_up b/s/bias, down b/s/bias, bias dtype
+        _f32, _f32,                              # alpha, limit
+        _ptr, _int, _ptr, _int,                  # out, out dtype, save, path
+        _int, _ptr,                               # blocks layout, stream
+    ],
     "bsa_moe_dispatch": [_ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr],
     "bsa_moe_gate_up": [_ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr, _int, _f32, _f32,
                         _ptr, _i64, _ptr, _int, _int, _ptr],

@@ -48,6 +48,8 @@
 // (odd) columns (gptoss.py:131).  Every forward kernel places gate column j
 // and up column j in the same lane (or adjacent lanes), so the clamped SwiGLU
 // runs in registers.
+#include <mutex>
+
 #include "bsa_common.h"
 
 namespace bsa {
@@ -2633,33 +2635,93 @@ extern "C" int bsa_moe_combine(const int64_t* router_indices, const void* routin
                         (int)k, (int)H, out, out_dtype, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int bsa_moe_experts_fwd(
-    const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+namespace bsa {
+
+// ---------------------------------------------------------------------------
+// Workspace of the no-allocation forward: a file-scope device array, one copy
+// per GPU, alive until the process ends.  Host code never passes the array's
+// name to a kernel (on the host it is only a stand-in symbol); it passes the
+// device address hipGetSymbolAddress returns, looked up once per device with
+// that device current.  Every no-allocation call on a GPU uses that GPU's
+// copy, so such calls must not overlap on one GPU (one stream at a time, or
+// ordered by events).  The forward writes every workspace word it later
+// reads, so nothing needs clearing between calls.
+// ---------------------------------------------------------------------------
+constexpr int64_t NOALLOC_SCRATCH_BYTES = BSA_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+// Device address of `scratch` on the device that owns stream `st` (the
+// current device for the null stream).
+static int scratch_of_stream(hipStream_t st, void** out) {
+  int dev = -1;
+  hipError_t e = st ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("no-alloc scratch: cannot find the stream's device: %s", hipGetErrorString(e));
+    return BSA_EHIP;
+  }
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) {
+    set_error("no-alloc scratch: device %d beyond the %d supported", dev, NOALLOC_MAX_DEVICES);
+    return BSA_EINVAL;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    if ((e = hipGetDevice(&cur)) == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur >= 0 && cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || !p) {
+      set_error("no-alloc scratch: hipGetSymbolAddress on device %d: %s", dev,
+                e != hipSuccess ? hipGetErrorString(e) : "null address");
+      return BSA_EHIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return BSA_OK;
+}
+
+// The whole forward (dispatch, gate_up, down, combine) on one workspace;
+// `what` names the entry point in error messages.  With `noalloc` the
+// workspace is the static scratch of the stream's device.
+static int experts_fwd(
+    const char* what, bool noalloc, const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
     const int64_t* router_indices, const void* routing_weights, int weight_dtype,
     const void* gate_up_blocks, const void* gate_up_scales, const void* gate_up_bias,
     const void* down_blocks, const void* down_scales, const void* down_bias, int bias_dtype,
     float alpha, float limit, void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
     void* save_gate_up, int path, int blocks_layout, void* stream) {
-  clear_error();
   const MoeShape m{T, H, I, E, k};
-  int rc = check_shape(m, "experts fwd");
+  int rc = check_shape(m, what);
   if (rc || T == 0) return rc;
   BSA_REQUIRE(dtype_ok(weight_dtype) && dtype_ok(bias_dtype) && dtype_ok(out_dtype),
-              "experts fwd: bad dtype code");
-  BSA_REQUIRE(path >= 0 && path <= 3, "experts fwd: path must be 0, 1, 2 or 3");
+              "%s: bad dtype code", what);
+  BSA_REQUIRE(path >= 0 && path <= 3, "%s: path must be 0, 1, 2 or 3", what);
   BSA_REQUIRE(hidden && router_indices && routing_weights && gate_up_blocks && gate_up_scales &&
                   down_blocks && down_scales && out,
-              "experts fwd: null pointer");
-  BSA_REQUIRE(reinterpret_cast<uintptr_t>(hidden) % 16 == 0, "experts fwd: hidden must be 16-byte aligned");
+              "%s: null pointer", what);
+  BSA_REQUIRE(reinterpret_cast<uintptr_t>(hidden) % 16 == 0, "%s: hidden must be 16-byte aligned", what);
   BSA_REQUIRE(reinterpret_cast<uintptr_t>(gate_up_blocks) % 8 == 0 &&
                   reinterpret_cast<uintptr_t>(down_blocks) % 8 == 0,
-              "experts fwd: packed blocks must be 8-byte aligned");
+              "%s: packed blocks must be 8-byte aligned", what);
   if ((rc = check_layout(blocks_layout, gate_up_blocks, 2 * I, H, "experts fwd (gate_up)")) ||
       (rc = check_layout(blocks_layout, down_blocks, H, I, "experts fwd (down)")))
     return rc;
-  Workspace w;
-  if ((rc = check_ws(m, workspace, workspace_bytes, &w, "experts fwd"))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (noalloc) {
+    workspace_bytes = carve(nullptr, T, H, I, E, k).bytes;
+    BSA_REQUIRE(workspace_bytes <= NOALLOC_SCRATCH_BYTES,
+                "%s: this shape needs %lld bytes of workspace and the static scratch holds %lld; "
+                "call bsa_moe_experts_fwd with a workspace instead",
+                what, (long long)workspace_bytes, (long long)NOALLOC_SCRATCH_BYTES);
+    if ((rc = scratch_of_stream(st, &workspace))) return rc;
+  }
+  Workspace w;
+  if ((rc = check_ws(m, workspace, workspace_bytes, &w, what))) return rc;
   if ((rc = stage_dispatch(m, router_indices, w, st))) return rc;
   if ((rc = stage_gate_up(m, hidden, gate_up_blocks, gate_up_scales, gate_up_bias, bias_dtype, alpha,
                           limit, w, save_gate_up, path, blocks_layout, st)))
@@ -2668,6 +2730,36 @@ extern "C" int bsa_moe_experts_fwd(
     return rc;
   return launch_combine(w.y, router_indices, routing_weights, weight_dtype, w.pair_pos, (int)T,
                         (int)k, (int)H, out, out_dtype, st);
+}
+
+}  // namespace bsa
+
+extern "C" int bsa_moe_experts_fwd(
+    const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+    const int64_t* router_indices, const void* routing_weights, int weight_dtype,
+    const void* gate_up_blocks, const void* gate_up_scales, const void* gate_up_bias,
+    const void* down_blocks, const void* down_scales, const void* down_bias, int bias_dtype,
+    float alpha, float limit, void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
+    void* save_gate_up, int path, int blocks_layout, void* stream) {
+  clear_error();
+  return experts_fwd("experts fwd", false, hidden, T, H, I, E, k, router_indices, routing_weights, weight_dtype,
+                     gate_up_blocks, gate_up_scales, gate_up_bias, down_blocks, down_scales, down_bias,
+                     bias_dtype, alpha, limit, out, out_dtype, workspace, workspace_bytes, save_gate_up,
+                     path, blocks_layout, stream);
+}
+
+extern "C" int bsa_moe_experts_fwd_noalloc(
+    const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+    const int64_t* router_indices, const void* routing_weights, int weight_dtype,
+    const void* gate_up_blocks, const void* gate_up_scales, const void* gate_up_bias,
+    const void* down_blocks, const void* down_scales, const void* down_bias, int bias_dtype,
+    float alpha, float limit, void* out, int out_dtype, void* save_gate_up, int path,
+    int blocks_layout, void* stream) {
+  clear_error();
+  return experts_fwd("experts fwd (no-alloc)", true, hidden, T, H, I, E, k, router_indices, routing_weights,
+                     weight_dtype, gate_up_blocks, gate_up_scales, gate_up_bias, down_blocks, down_scales,
+                     down_bias, bias_dtype, alpha, limit, out, out_dtype, nullptr, 0, save_gate_up, path,
+                     blocks_layout, stream);
 }
 
 namespace bsa {

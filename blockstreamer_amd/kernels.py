@@ -194,7 +194,7 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
                         gate_up_blocks: Tensor, gate_up_scales: Tensor, gate_up_bias: Tensor | None,
                         down_blocks: Tensor, down_scales: Tensor, down_bias: Tensor | None,
                         alpha: float = 1.702, limit: float = 7.0, *, save: bool = False,
-                        path: str = "auto"):
+                        path: str = "auto", noalloc: bool = False):
     """Fused MoE experts forward (block_streamer/gptoss.py:137-177).
 
     ``hidden [T, H]``, ``router_indices [T, k]``, ``routing_weights [T, k]``;
@@ -202,7 +202,15 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
     dtype of ``hidden``; with ``save=True`` also ``(workspace, gate_up_pre)``
     for the input-gradient backward.  Activations enter the MFMA as bfloat16,
     except on ``path="mx"`` (MXFP8, see ``PATHS``).
+
+    ``noalloc=True`` runs the same kernels through
+    ``bsa_moe_experts_fwd_noalloc``, whose workspace is the library's static
+    per-GPU scratch (16 MiB: decode batches); only the output is allocated
+    here.  Calls of it that overlap on one GPU race, and it cannot save for
+    the backward (the next call overwrites the scratch).
     """
+    if noalloc and save:
+        raise ValueError("noalloc=True cannot save for the backward: the scratch is shared by every call")
     if hidden.dim() != 2:
         raise ValueError(f"hidden_states must be [tokens, hidden], got {tuple(hidden.shape)}")
     if router_indices.dim() != 2 or router_indices.shape[0] != hidden.shape[0]:
@@ -235,19 +243,24 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
         _require_kpair_aligned(gu_b, "gate_up_proj_blocks")
         _require_kpair_aligned(dn_b, "down_proj_blocks")
     out = torch.empty((T, H), dtype=out_dtype, device=dev)
-    ws_bytes = moe_workspace_bytes(T, H, I, E, k)
-    ws = _aligned_bytes(ws_bytes, dev)
-    save_pre = torch.empty((T * k, 2 * I), dtype=torch.float32, device=dev) if save else None
 
     def ptr(t):
         return t.data_ptr() if t is not None else None
 
+    common = (x.data_ptr(), T, H, I, E, k, idx.data_ptr(), w.data_ptr(), w_code, gu_b.data_ptr(),
+              gu_s.data_ptr(), ptr(gub), dn_b.data_ptr(), dn_s.data_ptr(), ptr(dnb), bias_code,
+              float(alpha), float(limit), out.data_ptr(), out_code)
+    if noalloc:
+        with torch.cuda.device(dev):
+            _lib.call("bsa_moe_experts_fwd_noalloc", *common, None, PATHS[path], layout,
+                      _lib.stream_handle(dev))
+        return out
+    ws_bytes = moe_workspace_bytes(T, H, I, E, k)
+    ws = _aligned_bytes(ws_bytes, dev)
+    save_pre = torch.empty((T * k, 2 * I), dtype=torch.float32, device=dev) if save else None
     with torch.cuda.device(dev):
-        _lib.call("bsa_moe_experts_fwd", x.data_ptr(), T, H, I, E, k, idx.data_ptr(),
-                  w.data_ptr(), w_code, gu_b.data_ptr(), gu_s.data_ptr(), ptr(gub),
-                  dn_b.data_ptr(), dn_s.data_ptr(), ptr(dnb), bias_code, float(alpha),
-                  float(limit), out.data_ptr(), out_code, ws.data_ptr(), ws_bytes,
-                  ptr(save_pre), PATHS[path], layout, _lib.stream_handle(dev))
+        _lib.call("bsa_moe_experts_fwd", *common, ws.data_ptr(), ws_bytes, ptr(save_pre), PATHS[path],
+                  layout, _lib.stream_handle(dev))
     if save:
         return out, ws, save_pre
     return out

@@ -4,7 +4,9 @@
  * Every entry point takes plain device pointers, element counts and a HIP
  * stream (hipStream_t passed as void*; NULL = the legacy default stream), is
  * asynchronous on that stream, never synchronises and never allocates: the
- * caller owns every buffer, workspace included.  The return value is a
+ * caller owns every buffer, workspace included (bsa_moe_experts_fwd_noalloc
+ * alone takes its workspace from a static array of the library instead).
+ * The return value is a
  * status code; on failure bsa_last_error() returns a thread-local message.
  *
  * Tensors are dense row-major.  Packed MXFP4 weights keep the gpt-oss
@@ -58,8 +60,9 @@ const char *bsa_last_error(void);
 /* ABI version of this library (major * 100 + minor).  The major number
  * changes whenever an existing signature changes: 2 inserted the
  * blocks_layout argument before the stream in bsa_moe_experts_fwd,
- * bsa_moe_gate_up, bsa_moe_down and bsa_moe_experts_bwd.  A binding checks
- * the major number before its first call. */
+ * bsa_moe_gate_up, bsa_moe_down and bsa_moe_experts_bwd.  The minor number
+ * counts added entry points (201: bsa_moe_experts_fwd_noalloc).  A binding
+ * checks the major number before its first call. */
 #define BSA_VERSION_MAJOR 2
 int bsa_version(void);
 
@@ -171,6 +174,34 @@ int bsa_moe_experts_fwd(
     const void *down_bias, int bias_dtype, float alpha, float limit, void *out,
     int out_dtype, void *workspace, int64_t workspace_bytes,
     void *save_gate_up, int path, int blocks_layout, void *stream);
+
+/*
+ * bsa_moe_experts_fwd without the workspace arguments: the same kernels and
+ * the same results bit for bit, with the workspace taken from a static
+ * device array of the library (BSA_NOALLOC_SCRATCH_BYTES, one copy per GPU,
+ * held until the process ends).  Nothing is allocated: no hipMalloc, no
+ * hipFree, no allocating library call.
+ *
+ * No counterpart in the reference.  It is for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, and
+ * harnesses that forbid allocation.
+ *
+ * Limit: the shape's bsa_moe_workspace_bytes must be at most
+ * BSA_NOALLOC_SCRATCH_BYTES (16 MiB: about 190 tokens at top-4 with
+ * H = I = 2880, i.e. decode batches); larger shapes return BSA_EINVAL.
+ * Every call on one GPU shares that GPU's array, so calls that overlap on a
+ * GPU (concurrent streams, threads) race; order them.  The array's contents
+ * after a call are those of the last call; no call relies on them.
+ */
+#define BSA_NOALLOC_SCRATCH_BYTES (16ll << 20)
+int bsa_moe_experts_fwd_noalloc(
+    const void *hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+    const int64_t *router_indices, const void *routing_weights,
+    int weight_dtype, const void *gate_up_blocks, const void *gate_up_scales,
+    const void *gate_up_bias, const void *down_blocks, const void *down_scales,
+    const void *down_bias, int bias_dtype, float alpha, float limit, void *out,
+    int out_dtype, void *save_gate_up, int path, int blocks_layout,
+    void *stream);
 
 /*
  * The four stages bsa_moe_experts_fwd runs, callable one by one (same

@@ -38,6 +38,12 @@ def _fwd_args(T=4, H=2880, I=2880, E=128, k=4, hidden=FAKE, wdt=BF16, bdt=BF16, 
             ws, ws_bytes, None, path, layout, None)
 
 
+def _noalloc_args(T=4, H=2880, I=2880, E=128, k=4, hidden=FAKE, ptr=FAKE, path=0):
+    """bsa_moe_experts_fwd_noalloc: the forward's arguments without the workspace pair."""
+    a = _fwd_args(T=T, H=H, I=I, E=E, k=k, hidden=hidden, ptr=ptr, path=path, ws_bytes=0)
+    return a[:20] + a[22:]
+
+
 def _bwd_args(T=4, H=2880, I=2880, E=128, k=4, gdt=BF16, blocks=FAKE, save=FAKE, bwd_ws=FAKE,
               bwd_bytes=None, ghdt=BF16, layout=0):
     ws_bytes = _ws_bytes(T, H, I, E, k) if min(H, I, E, k) > 0 and T >= 0 else 0
@@ -70,6 +76,13 @@ CASES = [
      b"even group count"),
     ("fwd k-pair blocks alignment", "bsa_moe_experts_fwd", _fwd_args(layout=1, ptr=FAKE + 8), _lib.BSA_EINVAL,
      b"16-byte aligned blocks"),
+    ("no-alloc k = 0", "bsa_moe_experts_fwd_noalloc", _noalloc_args(k=0), _lib.BSA_EINVAL, b"bad shape"),
+    ("no-alloc T = 0", "bsa_moe_experts_fwd_noalloc", _noalloc_args(T=0, ptr=None, hidden=None), _lib.BSA_OK,
+     None),
+    ("no-alloc null", "bsa_moe_experts_fwd_noalloc", _noalloc_args(ptr=None), _lib.BSA_EINVAL, b"null"),
+    ("no-alloc path", "bsa_moe_experts_fwd_noalloc", _noalloc_args(path=9), _lib.BSA_EINVAL, b"path"),
+    ("no-alloc beyond the scratch", "bsa_moe_experts_fwd_noalloc", _noalloc_args(T=1024), _lib.BSA_EINVAL,
+     b"static scratch"),
     ("gate_up unknown layout", "bsa_moe_gate_up",
      (FAKE, 4, 64, 64, 8, 2, FAKE, FAKE, None, BF16, 1.702, 7.0, FAKE, 1 << 20, None, 0, 3, None),
      _lib.BSA_EINVAL, b"layout"),
@@ -150,6 +163,13 @@ def test_workspace_sizes_grow_with_tokens():
     assert 0 < a < b and a % 256 == 0 and b % 256 == 0
     c = _ws_bytes(64, **{k: v for k, v in GPTOSS.items() if k != "T"}, fn="bsa_moe_bwd_workspace_bytes")
     assert c > 0
+
+
+def test_noalloc_scratch_covers_decode_batches():
+    """The static scratch holds the 120b layer's workspace up to 190 tokens
+    (the decode batches), not 200."""
+    dims = {k: v for k, v in GPTOSS.items() if k != "T"}
+    assert _ws_bytes(190, **dims) <= 16 << 20 < _ws_bytes(200, **dims)
 
 
 def test_python_call_raises_value_error_with_the_message():
