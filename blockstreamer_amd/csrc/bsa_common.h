@@ -168,6 +168,114 @@ __device__ __forceinline__ int64_t bq_off(int kp, int64_t n, int g, int G) {
   return kp ? ((((n >> 4) * (G >> 1) + (g >> 1)) * 32 + (n & 15) * 2 + (g & 1)) * 16) : ((n * G + g) * 16);
 }
 
+// ---------------------------------------------------------------------------
+// OCP MXFP8 (E4M3 elements, one E8M0 scale per 32) arithmetic shared by the
+// activation quantisers.
+// ---------------------------------------------------------------------------
+// E4M3 code of v (RNE, saturating); |v| < 2^9 by construction of the scale.
+__device__ __forceinline__ uint32_t e4m3_rne_sat(float v) {
+  const uint32_t sign = (__float_as_uint(v) >> 24) & 0x80u;
+  const float a = fabsf(v);
+  uint32_t c;
+  if (a >= 448.f) {
+    c = 0x7Eu;
+  } else if (a < 0.015625f) {  // below 2^-6: subnormal steps of 2^-9
+    c = (uint32_t)rintf(a * 512.f);
+  } else {
+    // round the float32 mantissa to 3 bits (ties to even), carrying into the
+    // exponent; then rebias the exponent from 127 to 7
+    const uint32_t b = __float_as_uint(a);
+    c = ((b + 0x7FFFFu + ((b >> 20) & 1u)) >> 20) - (120u << 3);
+    c = c > 0x7Eu ? 0x7Eu : c;
+  }
+  return sign | c;
+}
+
+// 2^-X as a float for X in [-127, 127] (2^-127 is a float32 subnormal).
+__device__ __forceinline__ float pow2_neg(int X) {
+  return X == 127 ? __uint_as_float(0x00400000u) : __uint_as_float((uint32_t)(127 - X) << 23);
+}
+
+// Shared exponent X of a block with largest magnitude amax (finite, >= 0):
+// ceil(log2(amax / 448)), i.e. floor(log2(amax)) - 8, plus 1 when amax's
+// significand exceeds 1.75; clamped to [-127, 127]; -127 for amax = 0.
+__device__ __forceinline__ int mx_shared_exp(float amax) {
+  if (!(amax > 0.f)) return -127;
+  const uint32_t ab = __float_as_uint(amax);
+  const int e = (ab >> 23) ? (int)(ab >> 23) - 127 : (31 - (int)__clz(ab & 0x7FFFFFu)) - 149;
+  // a float32 subnormal amax clamps to -127 either way
+  return min(max(e - 8 + ((ab & 0x7FFFFFu) > 0x600000u ? 1 : 0), -127), 127);
+}
+
+// Value of a finite E4M3 code (bias 7; subnormals m * 2^-9).
+__device__ __forceinline__ float e4m3_value(uint32_t c) {
+  const uint32_t e = (c >> 3) & 15u, m = c & 7u;
+  const float mag = e ? __uint_as_float(((e + 120u) << 23) | (m << 20)) : (float)m * 0.001953125f;
+  return (c & 0x80u) ? -mag : mag;
+}
+
+// Two-term MXFP8 split of the 8 elements v of one lane, four consecutive
+// lanes holding a 32-element block: hi = E4M3(v / 2^X), lo =
+// E4M3((v - hi * 2^X) / 2^max(X-4, -127)) (round to nearest even); X the
+// block's shared exponent.  Every lane of the four must call it (the block
+// maximum goes through two lane shuffles).  Returns the scale byte (255 for
+// a block holding inf or NaN: then hi = 0x7F with the sign, lo = 0); hi and
+// lo get the 8 codes of the lane, element i in byte i % 4 of word i / 4.
+__device__ __forceinline__ uint32_t mx_split8(const float (&v)[8], uint32_t (&hi)[2], uint32_t (&lo)[2]) {
+  float amax = 0.f;
+  int bad = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float a = fabsf(v[i]);
+    bad |= !(a <= 3.402823466e38f);  // inf or NaN
+    amax = fmaxf(amax, a);
+  }
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  bad |= __shfl_xor(bad, 1);
+  bad |= __shfl_xor(bad, 2);
+  const int X = mx_shared_exp(amax);
+  hi[0] = hi[1] = lo[0] = lo[1] = 0;
+  if (!bad && X >= -122) {
+    // both scales 2^X and 2^(X-4) are normal floats: gfx950's scaled
+    // converters divide by the scale and round to nearest even
+    typedef short v2s __attribute__((ext_vector_type(2)));
+    typedef float v2f __attribute__((ext_vector_type(2)));
+    const float s = __uint_as_float((uint32_t)(X + 127) << 23);
+    const float sl = __uint_as_float((uint32_t)(X + 123) << 23);
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      v2s q = {0, 0};
+      q = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(q, v[4 * d], v[4 * d + 1], s, false);
+      q = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(q, v[4 * d + 2], v[4 * d + 3], s, true);
+      const uint32_t w = __builtin_bit_cast(uint32_t, q);
+      hi[d] = w;
+      const v2f b0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((int)w, s, false);
+      const v2f b1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((int)w, s, true);
+      v2s r = {0, 0};
+      r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, v[4 * d] - b0[0], v[4 * d + 1] - b0[1], sl, false);
+      r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, v[4 * d + 2] - b1[0], v[4 * d + 3] - b1[1], sl, true);
+      lo[d] = __builtin_bit_cast(uint32_t, r);
+    }
+  } else {
+    // tiny blocks (a scale below 2^-122 would be a float subnormal) and
+    // blocks holding inf or NaN: the same rounding in integer arithmetic
+    const int Xl = max(X - 4, -127);
+    const float inv = pow2_neg(X);
+    const float inv_l = pow2_neg(Xl);
+    const float sc = __uint_as_float(X > -127 ? (uint32_t)(X + 127) << 23 : 0x00400000u);  // 2^X
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t ch = e4m3_rne_sat(v[i] * inv);
+      const float res = v[i] - e4m3_value(ch) * sc;
+      const uint32_t cl = e4m3_rne_sat(res * inv_l);
+      hi[i >> 2] |= (bad ? ((__float_as_uint(v[i]) >> 24 & 0x80u) | 0x7Fu) : ch) << (8 * (i & 3));
+      lo[i >> 2] |= (bad ? 0u : cl) << (8 * (i & 3));
+    }
+  }
+  return bad ? 255u : (uint32_t)(X + 127);
+}
+
 // Activation / weight element types accepted by the kernels.
 enum DType : int { DT_BF16 = BSA_DTYPE_BF16, DT_F16 = BSA_DTYPE_F16, DT_F32 = BSA_DTYPE_F32 };
 

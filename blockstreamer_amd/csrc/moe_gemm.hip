@@ -63,8 +63,8 @@ int launch_combine(const float* Y, const int64_t* idx, const void* w, int w_dtyp
 int launch_bwd_prep(const void* dout, int dout_dtype, const float* y, const void* w, int w_dtype,
                     const int* pair_pos, int P, int k, int H, uint16_t* dy, float* grad_w,
                     hipStream_t st);
-int launch_quant_mxfp8(const void* x, int in_dtype, int64_t R, int64_t K, int64_t ldx, uint8_t* q,
-                       int64_t ldq, uint8_t* s, int64_t lds, hipStream_t st);
+int launch_quant_mxfp8_split(const void* x, int in_dtype, int64_t R, int64_t K, int64_t ldx, uint8_t* q,
+                             int64_t ldq, uint8_t* s, int64_t lds, hipStream_t st);
 
 enum Epi : int {
   EPI_SWIGLU = 0,    // out bf16 [P][N/2] = swiglu(acc + bias), optional f32 pre-activation save
@@ -72,6 +72,9 @@ enum Epi : int {
   EPI_STORE = 2,     // out (out_dtype) [P][N] = acc (+ bias if given)
   EPI_SWIGLU_BWD = 3,  // out bf16 [P][2N] = d(gate_up) from acc = d(act) and the saved
                        // f32 pre-activations in save_pre [P][2N]
+  EPI_SWIGLU_MX = 4,   // as EPI_SWIGLU, the bf16 activations then split into two MXFP8
+                       // terms: out uint8 [P][ldo] (hi/lo per 64-element k-tile, the
+                       // layout of launch_quant_mxfp8_split), out_s [P][ldos] scale bytes
 };
 
 struct GemmArgs {
@@ -98,6 +101,8 @@ struct GemmArgs {
   const uint8_t* As;     // MX path: E8M0 activation scales, row stride ldas bytes (% 4 == 0)
   int64_t ldq, ldas;
   int kp;                // Bq in the k-pair layout [E][N/16][K/64][16][2][16]
+  uint8_t* out_s;        // EPI_SWIGLU_MX: scale bytes of the split activations
+  int64_t ldos;
 };
 
 
@@ -221,31 +226,35 @@ __device__ __forceinline__ void epilogue_one(const GemmArgs& a, int64_t pos, int
 }
 
 
-// Epilogue of one wave's 128 x 32*NBW block of a tiled kernel (4 x NBW
-// blocks of 32 x 32 MFMA results: lane holds weight row n0w + 32*nb +
-// (lane & 31), block rows 8*(v/4) + 4*(lane >> 5) + v%4), staged through the
-// wave's own 4*NBW KiB of LDS so that every global store is 16 contiguous
-// bytes.
+// Epilogue of one wave's (32*MB) x (32*NBW) block of a tiled kernel (MB x
+// NBW blocks of 32 x 32 MFMA results: lane holds weight row n0w + 32*nb +
+// (lane & 31), block rows 8*(v/4) + 4*(lane >> 5) + v%4), starting at row
+// r0w of the tile, staged through the wave's own LDS (epi_lds_bytes) so that
+// every global store is 16 contiguous bytes.
 //  * EPI_SWIGLU: lanes 2j (gate) and 2j+1 (up) hold the same rows; the even
 //    lane finishes rows v < 8 and the odd lane rows v >= 8, trading halves
-//    with one shuffle; the bf16 activations of 128 rows x 32 columns go to
-//    LDS, then out to act[m0 + r][n0w/2 ..] (optional float32 pre-activation
-//    pairs are stored directly);
-//  * EPI_BIAS_F32: 32 rows x 32*NBW float32 at a time.
+//    with one shuffle; the bf16 activations of 32*MB rows x 16*NBW columns
+//    go to LDS, then out to act[m0 + r][n0w/2 ..] (optional float32
+//    pre-activation pairs are stored directly);
+//  * EPI_BIAS_F32: 32 rows x 32*CB float32 at a time (CB = min(NBW, 2)).
 // Needs 16-byte aligned output rows (ldo * element size % 16 == 0).
-template <int EPI, int NBW>
-__device__ __forceinline__ void epilogue_staged(const GemmArgs& a, const f32x16_t (&acc)[4][NBW],
-                                                const float (&bias)[NBW], int m0, int rows, int n0w,
-                                                uint8_t* wl, int lane) {
-  static_assert(EPI == EPI_SWIGLU || EPI == EPI_BIAS_F32, "staged epilogue");
+__host__ __device__ constexpr int epi_lds_bytes(int MB, int NBW) {
+  return (1024 * MB * NBW > 4096 * (NBW < 2 ? NBW : 2)) ? 1024 * MB * NBW : 4096 * (NBW < 2 ? NBW : 2);
+}
+
+template <int EPI, int MB, int NBW>
+__device__ __forceinline__ void epilogue_staged(const GemmArgs& a, const f32x16_t (&acc)[MB][NBW],
+                                                const float (&bias)[NBW], int m0, int r0w, int rows,
+                                                int n0w, uint8_t* wl, int lane) {
+  static_assert(EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_MX || EPI == EPI_BIAS_F32, "staged epilogue");
   const int l32 = lane & 31;
   const int lh = lane >> 5;
-  if constexpr (EPI == EPI_SWIGLU) {
+  if constexpr (EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_MX) {
     constexpr int AC = 16 * NBW;                   // activation columns of the wave
-    uint16_t* t = reinterpret_cast<uint16_t*>(wl);  // [128][AC] bf16
+    uint16_t* t = reinterpret_cast<uint16_t*>(wl);  // [32*MB][AC] bf16
     const bool odd = l32 & 1;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
       for (int nb = 0; nb < NBW; ++nb) {
         const int ng = n0w + nb * 32 + (l32 & ~1);
@@ -258,8 +267,8 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& a, const f32x16_
           const float u = odd ? hi : recv;
           const int vv = odd ? v + 8 : v;
           const int r = mb * 32 + 8 * (vv >> 2) + 4 * lh + (vv & 3);
-          if (a.save_pre && r < rows && ng + 1 < a.N)
-            *reinterpret_cast<float2*>(a.save_pre + (int64_t)(m0 + r) * a.N + ng) = make_float2(g, u);
+          if (a.save_pre && r0w + r < rows && ng + 1 < a.N)
+            *reinterpret_cast<float2*>(a.save_pre + (int64_t)(m0 + r0w + r) * a.N + ng) = make_float2(g, u);
           t[r * AC + nb * 16 + (l32 >> 1)] = (uint16_t)f32_to_bf16_bits(swiglu(g, u, a.alpha, a.limit));
         }
       }
@@ -269,43 +278,69 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& a, const f32x16_
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     constexpr int LPR = 2 * NBW;                   // lanes (16-byte pieces) per row
     const int half_n = a.N >> 1;
-    uint16_t* out = static_cast<uint16_t*>(a.out);
 #pragma unroll
-    for (int i = 0; i < 4 * NBW; ++i) {
+    for (int i = 0; i < MB * NBW; ++i) {
       const int r = i * (64 / LPR) + lane / LPR;
       const int ch = lane % LPR;
       const int c0 = (n0w >> 1) + ch * 8;
-      if (r < rows && c0 + 8 <= half_n)
-        *reinterpret_cast<u32x4_t*>(out + (int64_t)(m0 + r) * a.ldo + c0) =
-            *reinterpret_cast<const u32x4_t*>(wl + r * (2 * AC) + ch * 16);
+      const u32x4_t piece = *reinterpret_cast<const u32x4_t*>(wl + r * (2 * AC) + ch * 16);
+      const bool ok = r0w + r < rows && c0 + 8 <= half_n;
+      if constexpr (EPI == EPI_SWIGLU) {
+        if (ok)
+          *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(a.out) + (int64_t)(m0 + r0w + r) * a.ldo + c0) =
+              piece;
+      } else {
+        // the four lanes ch & ~3 .. ch | 3 hold one 32-element block (c0 is
+        // a multiple of 32 there: n0w / 2 is a multiple of 16 * NBW >= 32)
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[2 * j] = __uint_as_float(piece[j] << 16);
+          v[2 * j + 1] = __uint_as_float(piece[j] & 0xFFFF0000u);
+        }
+        uint32_t hq[2], lq[2];
+        const uint32_t sbyte = mx_split8(v, hq, lq);
+        if (ok) {
+          const int b = c0 >> 5;  // block of the row
+          uint8_t* q = static_cast<uint8_t*>(a.out) + (int64_t)(m0 + r0w + r) * a.ldo + (b >> 1) * 128 +
+                       (b & 1) * 32 + (ch & 3) * 8;
+          *reinterpret_cast<uint2*>(q) = make_uint2(hq[0], hq[1]);
+          *reinterpret_cast<uint2*>(q + 64) = make_uint2(lq[0], lq[1]);
+          if ((ch & 3) == 0) a.out_s[(int64_t)(m0 + r0w + r) * a.ldos + b] = (uint8_t)sbyte;
+        }
+      }
     }
   } else {
-    constexpr int WC = 32 * NBW;                   // columns of the wave
-    constexpr int LPR = 8 * NBW;                   // lanes (16-byte pieces) per row
+    constexpr int CB = NBW < 2 ? NBW : 2;          // column blocks per staging round
+    constexpr int WC = 32 * CB;                    // staged columns
+    constexpr int LPR = 8 * CB;                    // lanes (16-byte pieces) per row
     float* t = reinterpret_cast<float*>(wl);       // [32][WC] float32
     float* out = static_cast<float*>(a.out);
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-      for (int nb = 0; nb < NBW; ++nb)
+      for (int nc = 0; nc < NBW; nc += CB) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-          t[(8 * (v >> 2) + 4 * lh + (v & 3)) * WC + nb * 32 + l32] = acc[mb][nb][v] + bias[nb];
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        for (int nb = 0; nb < CB; ++nb)
 #pragma unroll
-      for (int i = 0; i < 4 * NBW; ++i) {
-        const int r = i * (64 / LPR) + lane / LPR;
-        const int ch = lane % LPR;
-        const int c0 = n0w + ch * 4;
-        if (mb * 32 + r < rows && c0 + 4 <= a.N)
-          *reinterpret_cast<u32x4_t*>(out + (int64_t)(m0 + mb * 32 + r) * a.ldo + c0) =
-              *reinterpret_cast<const u32x4_t*>(t + r * WC + ch * 4);
+          for (int v = 0; v < 16; ++v)
+            t[(8 * (v >> 2) + 4 * lh + (v & 3)) * WC + nb * 32 + l32] = acc[mb][nc + nb][v] + bias[nc + nb];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int i = 0; i < 4 * CB; ++i) {
+          const int r = i * (64 / LPR) + lane / LPR;
+          const int ch = lane % LPR;
+          const int c0 = n0w + nc * 32 + ch * 4;
+          if (r0w + mb * 32 + r < rows && c0 + 4 <= a.N)
+            *reinterpret_cast<u32x4_t*>(out + (int64_t)(m0 + r0w + mb * 32 + r) * a.ldo + c0) =
+                *reinterpret_cast<const u32x4_t*>(t + r * WC + ch * 4);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
 }
@@ -1585,13 +1620,17 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
 
   // epilogue through LDS: the stage buffers are free once every wave is done
   __syncthreads();
-  epilogue_staged<EPI, 2>(a, acc, bias, m0, rows, n0 + wave * 64, smem + wave * 8192, lane);
+  epilogue_staged<EPI, 4, 2>(a, acc, bias, m0, 0, rows, n0 + wave * 64, smem + wave * 8192, lane);
 }
 
 
 // ---------------------------------------------------------------------------
-// Native block-scaled MX kernel (prefill): MXFP8 activations x MXFP4 weights
-// on v_mfma_scale_f32_32x32x64_f8f6f4, no weight decode at all.
+// Native block-scaled MX kernel (prefill): the activations as two MXFP8
+// terms (hi + lo, launch_quant_mxfp8_split) x MXFP4 weights on
+// v_mfma_scale_f32_32x32x64_f8f6f4, two instructions per 64-element k-step,
+// no weight decode at all.  The two terms hold every bf16 activation exactly
+// unless it is below 2^-14 of its block's maximum, so the products are the
+// bf16 path's up to the accumulation order.
 //
 // Operand layout of that instruction (measured on gfx950): for 32 x 32 x 64,
 // lane l = 32*g + i supplies row/column i; its E2M1 operand is the 32
@@ -1602,48 +1641,54 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
 // its scale byte is still the scale of K block g.
 //
 // Tile 128 rows x BN weight rows, BK = 64 (two MX blocks), NS LDS stages
-// filled only by global_load_lds DMA.  The L1 -> L2 path is limited by the
-// number of requests, not bytes, so every DMA covers whole contiguous runs:
-//  * A stage [128][64] E4M3, 4 lanes per row (64 contiguous bytes); row r's
-//    16-byte chunk c sits at chunk c ^ ((r >> 2) & 3), so the fragment reads
-//    are bank-conflict free;
+// filled only by global_load_lds DMA, every DMA covering whole contiguous
+// runs:
+//  * A stage [128][128 B]: per row the k-tile's 64 hi codes then 64 lo codes
+//    (the split's row layout), 8 lanes per row; row r's 16-byte chunk c sits
+//    at chunk c ^ (r & 7), so the fragment reads are bank-conflict free;
 //  * B stage [BN rows][2 groups][16 bytes], 2 lanes per row (32 contiguous
-//    bytes), the two halves of row q swapped when bit 3 of q is set;
+//    bytes, 512 in the k-pair layout), the two halves of row q swapped when
+//    bit 3 of q is set;
 //  * scales are loaded once per tile, not per k-step: the B scales of the
 //    tile's BN weight rows are one contiguous BN*G-byte span of the
 //    checkpoint tensor; the A scales come from rows padded to ldas bytes
-//    (a multiple of 16) by the quantisation kernel.
-// WN waves (4: BN = 256, two workgroups per CU; 8: BN = 512, one workgroup
-// per CU with a deeper pipeline) split N; each wave computes 128 x 64 (4 x 2
-// blocks of 32 x 32).  Bound: MFMA (FP8 rate, 2x the bf16 rate).
+//    (a multiple of 16) by the quantisation kernel; lo's scale byte is hi's
+//    minus 4.
+// A WM x WN grid of waves (default 2 x 4: each wave 64 rows x 128 weight rows,
+// 2 x 4 blocks of 32 x 32, one workgroup per CU) splits the tile; 64 x 128
+// per wave reads 12 LDS fragments per 16 MFMAs where 128 x 64 reads 18.
+// Bound: MFMA at the FP8 rate, two instructions per step (the bf16 rate).
 // ---------------------------------------------------------------------------
 
 constexpr int MX_BM = 128;
 constexpr int MX_BK = 64;
-constexpr int MX_A_BYTES = MX_BM * MX_BK;   // 8 KiB
+constexpr int MX_A_BYTES = MX_BM * MX_BK * 2;   // 16 KiB: hi and lo codes
 
-// Per-configuration sizes: WN waves along N, each owning NBW 32-column MFMA
-// blocks (32*NBW weight rows) of the tile, BN = 32 * NBW * WN.
-template <int WN, int NBW>
+// Per-configuration sizes: WM x WN waves, wave (wm, wn) owning MB = 4/WM
+// row blocks and NB column blocks of 32 x 32 (rows 32*MB*wm .., weight rows
+// 32*NB*wn .. of the tile); BN = 32 * NB * WN weight rows per tile.
+template <int WM, int WN, int NB>
 struct MxCfg {
-  static constexpr int WCOLS = 32 * NBW;
+  static constexpr int W = WM * WN;                   // waves
+  static constexpr int MB = 4 / WM;
+  static constexpr int WCOLS = 32 * NB;
   static constexpr int BN = WCOLS * WN;
   static constexpr int B_BYTES = BN * 32;
   static constexpr int STAGE = MX_A_BYTES + B_BYTES;
-  static constexpr int A_DMA = 8 / WN;                // A instructions per wave per stage
-  static constexpr int B_DMA = NBW;                   // B instructions per wave per stage
+  static constexpr int A_DMA = 16 / W;                // A instructions per wave per stage
+  static constexpr int B_DMA = BN / 32 / W;           // B instructions per wave per stage
   static constexpr int DMA_PER_TILE = A_DMA + B_DMA;
-  static constexpr int EPI_LDS = 4096 * NBW;          // per-wave epilogue staging bytes
+  static constexpr int EPI_LDS = epi_lds_bytes(MB, NB);  // per-wave epilogue staging bytes
 };
 
 // LDS row stride of the A scales: an odd number of 16-byte chunks >= ldas.
 __host__ __device__ inline int mx_scale_ld(int ldas) { return (ldas / 16) % 2 ? ldas : ldas + 16; }
 
-// Dynamic LDS bytes of moe_mx_kernel<., ns, ., wn, nbw>: stages, A scales,
-// B scales.
-inline size_t mx_smem_bytes(int ns, int wn, int nbw, int K, int64_t ldas) {
-  const size_t bn = (size_t)32 * nbw * wn;
-  return (size_t)ns * (MX_A_BYTES + bn * 32) + (size_t)MX_BM * mx_scale_ld((int)ldas) + bn * (K / 32);
+// Dynamic LDS bytes of moe_mx_kernel with ns stages and bn weight rows per
+// tile: stages, A scales, B scales.
+inline size_t mx_smem_bytes(int ns, int bn, int K, int64_t ldas) {
+  return (size_t)ns * (MX_A_BYTES + (size_t)bn * 32) + (size_t)MX_BM * mx_scale_ld((int)ldas) +
+         (size_t)bn * (K / 32);
 }
 
 // Activation row read for sorted row r of a tile that starts at sorted row
@@ -1659,14 +1704,13 @@ __device__ __forceinline__ int64_t tile_src_row(const GemmArgs& a, int m0, int r
 // device function rather than a lambda: HIP-Clang does not emit the
 // host-side handle of these kernel templates when their bodies call a
 // capturing lambda.
-template <int WN, int NBW, int MX_NS>
+template <class C, int MX_NS>
 __device__ __forceinline__ void mx_issue(uint8_t* smem, int kt, int wave, const uint8_t* const* asrc,
                                          const uint8_t* const* bsrc, int bkt) {
-  using C = MxCfg<WN, NBW>;
   uint8_t* st = smem + (kt % MX_NS) * C::STAGE;
 #pragma unroll
   for (int j = 0; j < C::A_DMA; ++j)
-    __builtin_amdgcn_global_load_lds(asrc[j] + kt * MX_BK, (lds_void*)(st + (C::A_DMA * wave + j) * 1024),
+    __builtin_amdgcn_global_load_lds(asrc[j] + kt * 2 * MX_BK, (lds_void*)(st + (C::A_DMA * wave + j) * 1024),
                                      16, 0, 0);
 #pragma unroll
   for (int h = 0; h < C::B_DMA; ++h)
@@ -1674,13 +1718,15 @@ __device__ __forceinline__ void mx_issue(uint8_t* smem, int kt, int wave, const 
                                      (lds_void*)(st + MX_A_BYTES + (C::B_DMA * wave + h) * 1024), 16, 0, 0);
 }
 
-template <int EPI, int MX_NS, bool SB16, int WN, int NBW>
-__global__ __launch_bounds__(64 * WN, NBW == 2 ? 2 : 1) void moe_mx_kernel(GemmArgs a) {
-  using C = MxCfg<WN, NBW>;
+template <int EPI, int MX_NS, bool SB16, int WM, int WN, int NB>
+__global__ __launch_bounds__(64 * WM * WN, (WM * WN == 4 && NB == 2) ? 2 : 1) void moe_mx_kernel(GemmArgs a) {
+  using C = MxCfg<WM, WN, NB>;
+  constexpr int MB = C::MB;
+  constexpr int W = C::W;
   static_assert(MX_NS >= 2 && MX_NS <= 6, "pipeline depth");
-  static_assert(WN == 4 || WN == 8, "waves along N");
-  static_assert(NBW == 2 || NBW == 4, "MFMA blocks per wave");
-  static_assert(WN * C::EPI_LDS <= MX_NS * C::STAGE, "epilogue staging fits in the stages");
+  static_assert(WM * MB == 4 && (W == 4 || W == 8), "wave grid");
+  static_assert(C::B_DMA * W * 32 == C::BN, "B stage split over the waves");
+  static_assert(W * C::EPI_LDS <= MX_NS * C::STAGE, "epilogue staging fits in the stages");
   constexpr int BN = C::BN;
   extern __shared__ __align__(1024) uint8_t smem[];
   const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
@@ -1695,7 +1741,9 @@ __global__ __launch_bounds__(64 * WN, NBW == 2 ? 2 : 1) void moe_mx_kernel(GemmA
   const int n0 = nt * BN;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;  // weight rows WCOLS*wave .. +WCOLS of the tile
+  const int wave = tid >> 6;
+  const int wm = wave / WN;   // rows 32*MB*wm .. of the tile
+  const int wn = wave % WN;   // weight rows WCOLS*wn .. of the tile
   const int G = a.K / 32;
   const int KT = a.K / MX_BK;
   const int l32 = lane & 31;
@@ -1709,13 +1757,13 @@ __global__ __launch_bounds__(64 * WN, NBW == 2 ? 2 : 1) void moe_mx_kernel(GemmA
 
   // --- scales, once per tile ----------------------------------------------
   {
-    preload_b_scales<SB16, BN, WN>(a.Bs, e, a.N, n0, G, sbs, wave, lane);
+    preload_b_scales<SB16, BN, W>(a.Bs, e, a.N, n0, G, sbs, wave, lane);
     // A: 128 gathered rows of ldas bytes in 16-byte chunks (a padding chunk
     // reloads the row's first chunk)
     const int cpr = sld / 16;
     const int real = (int)a.ldas / 16;
     const int nch = MX_BM * cpr;
-    for (int j = wave; j * 64 < nch; j += WN) {
+    for (int j = wave; j * 64 < nch; j += W) {
       const int c = j * 64 + lane;
       if (c < nch) {
         const int r = c / cpr;
@@ -1730,12 +1778,14 @@ __global__ __launch_bounds__(64 * WN, NBW == 2 ? 2 : 1) void moe_mx_kernel(GemmA
   // --- per-lane stage DMA sources (every lane always issues all of them, so
   //     the per-wave vmcnt arithmetic is exact; rows or columns past the tile
   //     read a clamped valid address and are never stored) -----------------
-  // A: instruction i = A_DMA*wave + j covers rows 16i .. 16i+15, 4 lanes per row
+  // A: instruction i = A_DMA*wave + j covers rows 8i .. 8i+7, 8 lanes per
+  // row (the k-tile's 64 hi and 64 lo codes); row r's chunk c lands in slot
+  // c ^ (r & 7)
   const uint8_t* asrc[C::A_DMA];
 #pragma unroll
   for (int j = 0; j < C::A_DMA; ++j) {
-    const int r = 16 * (C::A_DMA * wave + j) + (lane >> 2);
-    const int ch = (lane & 3) ^ ((r >> 2) & 3);
+    const int r = 8 * (C::A_DMA * wave + j) + (lane >> 3);
+    const int ch = (lane & 7) ^ (r & 7);
     asrc[j] = a.Aq + tile_src_row(a, m0, rows, r) * a.ldq + ch * 16;
   }
   // B: instruction i = B_DMA*wave + h covers rows 32i .. 32i+31, 2 lanes per
@@ -1751,68 +1801,82 @@ __global__ __launch_bounds__(64 * WN, NBW == 2 ? 2 : 1) void moe_mx_kernel(GemmA
   const int bkt = a.kp ? 512 : 32;  // bytes per k-tile (two groups) along a row
 
   // this lane's B rows (one per 32-column block) and their bias
-  int bq[NBW];
-  float bias[NBW];
+  int bq[NB];
+  float bias[NB];
 #pragma unroll
-  for (int nb = 0; nb < NBW; ++nb) {
-    bq[nb] = wave * C::WCOLS + nb * 32 + l32;
+  for (int nb = 0; nb < NB; ++nb) {
+    bq[nb] = wn * C::WCOLS + nb * 32 + l32;
     const bool ok = n0 + bq[nb] < a.N;
     bias[nb] = ok ? bias_at(a.bias, a.bias_dtype, (int64_t)e * a.N + n0 + bq[nb]) : 0.f;
   }
-  // LDS byte offsets of this lane's A chunks lh and 2 + lh in row mb*32 + l32
-  // (the row's swizzle (r >> 2) & 3 does not depend on mb)
-  const int rsw = (l32 >> 2) & 3;
-  const uint32_t aoff0 = (uint32_t)(l32 * 64 + ((lh ^ rsw) * 16));
-  const uint32_t aoff1 = (uint32_t)(l32 * 64 + (((2 + lh) ^ rsw) * 16));
+  // LDS byte offsets of this lane's A chunks in row 32*(MB*wm + mb) + l32:
+  // hi codes in chunks lh and 2 + lh, lo codes in 4 + lh and 6 + lh (the
+  // row's swizzle r & 7 does not depend on the row block)
+  const int rsw = l32 & 7;
+  const uint32_t abase = (uint32_t)(MB * wm * 32 * 128 + l32 * 128);
+  const uint32_t aoff0 = abase + (uint32_t)((lh ^ rsw) * 16);
+  const uint32_t aoff1 = abase + (uint32_t)(((2 + lh) ^ rsw) * 16);
+  const uint32_t aoff2 = abase + (uint32_t)(((4 + lh) ^ rsw) * 16);
+  const uint32_t aoff3 = abase + (uint32_t)(((6 + lh) ^ rsw) * 16);
   // B: half lh ^ bsw of row bq (bsw = bit 3 of the row, the same for every nb)
   const uint32_t boff = (uint32_t)(bq[0] * 32 + ((lh ^ ((bq[0] >> 3) & 1)) * 16));
-  const uint8_t* sa_row = sas + l32 * sld + lh;          // + mb*32*sld + 2kt
-  const uint8_t* sb_row = sbs + bq[0] * G + lh;          // + nb*32*G + 2kt
+  const uint8_t* sa_row = sas + (MB * wm * 32 + l32) * sld + lh;  // + mb*32*sld + 2kt
+  const uint8_t* sb_row = sbs + bq[0] * G + lh;                   // + nb*32*G + 2kt
+  const int mbw = mbn - MB * wm;  // this wave's row blocks holding rows
 
-  f32x16_t acc[4][NBW];
+  f32x16_t acc[MB][NB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
-    for (int j = 0; j < NBW; ++j)
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
   for (int i = 0; i < MX_NS - 1; ++i)
-    if (i < KT) mx_issue<WN, NBW, MX_NS>(smem, i, wave, asrc, bsrc, bkt);
+    if (i < KT) mx_issue<C, MX_NS>(smem, i, wave, asrc, bsrc, bkt);
   for (int kt = 0; kt < KT; ++kt) {
     // tile kt (and, on the first pass, the scales issued before it) has
     // landed once at most the tiles issued after it are in flight
     wait_tiles_ahead<C::DMA_PER_TILE, MX_NS - 2>(min(MX_NS - 2, KT - 1 - kt));
     asm volatile("s_barrier" ::: "memory");
-    if (kt + MX_NS - 1 < KT) mx_issue<WN, NBW, MX_NS>(smem, kt + MX_NS - 1, wave, asrc, bsrc, bkt);
+    if (kt + MX_NS - 1 < KT) mx_issue<C, MX_NS>(smem, kt + MX_NS - 1, wave, asrc, bsrc, bkt);
     const uint8_t* st = smem + (kt % MX_NS) * C::STAGE;
-    int sb[NBW];
-    i32x8_t bop[NBW];
+    int sb[NB];
+    i32x8_t bop[NB];
 #pragma unroll
-    for (int nb = 0; nb < NBW; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
       sb[nb] = (int)sb_row[nb * 32 * G + 2 * kt];
       const u32x4_t w = *reinterpret_cast<const u32x4_t*>(st + MX_A_BYTES + boff + nb * 1024);
       bop[nb] = i32x8_t{(int)w[0], (int)w[1], (int)w[2], (int)w[3], 0, 0, 0, 0};
     }
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      if (mb >= mbn) continue;  // row block past the tile's valid rows
-      const uint8_t* ar = st + mb * 32 * 64;
+    for (int mb = 0; mb < MB; ++mb) {
+      if (mb >= mbw) continue;  // row block past the tile's valid rows
+      const uint8_t* ar = st + mb * 32 * 128;
       const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(ar + aoff0);
       const u32x4_t w1 = *reinterpret_cast<const u32x4_t*>(ar + aoff1);
-      const i32x8_t aop = {(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3],
+      const u32x4_t w2 = *reinterpret_cast<const u32x4_t*>(ar + aoff2);
+      const u32x4_t w3 = *reinterpret_cast<const u32x4_t*>(ar + aoff3);
+      const i32x8_t ahi = {(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3],
                            (int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
+      const i32x8_t alo = {(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3],
+                           (int)w3[0], (int)w3[1], (int)w3[2], (int)w3[3]};
       const int sa = (int)sa_row[mb * 32 * sld + 2 * kt];
+      const int sl = sa > 4 ? sa - 4 : 0;  // lo's scale 2^max(X-4, -127)
 #pragma unroll
-      for (int nb = 0; nb < NBW; ++nb)
-        acc[mb][nb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, bop[nb], acc[mb][nb], 0, 4, 0,
+      for (int nb = 0; nb < NB; ++nb) {
+        acc[mb][nb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ahi, bop[nb], acc[mb][nb], 0, 4, 0,
                                                                       sa, 0, sb[nb]);
+        acc[mb][nb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(alo, bop[nb], acc[mb][nb], 0, 4, 0,
+                                                                      sl, 0, sb[nb]);
+      }
     }
   }
 
   // epilogue through LDS: the stage buffers are free once every wave is done
   __syncthreads();
-  epilogue_staged<EPI, NBW>(a, acc, bias, m0, rows, n0 + wave * C::WCOLS, smem + wave * C::EPI_LDS, lane);
+  epilogue_staged<EPI, MB, NB>(a, acc, bias, m0, MB * wm * 32, rows, n0 + wn * C::WCOLS,
+                               smem + wave * C::EPI_LDS, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1831,9 +1895,9 @@ struct Workspace {
   int* num_tiles;
   uint16_t* act;  // [P][I] bf16 gated activations
   float* y;       // [P][H] f32 down-projection output (before the routing weight)
-  uint8_t* hq;    // MX path: [T][H] E4M3 hidden, [T][ldhs] scales
+  uint8_t* hq;    // MX path: [T][2H] hi/lo E4M3 hidden (in y's bytes), [T][ldhs] scales
   uint8_t* hs;
-  uint8_t* aq;    // MX path: [P][I] E4M3 activations, [P][ldas] scales
+  uint8_t* aq;    // MX path: [P][2I] hi/lo E4M3 activations (in act's bytes), [P][ldas] scales
   uint8_t* as;
   int64_t ldhs, ldas;
   int64_t bytes;
@@ -1860,9 +1924,12 @@ static Workspace carve(void* base, int64_t T, int64_t H, int64_t I, int64_t E, i
   w.y = reinterpret_cast<float*>(take(P * H * 4));
   w.ldhs = align_up(H / 32, 16);
   w.ldas = align_up(I / 32, 16);
-  w.hq = reinterpret_cast<uint8_t*>(take(T * H));
+  // MX path: the split hidden rows (T * 2H bytes) are dead once gate_up is
+  // done, before down writes y (P * 4H bytes) over them; the split
+  // activations (P * 2I bytes) take the place of the bf16 ones
+  w.hq = reinterpret_cast<uint8_t*>(w.y);
   w.hs = reinterpret_cast<uint8_t*>(take(T * w.ldhs));
-  w.aq = reinterpret_cast<uint8_t*>(take(P * I));
+  w.aq = reinterpret_cast<uint8_t*>(w.act);
   w.as = reinterpret_cast<uint8_t*>(take(P * w.ldas));
   w.bytes = off;
   return w;
@@ -2264,7 +2331,7 @@ static int allow_big_lds(const void* fn, int kind, int epi, int bytes = 160 * 10
   }
   // kinds: 1-3 packed-weight backward kernel, 4-5 tiled kernel, 6 persistent
   // decode kernel, 8-15 MX kernel configurations
-  static bool allowed[64][16][4];
+  static bool allowed[64][16][8];
   if (!allowed[dev][kind][epi]) {
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
       set_error("cannot allow %d bytes of dynamic LDS for a GEMM kernel", bytes);
@@ -2275,37 +2342,49 @@ static int allow_big_lds(const void* fn, int kind, int epi, int bytes = 160 * 10
   return BSA_OK;
 }
 
-template <int EPI, int NS, int WN, int NBW>
+template <int EPI, int NS, int WM, int WN, int NB>
 static int launch_mx_cfg(const GemmArgs& a, int64_t P, size_t smem, hipStream_t st) {
+  using C = MxCfg<WM, WN, NB>;
   const int64_t max_tiles = (P + MX_BM - 1) / MX_BM + a.E;
   GemmArgs b = a;
-  b.n_tiles_n = (a.N + MxCfg<WN, NBW>::BN - 1) / MxCfg<WN, NBW>::BN;
+  b.n_tiles_n = (a.N + C::BN - 1) / C::BN;
   const int64_t grid = align_up(max_tiles * b.n_tiles_n, 8);
   if (grid > INT32_MAX) {
     set_error("MX GEMM: grid too large");
     return BSA_EINVAL;
   }
   const bool sb16 = reinterpret_cast<uintptr_t>(a.Bs) % 16 == 0;
-  const void* fn = sb16 ? reinterpret_cast<const void*>(moe_mx_kernel<EPI, NS, true, WN, NBW>)
-                        : reinterpret_cast<const void*>(moe_mx_kernel<EPI, NS, false, WN, NBW>);
-  int rc = allow_big_lds(fn, 8 + (WN == 8 ? 4 : 0) + (NBW == 4 ? 2 : 0) + (sb16 ? 1 : 0), EPI);
+  const void* fn = sb16 ? reinterpret_cast<const void*>(moe_mx_kernel<EPI, NS, true, WM, WN, NB>)
+                        : reinterpret_cast<const void*>(moe_mx_kernel<EPI, NS, false, WM, WN, NB>);
+  int rc = allow_big_lds(fn, 8 + (sb16 ? 1 : 0), EPI);
   if (rc) return rc;
   if (sb16)
-    hipLaunchKernelGGL((moe_mx_kernel<EPI, NS, true, WN, NBW>), dim3((unsigned)grid), dim3(64 * WN), smem,
+    hipLaunchKernelGGL((moe_mx_kernel<EPI, NS, true, WM, WN, NB>), dim3((unsigned)grid), dim3(64 * C::W), smem,
                        st, b);
   else
-    hipLaunchKernelGGL((moe_mx_kernel<EPI, NS, false, WN, NBW>), dim3((unsigned)grid), dim3(64 * WN), smem,
-                       st, b);
+    hipLaunchKernelGGL((moe_mx_kernel<EPI, NS, false, WM, WN, NB>), dim3((unsigned)grid), dim3(64 * C::W),
+                       smem, st, b);
   BSA_LAUNCH_CHECK("MX grouped GEMM launch");
   return BSA_OK;
 }
 
 // Block-scaled MX grouped GEMM (K % 64 == 0; 16-byte aligned blocks, 4-byte
-// aligned weight scales; a.Aq / a.As filled by launch_quant_mxfp8 with a
-// 16-byte aligned scale buffer whose row stride is a multiple of 16).  Four
-// waves of 128 x 64, two workgroups per CU, 2 stages (measured faster on
-// gfx950 than 4 waves of 128 x 128 with 4 stages at one workgroup per CU,
-// 1.05 vs 1.13 ms for the 8192-token gpt-oss-120b gate_up).
+// aligned weight scales; a.Aq / a.As filled by launch_quant_mxfp8_split
+// with a 16-byte aligned scale buffer whose row stride is a multiple of 16).
+// Pipeline depth BSA_MX_NS, a BSA_MX_WM x BSA_MX_WN wave grid with
+// BSA_MX_NB 32-column blocks per wave (a build-time choice).
+#ifndef BSA_MX_NS
+#define BSA_MX_NS 2
+#endif
+#ifndef BSA_MX_WM
+#define BSA_MX_WM 2
+#endif
+#ifndef BSA_MX_WN
+#define BSA_MX_WN 4
+#endif
+#ifndef BSA_MX_NB
+#define BSA_MX_NB 4
+#endif
 template <int EPI>
 static int launch_gemm_mx(const GemmArgs& a, int64_t P, hipStream_t st) {
   if (a.K % MX_BK != 0 || reinterpret_cast<uintptr_t>(a.Bq) % 16 != 0 ||
@@ -2315,12 +2394,13 @@ static int launch_gemm_mx(const GemmArgs& a, int64_t P, hipStream_t st) {
               a.K);
     return BSA_EINVAL;
   }
-  const size_t small = mx_smem_bytes(2, 4, 2, a.K, a.ldas);
-  if (small > 160 * 1024) {
-    set_error("MX GEMM: K=%d needs %zu bytes of LDS", a.K, small);
+  using C = MxCfg<BSA_MX_WM, BSA_MX_WN, BSA_MX_NB>;
+  const size_t smem = mx_smem_bytes(BSA_MX_NS, C::BN, a.K, a.ldas);
+  if (smem > 160 * 1024) {
+    set_error("MX GEMM: K=%d needs %zu bytes of LDS", a.K, smem);
     return BSA_EINVAL;
   }
-  return launch_mx_cfg<EPI, 2, 4, 2>(a, P, small, st);
+  return launch_mx_cfg<EPI, BSA_MX_NS, BSA_MX_WM, BSA_MX_WN, BSA_MX_NB>(a, P, smem, st);
 }
 
 // Compute units of the current device (cached per device).
@@ -2512,14 +2592,24 @@ static int stage_gate_up(const MoeShape& m, const void* hidden, const void* bloc
   const int64_t P = m.T * m.k;
   const int chosen = pick_path(path, P, m.E, m.H);
   if (chosen == PATH_MX) {
-    // each token's hidden row is quantised once, then gathered per pair
-    int rc = launch_quant_mxfp8(hidden, DT_BF16, m.T, m.H, m.H, w.hq, m.H, w.hs, w.ldhs, st);
+    // each token's hidden row is split once, then gathered per pair
+    if (m.H % MX_BK != 0 || m.I % MX_BK != 0) {
+      set_error("gate_up (MX path): hidden %lld and intermediate %lld must be multiples of 64",
+                (long long)m.H, (long long)m.I);
+      return BSA_EINVAL;
+    }
+    int rc = launch_quant_mxfp8_split(hidden, DT_BF16, m.T, m.H, m.H, w.hq, 2 * m.H, w.hs, w.ldhs, st);
     if (rc) return rc;
     g.Aq = w.hq;
-    g.ldq = m.H;
+    g.ldq = 2 * m.H;
     g.As = w.hs;
     g.ldas = w.ldhs;
-    return launch_gemm_mx<EPI_SWIGLU>(g, P, st);
+    // the epilogue splits the activations for the down GEMM itself
+    g.out = w.aq;
+    g.ldo = 2 * m.I;
+    g.out_s = w.as;
+    g.ldos = w.ldas;
+    return launch_gemm_mx<EPI_SWIGLU_MX>(g, P, st);
   }
   return launch_gemm<EPI_SWIGLU>(g, chosen, P, st);
 }
@@ -2554,10 +2644,8 @@ static int stage_down(const MoeShape& m, const void* blocks, const void* scales,
       set_error("down (MX path): intermediate %lld is not a multiple of 64", (long long)m.I);
       return BSA_EINVAL;
     }
-    int rc = launch_quant_mxfp8(w.act, DT_BF16, P, m.I, m.I, w.aq, m.I, w.as, w.ldas, st);
-    if (rc) return rc;
-    g.Aq = w.aq;
-    g.ldq = m.I;
+    g.Aq = w.aq;  // written by the gate_up epilogue
+    g.ldq = 2 * m.I;
     g.As = w.as;
     g.ldas = w.ldas;
     return launch_gemm_mx<EPI_BIAS_F32>(g, P, st);

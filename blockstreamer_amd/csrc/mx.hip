@@ -24,30 +24,6 @@
 
 namespace bsa {
 
-// E4M3 code of v (RNE, saturating); |v| < 2^9 by construction of the scale.
-__device__ __forceinline__ uint32_t e4m3_rne_sat(float v) {
-  const uint32_t sign = (__float_as_uint(v) >> 24) & 0x80u;
-  const float a = fabsf(v);
-  uint32_t c;
-  if (a >= 448.f) {
-    c = 0x7Eu;
-  } else if (a < 0.015625f) {  // below 2^-6: subnormal steps of 2^-9
-    c = (uint32_t)rintf(a * 512.f);
-  } else {
-    // round the float32 mantissa to 3 bits (ties to even), carrying into the
-    // exponent; then rebias the exponent from 127 to 7
-    const uint32_t b = __float_as_uint(a);
-    c = ((b + 0x7FFFFu + ((b >> 20) & 1u)) >> 20) - (120u << 3);
-    c = c > 0x7Eu ? 0x7Eu : c;
-  }
-  return sign | c;
-}
-
-// 2^-X as a float for X in [-127, 127] (2^-127 is a float32 subnormal).
-__device__ __forceinline__ float pow2_neg(int X) {
-  return X == 127 ? __uint_as_float(0x00400000u) : __uint_as_float((uint32_t)(127 - X) << 23);
-}
-
 // Four lanes per 32-element block, eight elements per lane.
 template <int IN>
 __global__ __launch_bounds__(256) void mx_quant_kernel(const void* __restrict__ x, int64_t ldx,
@@ -90,14 +66,7 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(const void* __restrict__ 
   amax = fmaxf(amax, __shfl_xor(amax, 2));
   bad |= __shfl_xor(bad, 1);
   bad |= __shfl_xor(bad, 2);
-  int X = -127;
-  if (amax > 0.f) {
-    const uint32_t ab = __float_as_uint(amax);
-    const int e = (ab >> 23) ? (int)(ab >> 23) - 127 : (31 - (int)__clz(ab & 0x7FFFFFu)) - 149;
-    // significand above 1.75 needs the next exponent (a float32 subnormal
-    // amax clamps to -127 either way)
-    X = min(max(e - 8 + ((ab & 0x7FFFFFu) > 0x600000u ? 1 : 0), -127), 127);
-  }
+  const int X = mx_shared_exp(amax);
   const float inv = pow2_neg(X);
   uint32_t lo = 0, hi = 0;
 #pragma unroll
@@ -112,6 +81,59 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(const void* __restrict__ 
   if (ok) {
     *reinterpret_cast<uint2*>(q + r * ldq + g * 32 + part * 8) = make_uint2(lo, hi);
     if (part == 0) s[r * lds + g] = (uint8_t)(bad ? 255 : X + 127);
+  }
+}
+
+// Two-term MXFP8 split (the A operand of the MX prefill kernel).  Each
+// 32-element block x gets the MXFP8 scale X of mx_quant_kernel and
+//   hi = E4M3(x / 2^X)                      (the codes mx_quant_kernel writes)
+//   lo = E4M3((x - hi * 2^X) / 2^Xl),       Xl = max(X - 4, -127),
+// both round to nearest even.  x / 2^X is at most 448, where E4M3 steps are
+// at most 32, so the residual is at most 16 * 2^X and lo at most 256.  A
+// bfloat16 element keeps 8 significant bits, its residual at most 4, so
+// hi * 2^X + lo * 2^Xl equals x exactly for every element above about 2^-14
+// of the block maximum (E4M3 keeps 4 bits down to 2^-6).  The residual is
+// exact in float32 (x minus x rounded to 4 bits).
+// Output row layout, per 64-element k-tile t: bytes 128t .. 128t+63 the hi
+// codes of k = 64t .. 64t+63, then 64 bytes of lo codes; the scale bytes are
+// those of X (lo's is derived: max(byte - 4, 0)).  Blocks with an inf or NaN
+// get scale byte 255, hi codes 0x7F (NaN, sign kept) and lo codes 0.
+template <int IN>
+__global__ __launch_bounds__(256) void mx_split_kernel(const void* __restrict__ x, int64_t ldx,
+                                                       int64_t nblk, int G, uint8_t* __restrict__ q,
+                                                       int64_t ldq, uint8_t* __restrict__ s,
+                                                       int64_t lds) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const bool ok = (gid >> 2) < nblk;
+  const int64_t blk = ok ? (gid >> 2) : nblk - 1;
+  const int part = threadIdx.x & 3;
+  const int64_t r = blk / G;
+  const int g = (int)(blk - r * G);
+  const int64_t off = r * ldx + g * 32 + part * 8;
+  float v[8];
+  if constexpr (IN == DT_BF16) {
+    const u32x4_t w = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  } else if constexpr (IN == DT_F32) {
+    const float* p = static_cast<const float*>(x) + off;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = p[i];
+  } else {
+    const uint16_t* p = static_cast<const uint16_t*>(x) + off;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (float)__builtin_bit_cast(_Float16, p[i]);
+  }
+  uint32_t h[2], l[2];
+  const uint32_t sbyte = mx_split8(v, h, l);
+  if (ok) {
+    uint8_t* row = q + r * ldq + (g >> 1) * 128 + (g & 1) * 32 + part * 8;
+    *reinterpret_cast<uint2*>(row) = make_uint2(h[0], h[1]);
+    *reinterpret_cast<uint2*>(row + 64) = make_uint2(l[0], l[1]);
+    if (part == 0) s[r * lds + g] = (uint8_t)sbyte;
   }
 }
 
@@ -140,9 +162,49 @@ int launch_quant_mxfp8(const void* x, int in_dtype, int64_t R, int64_t K, int64_
   return BSA_OK;
 }
 
+// Two-term split of R rows of K (K % 64 == 0) elements into q [R][ldq]
+// (ldq >= 2K: hi and lo codes interleaved per 64-element k-tile) and scale
+// bytes s [R][lds].
+int launch_quant_mxfp8_split(const void* x, int in_dtype, int64_t R, int64_t K, int64_t ldx, uint8_t* q,
+                             int64_t ldq, uint8_t* s, int64_t lds, hipStream_t st) {
+  if (R == 0) return BSA_OK;
+  const int G = (int)(K / 32);
+  const int64_t nblk = R * G;
+  const int64_t grid = (nblk * 4 + 255) / 256;
+  if (grid > INT32_MAX) {
+    set_error("mxfp8 split: too many blocks");
+    return BSA_EINVAL;
+  }
+  if (in_dtype == DT_BF16)
+    hipLaunchKernelGGL(mx_split_kernel<DT_BF16>, dim3((unsigned)grid), dim3(256), 0, st, x, ldx, nblk, G, q,
+                       ldq, s, lds);
+  else if (in_dtype == DT_F32)
+    hipLaunchKernelGGL(mx_split_kernel<DT_F32>, dim3((unsigned)grid), dim3(256), 0, st, x, ldx, nblk, G, q,
+                       ldq, s, lds);
+  else
+    hipLaunchKernelGGL(mx_split_kernel<DT_F16>, dim3((unsigned)grid), dim3(256), 0, st, x, ldx, nblk, G, q,
+                       ldq, s, lds);
+  BSA_LAUNCH_CHECK("mxfp8 split launch");
+  return BSA_OK;
+}
+
 }  // namespace bsa
 
 using namespace bsa;
+
+extern "C" int bsa_quant_mxfp8_split(const void* x, int dtype, int64_t R, int64_t K, void* q, void* scales,
+                                     int64_t scale_ld, void* stream) {
+  clear_error();
+  BSA_REQUIRE(R >= 0 && K > 0 && K % 64 == 0, "mxfp8 split: needs K %% 64 == 0 (K=%lld)", (long long)K);
+  BSA_REQUIRE(scale_ld >= K / 32, "mxfp8 split: scale row stride %lld < K/32", (long long)scale_ld);
+  BSA_REQUIRE(dtype == DT_BF16 || dtype == DT_F16 || dtype == DT_F32, "mxfp8 split: bad dtype %d", dtype);
+  if (R == 0) return BSA_OK;
+  BSA_REQUIRE(x && q && scales, "mxfp8 split: null pointer");
+  BSA_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(q) % 8 == 0,
+              "mxfp8 split: x must be 16-byte and q 8-byte aligned");
+  return launch_quant_mxfp8_split(x, dtype, R, K, K, static_cast<uint8_t*>(q), 2 * K,
+                                  static_cast<uint8_t*>(scales), scale_ld, static_cast<hipStream_t>(stream));
+}
 
 extern "C" int bsa_quant_mxfp8(const void* x, int dtype, int64_t R, int64_t K, void* q, void* scales,
                                int64_t scale_ld, void* stream) {

@@ -105,9 +105,10 @@ def dequantize_mxfp4(blocks: Tensor, scales: Tensor, dtype: torch.dtype = torch.
 
 # Expert GEMM kernels: "stream" (weight streaming, decode), "tiled" (bf16
 # MFMA over LDS tiles, prefill), "auto" (by rows per expert) -- all bf16
-# activations x exactly dequantised MXFP4 weights; "mx" (MXFP8 activations x
-# MXFP4 weights on the block-scaled f8f6f4 MFMA; activation quantisation
-# error of a few 1e-2 relative, opt-in only).
+# activations x exactly dequantised MXFP4 weights; "mx" (the activations as
+# two MXFP8 terms x the packed MXFP4 weights on the block-scaled f8f6f4 MFMA,
+# prefill: the bf16 activations exactly, elements below 2^-14 of their
+# 32-element block's maximum aside).
 PATHS = {"auto": 0, "stream": 1, "tiled": 2, "mx": 3}
 
 
@@ -129,6 +130,30 @@ def quantize_mxfp8(x: Tensor) -> tuple[Tensor, Tensor]:
         _lib.call("bsa_quant_mxfp8", x.data_ptr(), code, R, K, q.data_ptr(), s.data_ptr(), K // 32,
                   _lib.stream_handle(dev))
     return q, s
+
+
+def quantize_mxfp8_split(x: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """Two-term MXFP8 split of a ``[R, K]`` tensor (K % 64 == 0): the
+    activation format of the ``"mx"`` GEMM path; no reference counterpart.
+
+    Returns ``(hi uint8 [R, K], lo uint8 [R, K], scales uint8 [R, K/32])``:
+    x ~ hi * 2^X + lo * 2^max(X - 4, -127) per 32-element block, X = scale - 127.
+    The kernel interleaves hi and lo per 64-element k-tile; they are returned
+    here as two views of that buffer.
+    """
+    if x.dim() != 2 or x.shape[1] % 64 != 0:
+        raise ValueError(f"x must be [rows, K] with K % 64 == 0, got {tuple(x.shape)}")
+    dev = _lib.require_gpu(x)
+    code = _lib.dtype_code(x.dtype)
+    x = x.contiguous()
+    R, K = x.shape
+    q = torch.empty((R, 2 * K), dtype=torch.uint8, device=dev)
+    s = torch.empty((R, K // 32), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("bsa_quant_mxfp8_split", x.data_ptr(), code, R, K, q.data_ptr(), s.data_ptr(), K // 32,
+                  _lib.stream_handle(dev))
+    tiles = q.view(R, K // 64, 2, 64)
+    return tiles[:, :, 0].reshape(R, K), tiles[:, :, 1].reshape(R, K), s
 
 
 def moe_workspace_bytes(T: int, H: int, I: int, E: int, k: int) -> int:
@@ -201,7 +226,7 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
     packed experts in the checkpoint layout.  Returns ``out [T, H]`` in the
     dtype of ``hidden``; with ``save=True`` also ``(workspace, gate_up_pre)``
     for the input-gradient backward.  Activations enter the MFMA as bfloat16,
-    except on ``path="mx"`` (MXFP8, see ``PATHS``).
+    except on ``path="mx"`` (two MXFP8 terms, see ``PATHS``).
 
     ``noalloc=True`` runs the same kernels through
     ``bsa_moe_experts_fwd_noalloc``, whose workspace is the library's static

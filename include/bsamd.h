@@ -151,13 +151,15 @@ int bsa_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
  *   save_gate_up    optional float32 [T*k, 2I]: gate_up pre-activations in
  *                   expert-sorted row order, for the backward
  *   path            0 = automatic, 1 = weight-streaming kernel, 2 = tiled kernel,
- *                   3 = native block-scaled MX kernel (activations quantised
- *                   to MXFP8 by bsa_quant_mxfp8's rule, then
- *                   v_mfma_scale_f32_32x32x64_f8f6f4 on the packed MXFP4
- *                   weights; needs H and I multiples of 64, 16-byte aligned
- *                   blocks, 4-byte aligned scales; not bit-compatible with
- *                   paths 0-2: the activation quantisation adds a relative
- *                   error of a few 1e-2)
+ *                   3 = native block-scaled MX kernel (activations split into
+ *                   two MXFP8 terms by bsa_quant_mxfp8_split's rule, then two
+ *                   v_mfma_scale_f32_32x32x64_f8f6f4 per 64-element k-step on
+ *                   the packed MXFP4 weights as they are; needs H and I
+ *                   multiples of 64, 16-byte aligned blocks, 4-byte aligned
+ *                   scales; not bit-compatible with paths 0-2, whose products
+ *                   it equals up to the matrix cores' accumulation order: the
+ *                   two terms hold every bf16 activation exactly unless it is
+ *                   below 2^-14 of its 32-element block's maximum)
  *   blocks_layout   layout of gate_up_blocks and down_blocks:
  *                   BSA_LAYOUT_CHECKPOINT or BSA_LAYOUT_KPAIR (the results
  *                   are the same bit for bit)
@@ -187,7 +189,7 @@ int bsa_moe_experts_fwd(
  * harnesses that forbid allocation.
  *
  * Limit: the shape's bsa_moe_workspace_bytes must be at most
- * BSA_NOALLOC_SCRATCH_BYTES (16 MiB: about 190 tokens at top-4 with
+ * BSA_NOALLOC_SCRATCH_BYTES (16 MiB: up to 240 tokens at top-4 with
  * H = I = 2880, i.e. decode batches); larger shapes return BSA_EINVAL.
  * Every call on one GPU shares that GPU's array, so calls that overlap on a
  * GPU (concurrent streams, threads) race; order them.  The array's contents
@@ -277,6 +279,28 @@ int bsa_router_topk(const void *logits, int dtype, int64_t T, int64_t E,
  */
 int bsa_quant_mxfp8(const void *x, int dtype, int64_t R, int64_t K, void *q,
                     void *scales, int64_t scale_ld, void *stream);
+
+/*
+ * Two-term MXFP8 split: the activation format of path 3 above.  No
+ * reference counterpart (the reference multiplies unquantised activations,
+ * block_streamer/gptoss.py:45-75; two terms reproduce a bfloat16 element
+ * exactly unless it is below about 2^-14 of its block's maximum).
+ *
+ *   x       dtype [R, K] (K % 64 == 0, 16-byte aligned)
+ *   q       uint8 [R, 2K]: per 64-element k-tile t, bytes 128t .. 128t+63
+ *           hold the hi codes of elements 64t .. 64t+63 and the next 64
+ *           bytes their lo codes
+ *   scales  uint8 [R, scale_ld] (scale_ld >= K/32): hi's scale bytes, as
+ *           bsa_quant_mxfp8 writes them
+ *
+ * hi = the codes bsa_quant_mxfp8 writes (X, its scale); lo = E4M3 of the
+ * residual x - hi * 2^X divided by 2^Xl, Xl = max(X - 4, -127), rounded to
+ * nearest even (lo's scale byte is max(byte - 4, 0)).  Blocks holding inf or
+ * NaN: scale byte 255, hi codes 0x7F with the element's sign, lo codes 0.
+ */
+int bsa_quant_mxfp8_split(const void *x, int dtype, int64_t R, int64_t K,
+                          void *q, void *scales, int64_t scale_ld,
+                          void *stream);
 
 /*
  * Bytes of the extra workspace bsa_moe_experts_bwd needs (the per-row

@@ -20,6 +20,8 @@ from .oracle import (  # noqa: F401
     mlp_ref,
     mxfp8_dequant_ref,
     mxfp8_quant_ref,
+    mxfp8_split_dequant_ref,
+    mxfp8_split_ref,
     rmsnorm_bwd_ref,
     rmsnorm_ref,
     router_ref,

@@ -302,18 +302,19 @@ def e4m3_decode(codes: np.ndarray) -> np.ndarray:
     return sign * mag
 
 
-def mxfp8_quant_ref(x: torch.Tensor) -> tuple[np.ndarray, np.ndarray]:
-    """[R, K] floats -> (E4M3 codes uint8 [R, K], E8M0 scale bytes uint8 [R, K/32])."""
-    a = x.detach().double().cpu().numpy()
-    R, K = a.shape
-    blk = a.reshape(R, K // 32, 32)
+def _mx_shared_exp(blk: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Blocks ``[..., 32]`` (float64) -> (X int64 [...], bad bool [...])."""
     amax = np.abs(blk).max(-1)
     bad = ~np.isfinite(blk).all(-1)
     f, e = np.frexp(np.where(np.isfinite(amax), amax, 1.0))   # amax = f * 2^e, f in [0.5, 1)
     X = np.clip(e - 1 - 8 + (2 * f > 1.75), -127, 127)
     X = np.where(amax == 0, -127, X)
-    scales = np.where(bad, 255, X + 127).astype(np.uint8)
-    y = blk / np.exp2(X.astype(np.float64))[..., None]
+    return X.astype(np.int64), bad
+
+
+def _e4m3_codes(y: np.ndarray) -> np.ndarray:
+    """E4M3 codes (int64) of float64 values, round to nearest even,
+    saturating at 448; the sign bit follows the sign of y (-0 included)."""
     mag = np.minimum(np.abs(y), E4M3_MAX)
     _, ee = np.frexp(mag)
     ee = np.maximum(ee - 1, -6)                       # subnormals: fixed step 2^-9
@@ -325,9 +326,52 @@ def mxfp8_quant_ref(x: torch.Tensor) -> tuple[np.ndarray, np.ndarray]:
     mant = np.where(normal, q / np.exp2(e2.astype(np.float64)) * 8 - 8, q / 2.0 ** -9)
     code = np.where(normal, ((e2 + 7) << 3) + np.rint(mant).astype(np.int64),
                     np.rint(mant).astype(np.int64))
-    code = code | (np.signbit(y).astype(np.int64) << 7)
+    return code | (np.signbit(y).astype(np.int64) << 7)
+
+
+def mxfp8_quant_ref(x: torch.Tensor) -> tuple[np.ndarray, np.ndarray]:
+    """[R, K] floats -> (E4M3 codes uint8 [R, K], E8M0 scale bytes uint8 [R, K/32])."""
+    a = x.detach().double().cpu().numpy()
+    R, K = a.shape
+    blk = a.reshape(R, K // 32, 32)
+    X, bad = _mx_shared_exp(blk)
+    scales = np.where(bad, 255, X + 127).astype(np.uint8)
+    y = blk / np.exp2(X.astype(np.float64))[..., None]
+    code = _e4m3_codes(y)
     code = np.where(bad[..., None], (np.signbit(blk).astype(np.int64) << 7) | 0x7F, code)
     return code.reshape(R, K).astype(np.uint8), scales
+
+
+def mxfp8_split_ref(x: torch.Tensor) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Two-term MXFP8 split of [R, K] floats (the MX GEMM path's activations):
+    (hi codes uint8 [R, K], lo codes uint8 [R, K], scale bytes uint8 [R, K/32]).
+
+    hi and the scales are ``mxfp8_quant_ref``'s; lo = E4M3 of the residual
+    x - hi * 2^X over 2^Xl, Xl = max(X - 4, -127), rounded to nearest even.
+    The residual is formed in float64, where it is exact (as it is in the
+    kernel's float32: x minus x rounded to 4 significant bits).  Blocks with
+    inf or NaN: hi = 0x7F with the sign, lo = 0, scale 255."""
+    hi, scales = mxfp8_quant_ref(x)
+    a = x.detach().double().cpu().numpy()
+    R, K = a.shape
+    blk = a.reshape(R, K // 32, 32)
+    X, bad = _mx_shared_exp(blk)
+    hv = e4m3_decode(hi.reshape(R, K // 32, 32)) * np.exp2(X.astype(np.float64))[..., None]
+    res = np.where(bad[..., None], 0.0, blk - np.where(bad[..., None], 0.0, hv))
+    Xl = np.maximum(X - 4, -127)
+    lo = _e4m3_codes(res / np.exp2(Xl.astype(np.float64))[..., None])
+    lo = np.where(bad[..., None], 0, lo)
+    return hi, lo.reshape(R, K).astype(np.uint8), scales
+
+
+def mxfp8_split_dequant_ref(hi: np.ndarray, lo: np.ndarray, scales: np.ndarray) -> torch.Tensor:
+    """hi * 2^X + lo * 2^max(X - 4, -127) per 32-element block -> float32."""
+    v_hi, v_lo = e4m3_decode(hi), e4m3_decode(lo)
+    R, K = v_hi.shape
+    X = np.asarray(scales).astype(np.float64) - 127.0
+    out = (v_hi.reshape(R, K // 32, 32) * np.exp2(X)[..., None]
+           + v_lo.reshape(R, K // 32, 32) * np.exp2(np.maximum(X - 4, -127))[..., None])
+    return torch.from_numpy(out.reshape(R, K).astype(np.float32))
 
 
 def mxfp8_dequant_ref(codes: np.ndarray, scales: np.ndarray) -> torch.Tensor:
@@ -343,10 +387,10 @@ def experts_mx_ref(h: torch.Tensor, router_indices: torch.Tensor, routing_weight
                    gate_up_blocks, gate_up_scales, gate_up_bias, down_blocks, down_scales,
                    down_bias, alpha: float = 1.702, limit: float = 7.0) -> torch.Tensor:
     """The MX path's arithmetic: ``experts_ref`` with both GEMMs' activations
-    quantised to MXFP8 (hidden per token; the gated activations after their
-    rounding to bfloat16), float32 elsewhere."""
+    replaced by their two-term MXFP8 split (hidden per token; the gated
+    activations after their rounding to bfloat16), float64 GEMMs."""
     E = gate_up_blocks.shape[0]
-    hq = mxfp8_dequant_ref(*mxfp8_quant_ref(h.float()))
+    hq = mxfp8_split_dequant_ref(*mxfp8_split_ref(h.float()))
     out = torch.zeros(h.shape, dtype=torch.float32)
     mask = F.one_hot(router_indices.to(torch.int64), num_classes=E).permute(2, 1, 0)
     for e in range(E):
@@ -357,7 +401,7 @@ def experts_mx_ref(h: torch.Tensor, router_indices: torch.Tensor, routing_weight
         w_dn = dequant_torch(down_blocks[e:e + 1], down_scales[e:e + 1], torch.float32)[0]
         gu = hq[token_idx].double() @ w_gu.double() + gate_up_bias[e].double()
         act = apply_gate_ref(gu.float(), alpha, limit).to(torch.bfloat16)
-        aq = mxfp8_dequant_ref(*mxfp8_quant_ref(act))
+        aq = mxfp8_split_dequant_ref(*mxfp8_split_ref(act))
         o = (aq.double() @ w_dn.double() + down_bias[e].double()).float()
         o = o * routing_weights[token_idx, top_k_pos, None].float()
         out = out.index_add(0, token_idx, o)

@@ -74,7 +74,8 @@ def test_sweep_forward(device, shape):
         announce(f"sweep forward {shape} mx")
         want_mx = oracle.experts_mx_ref(t["hidden"], idx, w, *expert_args(t))
         got = kernels.moe_experts_forward(g["hidden"], idx.to(device), w.to(device), *expert_args(g), path="mx")
-        assert_layer_close(got, want_mx, f"{shape} mx", absolute=True)
+        assert_layer_close(got, want_mx, f"{shape} mx vs MX oracle", absolute=True)
+        assert_layer_close(got, want, f"{shape} mx vs float32", absolute=True)
 
 
 @pytest.mark.parametrize("shape", SHAPES, ids=[f"E{s[0]}k{s[1]}H{s[2]}I{s[3]}T{s[4]}" for s in SHAPES])

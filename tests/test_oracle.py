@@ -403,3 +403,55 @@ def test_mxfp8_roundtrip_of_representable_blocks():
     zero = (want & 0x7F) == 0                                 # +-0 keep their sign
     assert np.array_equal(q[~zero], want[~zero])
     assert np.array_equal(s[:, 0], (X + 127).astype(np.uint8))
+
+
+@pytest.mark.parametrize("mag", [1e-3, 1.0, 1e4])
+def test_mxfp8_split_lo_matches_torch_cast_of_the_residual(mag):
+    """hi and the scales are the single-term quantisation's; lo is torch's
+    RNE float8_e4m3fn cast of (x - hi * 2^X) / 2^(X-4), with the residual
+    formed from torch's own cast of x / 2^X."""
+    g = torch.Generator().manual_seed(int(mag * 100) % 997 + 1)
+    x = (torch.randn(64, 256, generator=g) * mag).to(torch.bfloat16).float()
+    x[1, :32] = 0.0
+    hi, lo, s = oracle.mxfp8_split_ref(x)
+    q1, s1 = oracle.mxfp8_quant_ref(x)
+    assert np.array_equal(hi, q1) and np.array_equal(s, s1)
+    X = torch.from_numpy(s.astype(np.float64) - 127.0).repeat_interleave(32, dim=1)
+    xd = x.double()
+    hv = (xd / torch.exp2(X)).float().to(torch.float8_e4m3fn).double() * torch.exp2(X)
+    y = (xd - hv) / torch.exp2(torch.clamp(X - 4, min=-127))
+    cast = y.float().to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(cast, lo)
+
+
+def test_mxfp8_split_reconstructs_bf16_exactly():
+    """hi * 2^X + lo * 2^(X-4) is every bfloat16 element above 2^-13 of its
+    block maximum exactly, and misses smaller ones by less than 2^-21 of it."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(128, 512, generator=g)
+    x = x * torch.exp2(torch.randint(-20, 20, (128, 512), generator=g).float())   # wide blocks
+    x = x.to(torch.bfloat16).float()
+    rec = oracle.mxfp8_split_dequant_ref(*oracle.mxfp8_split_ref(x)).double()
+    xd = x.double()
+    amax = xd.view(128, 16, 32).abs().amax(-1, keepdim=True).expand(128, 16, 32).reshape(128, 512)
+    big = xd.abs() >= amax * 2.0 ** -13
+    assert torch.equal(rec[big], xd[big])
+    assert ((rec - xd).abs() <= amax * 2.0 ** -21).all()
+    # a single MXFP8 term is far from exact on the same data
+    one = oracle.mxfp8_dequant_ref(*oracle.mxfp8_quant_ref(x)).double()
+    assert not torch.equal(one[big], xd[big])
+
+
+def test_mxfp8_split_known_answers():
+    """1 + 2^-7 in a block whose maximum it is: X = -8, x / 2^X = 258 rounds to
+    256 (hi 0x78), the residual 2^-7 is 32 * 2^-12 (lo 0x60); zero blocks
+    split to zeros; a non-finite element makes hi NaN, lo zero, scale 255."""
+    x = torch.zeros(1, 128, dtype=torch.float64)
+    x[0, :32] = 1.0 + 2.0 ** -7
+    x[0, 96:] = 1.0
+    x[0, 100] = float("nan")
+    hi, lo, s = oracle.mxfp8_split_ref(x)
+    assert list(s[0]) == [119, 0, 0, 255]
+    assert (hi[0, :32] == 0x78).all() and (lo[0, :32] == 0x60).all()
+    assert (hi[0, 32:96] == 0).all() and (lo[0, 32:96] == 0).all()
+    assert (hi[0, 96:] & 0x7F == 0x7F).all() and (lo[0, 96:] == 0).all()
