@@ -16,20 +16,32 @@ mean launch duration, timed with HIP events on the launch stream (the same
 average rocprofv3 --stats reports for the kernel); ``traffic`` is the mean
 measured HBM bytes per launch from the rocprofv3 FETCH_SIZE/WRITE_SIZE runs
 recorded in profiles/traffic.json, each counter scaled by its plain-copy
-calibration factor (null when absent).  ``cpu_baseline`` times the oracle's torch restatement of the
-reference dequant on the host cores over a bounded sample of the same
-workload.
+calibration factor (null when absent).  ``cpu_baseline`` times the oracle's
+torch restatement of the reference dequant on the host cores over the same
+bytes (drawn on the CPU, copied to the GPU).
+
+``moe_layer`` holds the MoE layer workloads (router, dispatch, expert GEMMs,
+combine; inputs drawn on the CPU and copied to the GPU): the gpt-oss-120b
+decode batches of 1, 8 and 64 tokens (HBM roofline of the weight stream),
+the gpt-oss-20b layer at 2048 tokens and the gpt-oss-120b prefill at 8192
+tokens (MFMA rooflines; forward plus the LoRA input-gradient backward), each
+prefill on the two-term MX kernels and on the dequant-to-bf16 kernels, in
+both blocks layouts, with the relative L2 distance to a float32 reference,
+and CPU baselines of the oracle on token samples of the 64-, 2048- and
+8192-token batches.
 """
 
 from __future__ import annotations
 
 import argparse
+import functools
 import json
 import os
 import statistics
 import sys
 import time
 from pathlib import Path
+from typing import NamedTuple
 
 import torch
 
@@ -58,19 +70,28 @@ def traffic_record(key: str, field: str):
         return None
 
 
+@functools.lru_cache(maxsize=1)
+def cpu_packed() -> tuple:
+    """Both projections' packed weights of one gpt-oss-120b layer, drawn on the
+    CPU from seeded generators; the GPU run gets copies of these bytes."""
+    from blockstreamer_amd import synthetic
+
+    return (synthetic.packed_weights(*GATE_UP, seed=2, scale_lo=115, scale_hi=131),
+            synthetic.packed_weights(*DOWN, seed=3, scale_lo=115, scale_hi=131))
+
+
 def cpu_baseline_dequant() -> dict:
     """Oracle torch restatement of the reference dequant on the host cores.
 
     The sample is the whole workload: both projections of one gpt-oss-120b
-    layer (all 128 experts), median of 3 runs (about 10 s of CPU work).
+    layer (all 128 experts), the same bytes the GPU dequantises, median of 3
+    runs (about 10 s of CPU work).
     """
     import oracle
-    from blockstreamer_amd import synthetic
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    packed = [synthetic.packed_weights(*GATE_UP, seed=2, scale_lo=115, scale_hi=131),
-              synthetic.packed_weights(*DOWN, seed=3, scale_lo=115, scale_hi=131)]
+    packed = cpu_packed()
     oracle.dequant_torch(packed[1][0][:1], packed[1][1][:1], torch.bfloat16)  # warm-up
     times = []
     for _ in range(3):
@@ -88,18 +109,18 @@ def cpu_baseline_dequant() -> dict:
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
+        "cpu": cpu_model(),
         "sample": f"the whole workload (gate_up [128,5760,90,16] + down [128,2880,90,16] -> "
                   f"bf16), median of 3 runs ({t:.2f} s each)",
     }
 
 
 def bench_dequant(args) -> dict:
-    from blockstreamer_amd import kernels, synthetic
+    from blockstreamer_amd import kernels
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    gu_b, gu_s = synthetic.packed_weights(*GATE_UP, seed=2, scale_lo=115, scale_hi=131, device=dev)
-    dn_b, dn_s = synthetic.packed_weights(*DOWN, seed=3, scale_lo=115, scale_hi=131, device=dev)
+    (gu_b, gu_s), (dn_b, dn_s) = ((b.to(dev), sc.to(dev)) for b, sc in cpu_packed())
     gu_out = torch.empty((GATE_UP[0], GATE_UP[2] * 32, GATE_UP[1]), dtype=torch.bfloat16, device=dev)
     dn_out = torch.empty((DOWN[0], DOWN[2] * 32, DOWN[1]), dtype=torch.bfloat16, device=dev)
     bytes_gu = dequant_bytes(*GATE_UP)
@@ -163,10 +184,40 @@ def bench_dequant(args) -> dict:
 
 # ----------------------------------------------------------------------------- MoE layer
 
-GPTOSS_120B = dict(E=128, k=4, H=2880, I=2880)
 BF16_PEAK_TFLOPS = 2500.0
 FP8_PEAK_TFLOPS = 5000.0
 MXFP4_PEAK_TFLOPS = 10100.0
+
+
+class Workload(NamedTuple):
+    """A MoE layer workload: shape, seed and router bias std.  Expert scale
+    bytes are uniform in [115, 131], activations N(0, 1) in bf16, router
+    weights N(0, 0.02)."""
+    E: int
+    k: int
+    H: int
+    I: int
+    seed: int
+    bias_std: float
+
+
+# the 120b decode batches route with a per-expert bias of std 0.5 (uneven
+# expert load); the 20b layer uses 0.01; the 120b prefill 0
+DECODE = Workload(128, 4, 2880, 2880, seed=4, bias_std=0.5)
+LAYER_20B = Workload(32, 4, 2880, 2880, seed=3, bias_std=0.01)
+PREFILL = Workload(128, 4, 2880, 2880, seed=5, bias_std=0.0)
+EXPERT_KEYS = ("gate_up_proj_blocks", "gate_up_proj_scales", "gate_up_proj_bias",
+               "down_proj_blocks", "down_proj_scales", "down_proj_bias")
+
+
+@functools.lru_cache(maxsize=4)
+def cpu_layer(wl: Workload, T: int) -> dict:
+    """The layer's tensors drawn on the CPU from one seeded generator; the GPU
+    runs get copies of these bytes, so the CPU baseline sees the same ones."""
+    from blockstreamer_amd import synthetic
+
+    return synthetic.moe_layer(synthetic.MoEShape(wl.E, wl.k, wl.H, wl.I, T), seed=wl.seed, scale_lo=115,
+                               scale_hi=131, router_bias_std=wl.bias_std)
 
 
 def expert_bytes(H: int, I: int) -> int:
@@ -184,17 +235,52 @@ def _median_ms(pairs):
     return statistics.median([a.elapsed_time(b) for a, b in pairs])
 
 
-def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int,
-              path: str = "auto", layout: str = "checkpoint") -> dict:
-    from blockstreamer_amd import kernels, synthetic
+def fp32_reference(x, idx, w, args, alpha=1.702, limit=7.0):
+    """float32 torch reference of the experts on the GPU (block_streamer/
+    gptoss.py:137-177): dense weights from the dequant kernel (bit-exact with
+    the reference's dequant), float32 GEMMs and SwiGLU."""
+    from blockstreamer_amd import kernels
+
+    gub, gus, gubias, dnb, dns, dnbias = args
+    h = x.float()
+    out = torch.zeros_like(h)
+    for e in torch.unique(idx).tolist():
+        tok, pos = torch.where(idx == e)
+        wgu = kernels.dequantize_mxfp4(gub[e:e + 1], gus[e:e + 1], torch.float32)[0]
+        wdn = kernels.dequantize_mxfp4(dnb[e:e + 1], dns[e:e + 1], torch.float32)[0]
+        gu = h[tok] @ wgu + gubias[e].float()
+        gate, up = gu[:, 0::2].clamp(max=limit), gu[:, 1::2].clamp(min=-limit, max=limit)
+        act = (up + 1) * (gate * torch.sigmoid(gate * alpha))
+        o = act @ wdn + dnbias[e].float()
+        out.index_add_(0, tok, o * w[tok, pos, None].float())
+    return out
+
+
+def _resolved_kernel(path: str, T: int, wl: Workload) -> str:
+    """The expert GEMM kernels a forward runs for ``path`` (the library's
+    rule: automatic selection takes the MX kernels above 16 rows per expert
+    when H and I are multiples of 64 -- the bench's weights are aligned)."""
+    if path != "auto":
+        return path
+    if T * wl.k <= 16 * wl.E:
+        return "stream"
+    return "mx" if wl.H % 64 == 0 and wl.I % 64 == 0 else "tiled"
+
+
+def bench_moe(wl: Workload, T: int, steps: int, warmup: int, path: str = "auto", layout: str = "checkpoint",
+              train: bool = False, fwd: bool = True, ref: bool = False) -> dict:
+    """One MoE layer (router + dispatch + expert GEMMs + combine) of
+    ``wl`` at T tokens.  ``train``: also the LoRA training use, a
+    forward saving the gate_up pre-activations followed by the input-gradient
+    backward.  ``fwd=False``: only that (the profile of the training run).
+    ``ref``: also the output's relative L2 distance to a float32 reference."""
+    from blockstreamer_amd import kernels
 
     dev = torch.device("cuda", 0)
-    E, k, H, I = (GPTOSS_120B[x] for x in ("E", "k", "H", "I"))
-    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=seed, scale_lo=115,
-                            scale_hi=131, router_bias_std=router_bias_std, device=dev)
+    E, k, H, I = wl.E, wl.k, wl.H, wl.I
+    t = {n: v.to(dev) for n, v in cpu_layer(wl, T).items()}
     x = t["hidden"]
-    args = tuple(t[n] for n in ("gate_up_proj_blocks", "gate_up_proj_scales", "gate_up_proj_bias",
-                                "down_proj_blocks", "down_proj_scales", "down_proj_bias"))
+    args = tuple(t[n] for n in EXPERT_KEYS)
     if layout == "kpair":
         # the k-pair shard layout is an on-disk format: repacked once, before
         # anything is timed
@@ -209,119 +295,137 @@ def bench_moe(T: int, steps: int, warmup: int, router_bias_std: float, seed: int
         idx, w = route()
         return kernels.moe_experts_forward(x, idx, w, *args, path=path)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-
-    # per-stage HIP events on the launch stream (a separate pass, so the
-    # events do not sit inside the timed layer steps above)
-    idx, w = route()
-    hit = int(torch.unique(idx).numel())
-    st = kernels.MoEStages(x, idx, w, *args, path=path)
-    names = ("route", "dispatch", "gate_up", "down", "combine")
-    ev = {n: [] for n in names}
-    for _ in range(max(steps, 5)):
-        e = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
-        e[0].record()
-        route()
-        e[1].record()
-        st.dispatch()
-        e[2].record()
-        st.gate_up()
-        e[3].record()
-        st.down()
-        e[4].record()
-        st.combine()
-        e[5].record()
-        for i, n in enumerate(names):
-            ev[n].append((e[i], e[i + 1]))
-    torch.cuda.synchronize()
-    ms = {n: round(_median_ms(ev[n]), 4) for n in names}
-    gemm_ms = ms["gate_up"] + ms["down"]
     flops = moe_flops(T, k, H, I)
-    wbytes = hit * expert_bytes(H, I)
-    res = {
-        "tokens": T,
-        "tokens_per_s": round(T * steps / wall, 1),
-        "ms_per_layer": round(wall / steps * 1e3, 4),
-        "stage_ms": ms,
-        "hit_experts": hit,
-    }
-    hbm = wbytes / (gemm_ms / 1e3) / 1e9
-    tfl = flops / (gemm_ms / 1e3) / 1e12
-    res["path"] = path
-    res["layout"] = layout
-    if T >= 4096 and path != "mx":
+    kernel = _resolved_kernel(path, T, wl)
+    res = {"tokens": T, "path": path, "kernel_path": kernel, "layout": layout}
+    if fwd:
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+
+        # per-stage HIP events on the launch stream (a separate pass, so the
+        # events do not sit inside the timed layer steps above)
+        idx, w = route()
+        hit = int(torch.unique(idx).numel())
+        st = kernels.MoEStages(x, idx, w, *args, path=path)
+        names = ("route", "dispatch", "gate_up", "down", "combine")
+        ev = {n: [] for n in names}
+        for _ in range(max(steps, 5)):
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+            e[0].record()
+            route()
+            e[1].record()
+            st.dispatch()
+            e[2].record()
+            st.gate_up()
+            e[3].record()
+            st.down()
+            e[4].record()
+            st.combine()
+            e[5].record()
+            for i, n in enumerate(names):
+                ev[n].append((e[i], e[i + 1]))
+        torch.cuda.synchronize()
+        ms = {n: round(_median_ms(ev[n]), 4) for n in names}
+        gemm_ms = ms["gate_up"] + ms["down"]
+        wbytes = hit * expert_bytes(H, I)
+        res.update({"tokens_per_s": round(T * steps / wall, 1), "ms_per_layer": round(wall / steps * 1e3, 4),
+                    "stage_ms": ms, "hit_experts": hit})
+        hbm = wbytes / (gemm_ms / 1e3) / 1e9
+        tfl = flops / (gemm_ms / 1e3) / 1e12
+        if kernel == "stream":
+            res["roofline"] = {"bound": "hbm", "achieved": round(hbm, 1), "peak": HBM_PEAK_GBS,
+                               "unit": "GB/s", "frac": round(hbm / HBM_PEAK_GBS, 4),
+                               "kernel": "moe_stream_persist_kernel gate_up + down",
+                               "algorithmic_bytes": wbytes}
+            if T == 64 and layout == "checkpoint":
+                gu_b = traffic_record("moe_layer_gptoss120b_decode_t64", "gate_up_hbm_bytes")
+                dn_b = traffic_record("moe_layer_gptoss120b_decode_t64", "down_hbm_bytes")
+                res["roofline"]["traffic"] = gu_b + dn_b if gu_b and dn_b else None
+        elif kernel == "mx":
+            # two f8f6f4 instructions (hi and lo activation terms) per 64-k
+            # step, each at the FP8 rate: the path's own ceiling is half of it
+            res["roofline"] = {"bound": "mfma", "achieved": round(tfl, 1), "peak": FP8_PEAK_TFLOPS,
+                               "unit": "TFLOP/s", "frac": round(tfl / FP8_PEAK_TFLOPS, 4),
+                               "path_ceiling": FP8_PEAK_TFLOPS / 2,
+                               "frac_of_path_ceiling": round(tfl / (FP8_PEAK_TFLOPS / 2), 4),
+                               "frac_of_mxfp4_peak": round(tfl / MXFP4_PEAK_TFLOPS, 4),
+                               "kernel": "moe_mx_kernel (two-term MXFP8 x MXFP4) gate_up + down, "
+                                         "with the split of the hidden rows",
+                               "algorithmic_flops": flops}
+        else:
+            res["roofline"] = {"bound": "mfma", "achieved": round(tfl, 1), "peak": BF16_PEAK_TFLOPS,
+                               "unit": "TFLOP/s", "frac": round(tfl / BF16_PEAK_TFLOPS, 4),
+                               "frac_of_mxfp4_peak": round(tfl / MXFP4_PEAK_TFLOPS, 4),
+                               "kernel": "moe_tiled2_kernel gate_up + down",
+                               "algorithmic_flops": flops}
+        if ref:
+            want = fp32_reference(x, idx, w, args if layout == "checkpoint" else tuple(t[n] for n in EXPERT_KEYS))
+            got = kernels.moe_experts_forward(x, idx, w, *args, path=path).float()
+            res["rel_l2_vs_fp32"] = round(((got - want).norm() / want.norm()).item(), 6)
+    if train:
         # the LoRA training use: forward saving the gate_up pre-activations,
         # then the input-gradient backward (expert weights frozen)
+        idx, w = route()
         g = (torch.randn(T, H, generator=torch.Generator().manual_seed(7)) * 0.1).to(torch.bfloat16).to(dev)
 
+        def fwd_only():
+            return kernels.moe_experts_forward(x, idx, w, *args, path=path, save=True)
+
         def fwd_bwd():
-            out, ws, pre = kernels.moe_experts_forward(x, idx, w, *args, save=True)
+            out, ws, pre = fwd_only()
             return kernels.moe_experts_backward(g, x, idx, w, args[0], args[1], args[3], args[4], ws, pre)
 
         for _ in range(2):
             fwd_bwd()
         torch.cuda.synchronize()
-        pairs = []
+        pairs, fpairs = [], []
         for _ in range(max(steps // 2, 3)):
-            a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a0, a1, a2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
             a0.record()
-            fwd_bwd()
+            fwd_only()
             a1.record()
-            pairs.append((a0, a1))
+            fwd_bwd()
+            a2.record()
+            fpairs.append((a0, a1))
+            pairs.append((a1, a2))
         torch.cuda.synchronize()
         fb_ms = _median_ms(pairs)
-        fwd_ms = ms["dispatch"] + ms["gate_up"] + ms["down"] + ms["combine"]
+        f_ms = _median_ms(fpairs)
         res["fwd_bwd_ms"] = round(fb_ms, 4)
-        res["bwd_ms"] = round(fb_ms - fwd_ms, 4)
-        res["bwd_TFLOP_per_s"] = round(flops / ((fb_ms - fwd_ms) / 1e3) / 1e12, 1)
-    if path == "mx":
-        # MXFP8 x MXFP4 on the block-scaled MFMA runs at the FP8 rate
-        res["roofline"] = {"bound": "mfma", "achieved": round(tfl, 1), "peak": FP8_PEAK_TFLOPS,
-                           "unit": "TFLOP/s", "frac": round(tfl / FP8_PEAK_TFLOPS, 4),
-                           "frac_of_mxfp4_peak": round(tfl / MXFP4_PEAK_TFLOPS, 4),
-                           "kernel": "mx_quant + moe_mx_kernel gate_up + down",
-                           "algorithmic_flops": flops}
-        ref = kernels.moe_experts_forward(x, idx, w, *args, path="auto").float()
-        got = kernels.moe_experts_forward(x, idx, w, *args, path="mx").float()
-        res["rel_l2_vs_bf16_path"] = round(((got - ref).norm() / ref.norm()).item(), 5)
-    elif T * k <= 16 * E:
-        res["roofline"] = {"bound": "hbm", "achieved": round(hbm, 1), "peak": HBM_PEAK_GBS,
-                           "unit": "GB/s", "frac": round(hbm / HBM_PEAK_GBS, 4),
-                           "kernel": "moe_stream_persist_kernel gate_up + down",
-                           "algorithmic_bytes": wbytes}
-        if T == 64 and layout == "checkpoint":
-            gu_b = traffic_record("moe_layer_gptoss120b_decode_t64", "gate_up_hbm_bytes")
-            dn_b = traffic_record("moe_layer_gptoss120b_decode_t64", "down_hbm_bytes")
-            res["roofline"]["traffic"] = gu_b + dn_b if gu_b and dn_b else None
-    else:
-        res["roofline"] = {"bound": "mfma", "achieved": round(tfl, 1), "peak": BF16_PEAK_TFLOPS,
-                           "unit": "TFLOP/s", "frac": round(tfl / BF16_PEAK_TFLOPS, 4),
-                           "frac_of_mxfp4_peak": round(tfl / MXFP4_PEAK_TFLOPS, 4),
-                           "kernel": "moe_tiled2_kernel gate_up + down",
-                           "algorithmic_flops": flops}
+        res["bwd_ms"] = round(fb_ms - f_ms, 4)
+        res["bwd_TFLOP_per_s"] = round(flops / ((fb_ms - f_ms) / 1e3) / 1e12, 1)
     return res
 
 
-def cpu_baseline_moe(T: int = 64, sample: int = 64) -> dict:
-    """Oracle (fp32 torch restatement of the reference) on the 64-token decode batch."""
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline_moe(wl: Workload, T: int, sample: int, what: str) -> dict:
+    """The oracle (float32 torch restatement of the reference path, router
+    and per-expert dequant + GEMMs + SwiGLU + combine) on the host cores, over
+    the first ``sample`` tokens of the same bytes the GPU runs; tokens/s of
+    that sample, median of 3 runs."""
     import oracle
-    from blockstreamer_amd import synthetic
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    E, k, H, I = (GPTOSS_120B[x] for x in ("E", "k", "H", "I"))
-    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=4, scale_lo=115,
-                            scale_hi=131, router_bias_std=0.5)
+    k = wl.k
+    t = cpu_layer(wl, T)
     h = t["hidden"][:sample]
-    args = tuple(t[n] for n in ("gate_up_proj_blocks", "gate_up_proj_scales", "gate_up_proj_bias",
-                                "down_proj_blocks", "down_proj_scales", "down_proj_bias"))
+    args = tuple(t[n] for n in EXPERT_KEYS)
     times = []
     for _ in range(3):
         t0 = time.perf_counter()
@@ -330,9 +434,9 @@ def cpu_baseline_moe(T: int = 64, sample: int = 64) -> dict:
         times.append(time.perf_counter() - t0)
     tm = statistics.median(times)
     return {"value": round(sample / tm, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"{sample} tokens of the 64-token gpt-oss-120b decode batch, router + "
-                      f"experts in float32 (per-expert dequant + GEMMs), median of 3 "
-                      f"({tm:.2f} s each)"}
+            "cpu": cpu_model(),
+            "sample": f"the first {sample} tokens of the {what} ({T} tokens), router + experts in "
+                      f"float32 (per-expert dequant + GEMMs), median of 3 ({tm:.2f} s each)"}
 
 
 def bench_norm(T: int, reps: int = 50) -> dict:
@@ -350,7 +454,7 @@ def bench_norm(T: int, reps: int = 50) -> dict:
     from blockstreamer_amd import gptoss, kernels
 
     dev = torch.device("cuda", 0)
-    H, eps = GPTOSS_120B["H"], 1e-5
+    H, eps = PREFILL.H, 1e-5
     gen = torch.Generator().manual_seed(11)
     w = (torch.randn(H, generator=gen) * 0.3 + 1.0).to(dev)
     x = torch.randn(T, H, generator=gen).to(torch.bfloat16).to(dev)
@@ -440,9 +544,14 @@ def focused(args) -> int:
     elif args.workload == "norm":
         res = {"norm": [bench_norm(t, reps=max(args.steps, 20)) for t in (64, 8192)]}
     elif args.workload == "moe_decode":
-        res = bench_moe(args.tokens, args.steps, args.warmup, 0.5, seed=4, path=args.path, layout=args.layout)
+        res = bench_moe(DECODE, args.tokens, args.steps, args.warmup, path=args.path, layout=args.layout)
+    elif args.workload == "moe_20b":
+        res = bench_moe(LAYER_20B, 2048, args.steps, args.warmup, path=args.path, layout=args.layout)
+    elif args.workload == "moe_prefill_train":
+        res = bench_moe(PREFILL, 8192, args.steps, args.warmup, path=args.path, layout=args.layout,
+                        train=True, fwd=False)
     else:
-        res = bench_moe(8192, args.steps, args.warmup, 0.0, seed=5, path=args.path, layout=args.layout)
+        res = bench_moe(PREFILL, 8192, args.steps, args.warmup, path=args.path, layout=args.layout)
     print(json.dumps({"workload": args.workload, "steps": args.steps, "warmup": args.warmup, **res}),
           flush=True)
     return 0
@@ -454,13 +563,16 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="dequant",
-                    choices=["dequant", "moe_decode", "moe_prefill", "copy", "norm"],
-                    help="dequant: the headline line (plus MoE layer results); moe_decode / "
-                         "moe_prefill: one MoE workload alone; copy: a plain 2 GiB device copy "
-                         "that calibrates the HBM byte counters; norm: the post-attention "
-                         "RMSNorm, fused and eager")
+                    choices=["dequant", "moe_decode", "moe_20b", "moe_prefill", "moe_prefill_train", "copy",
+                             "norm"],
+                    help="dequant: the headline line (plus MoE layer results); moe_decode / moe_20b / "
+                         "moe_prefill: one MoE layer forward alone; moe_prefill_train: the 8192-token "
+                         "forward that saves for the backward plus the input-gradient backward; copy: a "
+                         "plain 2 GiB device copy that calibrates the HBM byte counters; norm: the "
+                         "post-attention RMSNorm, fused and eager")
     ap.add_argument("--path", default="auto", choices=["auto", "stream", "tiled", "mx"],
-                    help="expert GEMM kernel for the moe_decode / moe_prefill workloads")
+                    help="expert GEMM kernels for the MoE workloads (auto: weight streaming for decode, "
+                         "the two-term MX kernels for prefill)")
     ap.add_argument("--tokens", type=int, default=64, choices=[1, 8, 64],
                     help="token batch of the moe_decode workload (the decode batches 1, 8 and 64)")
     ap.add_argument("--layout", default="checkpoint", choices=["checkpoint", "kpair"],
@@ -496,23 +608,30 @@ def main() -> int:
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_dequant(),
     }
     if not args.no_moe:
+        n_pre = max(args.steps // 4, 5)
         moe = {
-            "decode_t1": bench_moe(1, max(args.steps, 20), args.warmup, 0.5, seed=4),
-            "decode_t8": bench_moe(8, max(args.steps, 20), args.warmup, 0.5, seed=4),
-            "decode_t64": bench_moe(64, max(args.steps, 20), args.warmup, 0.5, seed=4),
-            "prefill_t8192": bench_moe(8192, max(args.steps // 4, 5), args.warmup, 0.0, seed=5),
-            # the same prefill on the native block-scaled MXFP4 matrix cores
-            # (MXFP8 activations), beside the dequant-to-bf16 path above
-            "prefill_t8192_mx": bench_moe(8192, max(args.steps // 4, 5), args.warmup, 0.0, seed=5, path="mx"),
+            "decode_t1": bench_moe(DECODE, 1, max(args.steps, 20), args.warmup),
+            "decode_t8": bench_moe(DECODE, 8, max(args.steps, 20), args.warmup),
+            "decode_t64": bench_moe(DECODE, 64, max(args.steps, 20), args.warmup),
+            # gpt-oss-20b-shaped layer: 32 experts, top-4, 2048 tokens
+            "layer_20b_t2048": bench_moe(LAYER_20B, 2048, max(args.steps, 10), args.warmup, ref=True),
+            # the 8192-token prefill on the native block-scaled MX kernels
+            # (auto), with the LoRA training use, beside the dequant-to-bf16
+            # tiled kernels
+            "prefill_t8192": bench_moe(PREFILL, 8192, n_pre, args.warmup, train=True, ref=True),
+            "prefill_t8192_bf16": bench_moe(PREFILL, 8192, n_pre, args.warmup, path="tiled", ref=True),
             # the same workloads with the blocks in the k-pair shard layout
-            "decode_t64_kpair": bench_moe(64, max(args.steps, 20), args.warmup, 0.5, seed=4, layout="kpair"),
-            "prefill_t8192_kpair": bench_moe(8192, max(args.steps // 4, 5), args.warmup, 0.0, seed=5,
-                                             layout="kpair"),
-            "prefill_t8192_mx_kpair": bench_moe(8192, max(args.steps // 4, 5), args.warmup, 0.0, seed=5,
-                                                path="mx", layout="kpair"),
+            "decode_t64_kpair": bench_moe(DECODE, 64, max(args.steps, 20), args.warmup, layout="kpair"),
+            "prefill_t8192_kpair": bench_moe(PREFILL, 8192, n_pre, args.warmup, layout="kpair", ref=True),
+            "prefill_t8192_bf16_kpair": bench_moe(PREFILL, 8192, n_pre, args.warmup, path="tiled",
+                                                  layout="kpair", ref=True),
         }
         if not args.no_cpu_baseline:
-            moe["decode_t64"]["cpu_baseline"] = cpu_baseline_moe()
+            moe["decode_t64"]["cpu_baseline"] = cpu_baseline_moe(DECODE, 64, 64, "gpt-oss-120b decode batch")
+            moe["layer_20b_t2048"]["cpu_baseline"] = cpu_baseline_moe(LAYER_20B, 2048, 256,
+                                                                      "gpt-oss-20b layer batch")
+            moe["prefill_t8192"]["cpu_baseline"] = cpu_baseline_moe(PREFILL, 8192, 64,
+                                                                    "gpt-oss-120b prefill batch")
         line["moe_layer"] = moe
         line["post_attention_norm"] = {"t64": bench_norm(64), "t8192": bench_norm(8192)}
     print(json.dumps(line), flush=True)

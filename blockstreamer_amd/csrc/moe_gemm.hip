@@ -2493,7 +2493,7 @@ static int launch_gemm(const GemmArgs& a, int path, int64_t P, hipStream_t st) {
 }
 
 static int pick_path(int path, int64_t P, int64_t E, int64_t K) {
-  if (path == PATH_MX) return PATH_MX;     // explicit only; checks its own shape
+  if (path == PATH_MX) return PATH_MX;     // checks its own shape
   if (K % TL_BK != 0) return PATH_STREAM;  // the tiled kernel steps K by 64
   if (path != PATH_AUTO) return path;
   // rows per expert on average: weight streaming while they fit one or two
@@ -2519,6 +2519,22 @@ namespace bsa {
 struct MoeShape {
   int64_t T, H, I, E, k;
 };
+
+// The path of a whole forward (both projections).  Automatic selection takes
+// the MX kernels for prefill-sized batches when both projections can run
+// them: their gate_up stage leaves the split activations, not bf16 ones, for
+// the down stage, so the choice is made once, from both weights' alignment.
+// (The single-stage entry points see one projection only; for them automatic
+// selection stays on paths 1-2.)
+static int resolve_path(int path, const MoeShape& m, const void* gu_b, const void* gu_s, const void* dn_b,
+                        const void* dn_s) {
+  if (path != PATH_AUTO) return path;
+  const bool a16 = reinterpret_cast<uintptr_t>(gu_b) % 16 == 0 && reinterpret_cast<uintptr_t>(dn_b) % 16 == 0;
+  const bool s4 = reinterpret_cast<uintptr_t>(gu_s) % 4 == 0 && reinterpret_cast<uintptr_t>(dn_s) % 4 == 0;
+  const int64_t P = m.T * m.k;
+  if (P > 16 * m.E && m.H % MX_BK == 0 && m.I % MX_BK == 0 && a16 && s4) return PATH_MX;
+  return PATH_AUTO;
+}
 
 static int check_shape(const MoeShape& m, const char* what) {
   BSA_REQUIRE(m.T >= 0 && m.H > 0 && m.I > 0 && m.E > 0 && m.k > 0,
@@ -2800,6 +2816,7 @@ static int experts_fwd(
       (rc = check_layout(blocks_layout, down_blocks, H, I, "experts fwd (down)")))
     return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  path = resolve_path(path, m, gate_up_blocks, gate_up_scales, down_blocks, down_scales);
   if (noalloc) {
     workspace_bytes = carve(nullptr, T, H, I, E, k).bytes;
     BSA_REQUIRE(workspace_bytes <= NOALLOC_SCRATCH_BYTES,

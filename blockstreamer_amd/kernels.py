@@ -291,6 +291,21 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
     return out
 
 
+def _whole_forward_path(path: str, T: int, k: int, E: int, H: int, I: int, gu_b: Tensor, gu_s: Tensor,
+                        dn_b: Tensor, dn_s: Tensor) -> int:
+    """The path code the fused forward runs for ``path`` (the C library's
+    rule for a whole forward): "auto" takes the MX kernels for prefill-sized
+    batches (more than 16 rows per expert on average) when both projections
+    can run them -- H and I multiples of 64, 16-byte aligned blocks, 4-byte
+    aligned scales -- because its gate_up stage leaves split activations for
+    its down stage."""
+    if path != "auto":
+        return PATHS[path]
+    ok = (T * k > 16 * E and H % 64 == 0 and I % 64 == 0 and gu_b.data_ptr() % 16 == 0
+          and dn_b.data_ptr() % 16 == 0 and gu_s.data_ptr() % 4 == 0 and dn_s.data_ptr() % 4 == 0)
+    return PATHS["mx"] if ok else PATHS["auto"]
+
+
 class MoEStages:
     """The four forward stages of one MoE layer call, launched one by one.
 
@@ -321,7 +336,11 @@ class MoEStages:
         self.gu = (_as_u8(gate_up_blocks), _as_u8(gate_up_scales), gate_up_bias)
         self.dn = (_as_u8(down_blocks), _as_u8(down_scales), down_bias)
         self.bias_code = _lib.dtype_code(gate_up_bias.dtype) if gate_up_bias is not None else 0
-        self.alpha, self.limit, self.path = float(alpha), float(limit), PATHS[path]
+        # the stage entry points see one projection each: the path of the
+        # whole forward is resolved here, as the fused call resolves it
+        self.alpha, self.limit = float(alpha), float(limit)
+        self.path = _whole_forward_path(path, self.T, self.k, self.E, self.H, self.I, self.gu[0], self.gu[1],
+                                        self.dn[0], self.dn[1])
         self.ws_bytes = moe_workspace_bytes(self.T, self.H, self.I, self.E, self.k)
         self.ws = _aligned_bytes(self.ws_bytes, self.dev)
         self.out = torch.empty((self.T, self.H), dtype=torch.bfloat16, device=self.dev)

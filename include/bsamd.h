@@ -150,7 +150,10 @@ int bsa_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
  *                   what a later backward reads
  *   save_gate_up    optional float32 [T*k, 2I]: gate_up pre-activations in
  *                   expert-sorted row order, for the backward
- *   path            0 = automatic, 1 = weight-streaming kernel, 2 = tiled kernel,
+ *   path            0 = automatic (path 3 when more than 16 rows per expert
+ *                   on average and both projections can take it, else 1 up to
+ *                   16 rows per expert and 2 beyond), 1 = weight-streaming
+ *                   kernel, 2 = tiled kernel,
  *                   3 = native block-scaled MX kernel (activations split into
  *                   two MXFP8 terms by bsa_quant_mxfp8_split's rule, then two
  *                   v_mfma_scale_f32_32x32x64_f8f6f4 per 64-element k-step on
@@ -219,6 +222,10 @@ int bsa_moe_experts_fwd_noalloc(
  * bsa_moe_combine    replaces gptoss.py:175-176: routing-weight scale and the
  *                    per-token sum (ascending expert order) into out.
  * blocks_layout is that of the blocks argument, as for bsa_moe_experts_fwd.
+ * path is as for bsa_moe_experts_fwd, except that 0 never selects path 3
+ * here (a stage sees one projection only); a caller that wants path 3 for a
+ * layer passes 3 to both bsa_moe_gate_up and bsa_moe_down (the gate_up stage
+ * of path 3 leaves split activations that only path 3's down stage reads).
  */
 int bsa_moe_dispatch(const int64_t *router_indices, int64_t T, int64_t H,
                      int64_t I, int64_t E, int64_t k, void *workspace,
