@@ -60,6 +60,8 @@ _SIGNATURES = {
     "bsa_router_topk": [_ptr, _int, _i64, _i64, _i64, _ptr, _ptr, _ptr],
     "bsa_quant_mxfp8": [_ptr, _int, _i64, _i64, _ptr, _ptr, _i64, _ptr],
     "bsa_quant_mxfp8_split": [_ptr, _int, _i64, _i64, _ptr, _ptr, _i64, _ptr],
+    "bsa_mxfp4_matmul_workspace_bytes": [_i64, _i64, _i64, _int, _int, ctypes.POINTER(_i64)],
+    "bsa_mxfp4_matmul": [_ptr, _int, _i64, _i64, _i64, _ptr, _ptr, _int, _int, _ptr, _int, _ptr, _i64, _ptr],
     "bsa_moe_bwd_workspace_bytes": [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_i64)],
     "bsa_moe_experts_bwd": [
         _ptr, _int, _i64, _i64, _i64, _i64, _i64,  # grad_out, dtype, T, H, I, E, k

@@ -2993,3 +2993,184 @@ extern "C" int bsa_moe_experts_bwd(
   return launch_combine(b.dx, router_indices, nullptr, DT_F32, w.pair_pos, (int)T, (int)k, (int)H,
                         grad_hidden, grad_hidden_dtype, st);
 }
+
+// ---------------------------------------------------------------------------
+// One expert's packed matmul: block_streamer/gptoss.py:45-75 (mxfp4_matmul),
+// forward x @ W and its input gradient g @ W^T, with W = dequant(blocks,
+// scales) in the [K, N] orientation of gptoss.py:41.  No dense W exists: the
+// forward runs the grouped GEMMs above on a one-expert dispatch, the
+// transposed product the packed-row kernel of the backward.  The activation
+// operand enters the MFMA as bf16; a float16 x is split into 2 bf16 terms and
+// a float32 x into 3 (their sum is x exactly), one pass per term, and the
+// float32 partial products are summed in term order and rounded once.  The
+// products of the terms with the weights are exact, so a float32 x gets
+// float32 accuracy (the sum order differs from a library GEMM's).
+// ---------------------------------------------------------------------------
+namespace bsa {
+
+__global__ void mm_setup_kernel(int M, int* counts, int* offsets, int2* tiles, int* num_tiles) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const int nt = (M + TL_BM - 1) / TL_BM;
+  if (i < nt) tiles[i] = make_int2(0, i * TL_BM);
+  if (i == 0) {
+    counts[0] = M;
+    offsets[0] = 0;
+    offsets[1] = M;
+    *num_tiles = nt;
+  }
+}
+
+// x (n elements, dtype) -> `terms` bf16 arrays [terms][n] whose sum is x.
+__global__ void mm_split_kernel(const void* __restrict__ x, int dtype, int64_t n, int terms,
+                                uint16_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float v;
+  if (dtype == DT_F32)
+    v = static_cast<const float*>(x)[i];
+  else if (dtype == DT_BF16)
+    v = __uint_as_float((uint32_t) static_cast<const uint16_t*>(x)[i] << 16);
+  else
+    v = (float)__builtin_bit_cast(_Float16, static_cast<const uint16_t*>(x)[i]);
+  for (int t = 0; t < terms; ++t) {
+    const uint32_t b = f32_to_bf16_bits(v);
+    out[t * n + i] = (uint16_t)b;
+    v -= __uint_as_float(b << 16);  // exact: v minus v rounded to 8 bits
+  }
+}
+
+// out[i] = sum over t of parts[t][i], rounded once to out_dtype.
+__global__ void mm_sum_kernel(const float* __restrict__ parts, int terms, int64_t n, void* __restrict__ out,
+                              int out_dtype) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float v = parts[i];
+  for (int t = 1; t < terms; ++t) v += parts[t * n + i];
+  if (out_dtype == DT_F32)
+    static_cast<float*>(out)[i] = v;
+  else if (out_dtype == DT_BF16)
+    static_cast<uint16_t*>(out)[i] = (uint16_t)f32_to_bf16_bits(v);
+  else
+    static_cast<uint16_t*>(out)[i] = (uint16_t)f32_to_f16_bits(v);
+}
+
+struct MmWorkspace {
+  int* counts;
+  int* offsets;
+  int2* tiles;
+  int* num_tiles;
+  uint16_t* terms;  // [terms][M][kin] bf16
+  float* parts;     // [terms][M][nout] f32
+  int64_t bytes;
+};
+
+static int mm_terms(int dtype) { return dtype == DT_F32 ? 3 : (dtype == DT_F16 ? 2 : 1); }
+
+// kin / nout: the activation's and the output's columns (K, N forward; N, K
+// transposed).
+static MmWorkspace carve_mm(void* base, int64_t M, int64_t kin, int64_t nout, int terms) {
+  char* p = static_cast<char*>(base);
+  int64_t off = 0;
+  MmWorkspace w{};
+  auto take = [&](int64_t bytes) {
+    char* r = p ? p + off : nullptr;
+    off = align_up(off + bytes, 256);
+    return r;
+  };
+  w.counts = reinterpret_cast<int*>(take(4));
+  w.offsets = reinterpret_cast<int*>(take(8));
+  w.tiles = reinterpret_cast<int2*>(take(((M + TL_BM - 1) / TL_BM + 1) * 8));
+  w.num_tiles = reinterpret_cast<int*>(take(4));
+  w.terms = reinterpret_cast<uint16_t*>(take(terms * M * kin * 2));
+  w.parts = reinterpret_cast<float*>(take(terms * M * nout * 4));
+  w.bytes = off;
+  return w;
+}
+
+static int mm_check(int64_t M, int64_t K, int64_t N, int x_dtype, int transpose, const char* what) {
+  BSA_REQUIRE(M >= 0 && K > 0 && N > 0 && K % 32 == 0, "%s: bad shape M=%lld K=%lld N=%lld (K %% 32 == 0)",
+              what, (long long)M, (long long)K, (long long)N);
+  BSA_REQUIRE(dtype_ok(x_dtype), "%s: bad dtype %d", what, x_dtype);
+  BSA_REQUIRE(transpose == 0 || transpose == 1, "%s: transpose must be 0 or 1", what);
+  BSA_REQUIRE(M * (K > N ? K : N) * 3 < ((int64_t)1 << 40) && M < INT32_MAX / 2, "%s: too large", what);
+  if (transpose)
+    BSA_REQUIRE(N % 64 == 0 && N % 8 == 0 && (N * (K / 32)) % 16 == 0,
+                "%s: the transposed product needs N %% 64 == 0 (N=%lld)", what, (long long)N);
+  return BSA_OK;
+}
+
+}  // namespace bsa
+
+extern "C" int bsa_mxfp4_matmul_workspace_bytes(int64_t M, int64_t K, int64_t N, int x_dtype, int transpose,
+                                                int64_t* bytes) {
+  clear_error();
+  BSA_REQUIRE(bytes, "mxfp4 matmul workspace size: null output pointer");
+  int rc = mm_check(M, K, N, x_dtype, transpose, "mxfp4 matmul workspace size");
+  if (rc) return rc;
+  *bytes = carve_mm(nullptr, M, transpose ? N : K, transpose ? K : N, mm_terms(x_dtype)).bytes;
+  return BSA_OK;
+}
+
+extern "C" int bsa_mxfp4_matmul(const void* x, int x_dtype, int64_t M, int64_t K, int64_t N, const void* blocks,
+                                const void* scales, int blocks_layout, int transpose, void* out, int out_dtype,
+                                void* workspace, int64_t workspace_bytes, void* stream) {
+  clear_error();
+  int rc = mm_check(M, K, N, x_dtype, transpose, "mxfp4 matmul");
+  if (rc || M == 0) return rc;
+  BSA_REQUIRE(dtype_ok(out_dtype), "mxfp4 matmul: bad output dtype %d", out_dtype);
+  BSA_REQUIRE(x && blocks && scales && out && workspace, "mxfp4 matmul: null pointer");
+  BSA_REQUIRE(reinterpret_cast<uintptr_t>(blocks) % 8 == 0 && reinterpret_cast<uintptr_t>(scales) % 4 == 0,
+              "mxfp4 matmul: blocks must be 8-byte and scales 4-byte aligned");
+  BSA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "mxfp4 matmul: workspace must be 256-byte aligned");
+  BSA_REQUIRE(x_dtype == DT_F32 ? reinterpret_cast<uintptr_t>(x) % 4 == 0 : reinterpret_cast<uintptr_t>(x) % 2 == 0,
+              "mxfp4 matmul: x not aligned to its element size");
+  if ((rc = check_layout(blocks_layout, blocks, N, K, "mxfp4 matmul"))) return rc;
+  const int terms = mm_terms(x_dtype);
+  const int64_t kin = transpose ? N : K, nout = transpose ? K : N;
+  const MmWorkspace w = carve_mm(workspace, M, kin, nout, terms);
+  BSA_REQUIRE(workspace_bytes >= w.bytes, "mxfp4 matmul: workspace of %lld bytes, need %lld",
+              (long long)workspace_bytes, (long long)w.bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t nt = (M + TL_BM - 1) / TL_BM;
+  hipLaunchKernelGGL(mm_setup_kernel, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st, (int)M, w.counts,
+                     w.offsets, w.tiles, w.num_tiles);
+  const int64_t nin = M * kin, nres = M * nout;
+  hipLaunchKernelGGL(mm_split_kernel, dim3((unsigned)((nin + 255) / 256)), dim3(256), 0, st, x, x_dtype, nin,
+                     terms, w.terms);
+  BSA_LAUNCH_CHECK("mxfp4 matmul set-up launch");
+  for (int t = 0; t < terms; ++t) {
+    GemmArgs g{};
+    g.kp = blocks_layout == BSA_LAYOUT_KPAIR;
+    g.A = w.terms + t * nin;
+    g.lda = kin;
+    g.row_pair = nullptr;
+    g.topk = 1;
+    g.Bq = static_cast<const uint8_t*>(blocks);
+    g.Bs = static_cast<const uint8_t*>(scales);
+    g.counts = w.counts;
+    g.offsets = w.offsets;
+    g.E = 1;
+    g.out = w.parts + t * nres;
+    g.ldo = nout;
+    g.out_dtype = DT_F32;
+    g.tiles = w.tiles;
+    g.num_tiles = w.num_tiles;
+    if (!transpose) {
+      g.N = (int)N;
+      g.K = (int)K;
+      g.n_tiles_n = (int)((N + TL_BN - 1) / TL_BN);
+      rc = launch_gemm<EPI_BIAS_F32>(g, pick_path(PATH_AUTO, M, 1, K), M, st);
+    } else {
+      // the packed rows (N of them) are the reduction; outputs run along K
+      g.N = (int)K;
+      g.K = (int)N;
+      BSA_REQUIRE(bwd_packed_ok(g), "mxfp4 matmul: unsupported operand layout for the transposed product");
+      rc = launch_gemm_packed_rows<EPI_STORE>(g, M, st);
+    }
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(mm_sum_kernel, dim3((unsigned)((nres + 255) / 256)), dim3(256), 0, st, w.parts, terms, nres,
+                     out, out_dtype);
+  BSA_LAUNCH_CHECK("mxfp4 matmul sum launch");
+  return BSA_OK;
+}

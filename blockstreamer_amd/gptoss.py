@@ -9,6 +9,8 @@ The arithmetic runs in hand-written gfx950 HIP kernels (``libbsamd.so``):
 * ``MXFP4Experts.forward`` is one device-side dispatch, two grouped GEMMs
   that decode MXFP4 on the fly (bias and clamped SwiGLU fused), and a
   combine -- no host synchronisation and no dense weight in memory;
+* ``mxfp4_matmul`` runs one expert's product and its input gradient on the
+  packed GEMM kernels (float32 inputs to float32 accuracy);
 * ``dequantize_expert`` is the dequant kernel, bit-exact with the reference.
 
 The module reads its parameters at every call and never caches device
@@ -16,6 +18,8 @@ pointers or mutates them (the StreamedModel contract, streamer.py:159-174).
 """
 
 from __future__ import annotations
+
+import warnings
 
 import torch
 from torch import Tensor, nn
@@ -43,31 +47,46 @@ def dequantize_expert(
     return dense.squeeze(0)
 
 
-class _MXFP4Matmul(torch.autograd.Function):
-    """x @ dequantize(blocks, scales), re-dequantizing in backward.
+def _autocast_dtype(x: Tensor) -> torch.dtype:
+    """The dtype a matmul on ``x`` runs in: the autocast dtype while GPU
+    autocast is on (as ``x @ W`` would be cast inside an autocast region),
+    else ``x``'s own."""
+    if x.is_cuda and torch.is_autocast_enabled("cuda"):
+        return torch.get_autocast_dtype("cuda")
+    return x.dtype
 
-    block_streamer/gptoss.py:45-71.  Only the packed tensors are saved, so the
-    dense weight is a temporary in both directions; backward returns dX only.
+
+class _MXFP4Matmul(torch.autograd.Function):
+    """Packed-weight product for one expert (block_streamer/gptoss.py:45-71).
+
+    Both directions run the hand-written packed GEMMs (``kernels.mxfp4_matmul``):
+    the forward reads the MXFP4 blocks as the B operand, the input gradient
+    reads the same blocks along their rows.  No dense weight is formed, and
+    the context keeps only the packed tensors (already resident as staged
+    state), so nothing of size K x N outlives the call.  The weights are
+    frozen: only the input gets a gradient.
     """
 
     @staticmethod
+    @torch.amp.custom_fwd(device_type="cuda")
     def forward(ctx, x: Tensor, blocks: Tensor, scales: Tensor) -> Tensor:
-        weight = dequantize_expert(blocks, scales, x.dtype)
-        ctx.save_for_backward(x, blocks, scales)
-        return x @ weight
+        dtype = _autocast_dtype(x)
+        ctx.save_for_backward(blocks, scales)
+        ctx.x_dtype = x.dtype
+        return kernels.mxfp4_matmul(x.to(dtype), blocks, scales)
 
     @staticmethod
+    @torch.amp.custom_bwd(device_type="cuda")
     def backward(ctx, grad: Tensor) -> tuple[Tensor | None, None, None]:
-        x, blocks, scales = ctx.saved_tensors
-        grad_x = None
-        if ctx.needs_input_grad[0]:
-            weight = dequantize_expert(blocks, scales, x.dtype)
-            grad_x = grad @ weight.transpose(-2, -1)
-        return grad_x, None, None
+        if not ctx.needs_input_grad[0]:
+            return None, None, None
+        blocks, scales = ctx.saved_tensors
+        return kernels.mxfp4_matmul(grad, blocks, scales, transpose=True, out_dtype=ctx.x_dtype), None, None
 
 
 def mxfp4_matmul(x: Tensor, blocks: Tensor, scales: Tensor) -> Tensor:
-    """block_streamer/gptoss.py:74-75."""
+    """``x @ dequantize_expert(blocks, scales, x.dtype)``, differentiable in
+    ``x`` (block_streamer/gptoss.py:74-75), without the dense weight."""
     return _MXFP4Matmul.apply(x, blocks, scales)
 
 
@@ -169,6 +188,11 @@ class MXFP4Experts(nn.Module):
             raise ValueError("MXFP4Experts.forward needs router_indices and routing_weights")
         shape = hidden_states.shape
         flat = hidden_states.reshape(-1, shape[-1])
+        if flat.dtype != torch.bfloat16 and not (flat.is_cuda and torch.is_autocast_enabled("cuda")):
+            warnings.warn(
+                f"MXFP4Experts: {flat.dtype} hidden states enter the fused expert GEMMs as bfloat16 (the "
+                "result keeps the input dtype); run the layer in bfloat16 or under torch.autocast, or use "
+                "mxfp4_matmul per expert for float32 products", stacklevel=2)
         out = _MoEExperts.apply(
             flat, router_indices, routing_weights,
             self.gate_up_proj_blocks, self.gate_up_proj_scales, self.gate_up_proj_bias,

@@ -103,6 +103,48 @@ def dequantize_mxfp4(blocks: Tensor, scales: Tensor, dtype: torch.dtype = torch.
     return out
 
 
+def mxfp4_matmul(x: Tensor, blocks: Tensor, scales: Tensor, transpose: bool = False,
+                 out_dtype: torch.dtype | None = None) -> Tensor:
+    """One expert's packed matmul with no dense weight (block_streamer/
+    gptoss.py:45-75): ``x [..., K] @ W`` (``W`` the ``[K, N]`` matrix
+    ``dequantize_expert`` returns), or with ``transpose=True``
+    ``x [..., N] @ W.T``, from ``blocks [1, N, K/32, 16]`` and
+    ``scales [1, N, K/32]`` (the expert axis as the reference passes it; the
+    k-pair layout is accepted too).  bf16, f16 and f32 ``x``; the result is in
+    ``out_dtype`` (default ``x.dtype``).  f32 ``x`` keeps float32 accuracy
+    (three exact bf16 terms, one GEMM pass each)."""
+    layout = blocks_layout(blocks)
+    E, N, G = packed_shape(blocks)
+    if E != 1 or tuple(scales.shape) != (1, N, G):
+        raise ValueError(f"expected one expert's blocks [1, N, K/32, 16] and scales [1, N, K/32], got "
+                         f"{tuple(blocks.shape)} and {tuple(scales.shape)}")
+    K = G * 32
+    kin, nout = (N, K) if transpose else (K, N)
+    if x.shape[-1] != kin:
+        raise ValueError(f"x has {x.shape[-1]} columns; this product needs {kin}")
+    dev = _lib.require_gpu(x, blocks, scales)
+    code = _lib.dtype_code(x.dtype)
+    out_dtype = out_dtype or x.dtype
+    blocks, scales = _as_u8(blocks), _as_u8(scales)
+    if layout == LAYOUT_KPAIR:
+        _require_kpair_aligned(blocks, "blocks")
+    blocks = _aligned(blocks, 8)
+    scales = _aligned(scales, 4)
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, kin).contiguous()
+    M = x2.shape[0]
+    out = torch.empty((M, nout), dtype=out_dtype, device=dev)
+    import ctypes
+    n = ctypes.c_int64(0)
+    _lib.call("bsa_mxfp4_matmul_workspace_bytes", M, K, N, code, int(transpose), ctypes.byref(n))
+    ws = _aligned_bytes(n.value, dev)
+    with torch.cuda.device(dev):
+        _lib.call("bsa_mxfp4_matmul", x2.data_ptr(), code, M, K, N, blocks.data_ptr(), scales.data_ptr(),
+                  layout, int(transpose), out.data_ptr(), _lib.dtype_code(out_dtype), ws.data_ptr(), n.value,
+                  _lib.stream_handle(dev))
+    return out.reshape(*lead, nout)
+
+
 # Expert GEMM kernels: "stream" (weight streaming, decode), "tiled" (bf16
 # MFMA over LDS tiles, prefill), "auto" (by rows per expert) -- all bf16
 # activations x exactly dequantised MXFP4 weights; "mx" (the activations as

@@ -61,7 +61,8 @@ const char *bsa_last_error(void);
  * changes whenever an existing signature changes: 2 inserted the
  * blocks_layout argument before the stream in bsa_moe_experts_fwd,
  * bsa_moe_gate_up, bsa_moe_down and bsa_moe_experts_bwd.  The minor number
- * counts added entry points (201: bsa_moe_experts_fwd_noalloc).  A binding
+ * counts added entry points (201: bsa_moe_experts_fwd_noalloc; 202:
+ * bsa_quant_mxfp8_split, bsa_mxfp4_matmul).  A binding
  * checks the major number before its first call. */
 #define BSA_VERSION_MAJOR 2
 int bsa_version(void);
@@ -308,6 +309,33 @@ int bsa_quant_mxfp8(const void *x, int dtype, int64_t R, int64_t K, void *q,
 int bsa_quant_mxfp8_split(const void *x, int dtype, int64_t R, int64_t K,
                           void *q, void *scales, int64_t scale_ld,
                           void *stream);
+
+/*
+ * One expert's packed matmul.  Replaces block_streamer/gptoss.py:45-75
+ * (_MXFP4Matmul / mxfp4_matmul: x @ dequantize_expert(blocks, scales) and
+ * its input gradient g @ W^T), with no dense weight: W = the [K, N] matrix
+ * of gptoss.py:41 from blocks uint8 [N, K/32, 16] (or the k-pair layout) and
+ * scales uint8 [N, K/32].
+ *
+ *   transpose 0: out [M, N] = x [M, K] @ W
+ *   transpose 1: out [M, K] = x [M, N] @ W^T   (needs N % 64 == 0)
+ *
+ * x is bf16, f16 or f32 (x_dtype); out is out_dtype.  The activation operand
+ * enters the matrix cores as bf16: f16 x is split into 2 bf16 terms and f32
+ * x into 3 (their sum is x exactly), one pass per term; the float32 partial
+ * products are summed in term order and rounded once to out_dtype, so an f32
+ * x gets float32 accuracy (a different summation order from a library
+ * GEMM's).  K % 32 == 0; blocks 8-byte and scales 4-byte aligned; workspace
+ * >= bsa_mxfp4_matmul_workspace_bytes(...), 256-byte aligned.
+ */
+int bsa_mxfp4_matmul_workspace_bytes(int64_t M, int64_t K, int64_t N,
+                                     int x_dtype, int transpose,
+                                     int64_t *bytes);
+int bsa_mxfp4_matmul(const void *x, int x_dtype, int64_t M, int64_t K,
+                     int64_t N, const void *blocks, const void *scales,
+                     int blocks_layout, int transpose, void *out,
+                     int out_dtype, void *workspace, int64_t workspace_bytes,
+                     void *stream);
 
 /*
  * Bytes of the extra workspace bsa_moe_experts_bwd needs (the per-row

@@ -119,6 +119,30 @@ CASES = [
     ("mxfp8 alignment", "bsa_quant_mxfp8", (FAKE + 8, BF16, 4, 128, FAKE, FAKE, 4, None), _lib.BSA_EINVAL,
      b"aligned"),
     ("mxfp8 R = 0", "bsa_quant_mxfp8", (None, BF16, 0, 128, None, None, 4, None), _lib.BSA_OK, None),
+    ("split K % 64", "bsa_quant_mxfp8_split", (FAKE, BF16, 4, 96, FAKE, FAKE, 3, None), _lib.BSA_EINVAL,
+     b"K % 64"),
+    ("split alignment", "bsa_quant_mxfp8_split", (FAKE + 8, BF16, 4, 128, FAKE, FAKE, 4, None), _lib.BSA_EINVAL,
+     b"aligned"),
+    ("split R = 0", "bsa_quant_mxfp8_split", (None, BF16, 0, 128, None, None, 4, None), _lib.BSA_OK, None),
+    ("matmul ws size K % 32", "bsa_mxfp4_matmul_workspace_bytes", (8, 48, 64, F32, 0, OUT), _lib.BSA_EINVAL,
+     b"K % 32"),
+    ("matmul ws size null", "bsa_mxfp4_matmul_workspace_bytes", (8, 128, 64, F32, 0, None), _lib.BSA_EINVAL,
+     b"null"),
+    ("matmul transpose N % 64", "bsa_mxfp4_matmul",
+     (FAKE, F32, 8, 128, 96, FAKE, FAKE, 0, 1, FAKE, F32, FAKE, 1 << 20, None), _lib.BSA_EINVAL, b"N % 64"),
+    ("matmul bad transpose", "bsa_mxfp4_matmul",
+     (FAKE, F32, 8, 128, 64, FAKE, FAKE, 0, 2, FAKE, F32, FAKE, 1 << 20, None), _lib.BSA_EINVAL, b"transpose"),
+    ("matmul dtype", "bsa_mxfp4_matmul",
+     (FAKE, 7, 8, 128, 64, FAKE, FAKE, 0, 0, FAKE, F32, FAKE, 1 << 20, None), _lib.BSA_EINVAL, b"dtype"),
+    ("matmul null", "bsa_mxfp4_matmul",
+     (FAKE, F32, 8, 128, 64, None, FAKE, 0, 0, FAKE, F32, FAKE, 1 << 20, None), _lib.BSA_EINVAL, b"null"),
+    ("matmul blocks alignment", "bsa_mxfp4_matmul",
+     (FAKE, F32, 8, 128, 64, FAKE + 4, FAKE, 0, 0, FAKE, F32, FAKE, 1 << 20, None), _lib.BSA_EINVAL,
+     b"8-byte"),
+    ("matmul workspace too small", "bsa_mxfp4_matmul",
+     (FAKE, F32, 8, 128, 64, FAKE, FAKE, 0, 0, FAKE, F32, FAKE, 256, None), _lib.BSA_EINVAL, b"workspace"),
+    ("matmul M = 0", "bsa_mxfp4_matmul",
+     (None, F32, 0, 128, 64, None, None, 0, 0, None, F32, None, 0, None), _lib.BSA_OK, None),
     ("dequant unknown layout", "bsa_dequant_mxfp4_layout", (FAKE, FAKE, FAKE, BF16, 1, 32, 4, 0, 2, None),
      _lib.BSA_EINVAL, b"layout"),
     ("dequant k-pair rows", "bsa_dequant_mxfp4_layout", (FAKE, FAKE, FAKE, BF16, 1, 24, 4, 0, 1, None),
