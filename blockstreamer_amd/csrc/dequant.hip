@@ -7,13 +7,16 @@
 // reads each packed byte once and writes each output element once.
 //
 // Vectorised path: a workgroup owns 64 consecutive packed rows r of one
-// expert (a contiguous 64 * G * 16-byte span) and walks all G groups.  Each
-// lane decodes 8 consecutive rows of one group (8 x 16-byte loads; for a
-// fixed row the 8 lanes of a row-group read 128 contiguous bytes), then
-// transposes in registers so that for each of the group's 32 output rows k it
-// stores the 8 adjacent columns r..r+7 as one 16-byte store (for a fixed k,
-// 8 lanes write 128 contiguous bytes).  Everything is HBM-bound: 2.53 bytes
-// of traffic per bf16 output element.
+// expert and 32 of their groups, one 8-group tile per wave, and exits (short
+// workgroups measured faster than ones walking all G groups).  Each lane
+// decodes 8 consecutive rows of one group (8 x 16-byte loads; for a fixed row
+// the 8 lanes of a row-group read 128 contiguous bytes), then transposes in
+// registers so that for each of the group's 32 output rows k it stores the 8
+// adjacent columns r..r+7 as one 16-byte store (for a fixed k, 8 lanes write
+// 128 contiguous bytes).  Everything is HBM-bound: 2.53 bytes of traffic per
+// bf16 output element.  Each scale byte is read by the one lane that decodes
+// its 32 elements, straight from memory: a lane owns whole groups, so an LDS
+// broadcast would have no second reader.
 #include <algorithm>
 
 #include "bsa_common.h"
@@ -23,6 +26,7 @@ namespace bsa {
 constexpr int DQ_ROWG = 8;             // row-groups of 8 rows per wave
 constexpr int DQ_GPW = 64 / DQ_ROWG;   // groups per wave
 constexpr int DQ_ROWS = 8 * DQ_ROWG;   // rows per workgroup (64)
+constexpr int DQ_GPB = 4 * DQ_GPW;     // groups per workgroup (32): one group tile per wave
 
 template <int OUT>
 __device__ __forceinline__ void dq_store8(void* out, size_t elem_off, const uint32_t v2[4]) {
@@ -43,45 +47,58 @@ __device__ __forceinline__ void dq_store8(void* out, size_t elem_off, const uint
 }
 
 template <int OUT, bool HW>
+__device__ __forceinline__ uint32_t dq_decode_byte(uint32_t d, int b, uint32_t s) {
+  const uint32_t byte = (d >> (8 * b)) & 0xFFu;
+  if constexpr (OUT == DT_F16) {
+    return mx_byte_to_f16x2(byte, s);
+  } else if constexpr (HW) {
+    return mx_byte_to_bf16x2_hw<0>(byte, mx_scale_f32(s));
+  } else {
+    return mx_byte_to_bf16x2_exact(byte, s);
+  }
+}
+
+template <int OUT, bool HW>
 __device__ __forceinline__ void dq_decode_store(const u32x4_t (&pk)[8], const uint32_t (&s)[8],
                                                 void* out, size_t out_base, int R) {
   // out_base = element offset of (k = 32g, r) for this lane's first row.
+  // One packed byte column (codes 2j, 2j+1 of the 8 rows) at a time, so that
+  // only 8 decoded words are live next to the packed bytes.
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    uint32_t c[8][4];  // c[row][byte b] = bf16x2 of codes (2j, 2j+1), j = 4q + b
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t d = pk[i][q];
-      if constexpr (OUT == DT_F16) {
-        c[i][0] = mx_byte_to_f16x2(d & 0xFFu, s[i]);
-        c[i][1] = mx_byte_to_f16x2((d >> 8) & 0xFFu, s[i]);
-        c[i][2] = mx_byte_to_f16x2((d >> 16) & 0xFFu, s[i]);
-        c[i][3] = mx_byte_to_f16x2(d >> 24, s[i]);
-      } else if constexpr (HW) {
-        const float sf = mx_scale_f32(s[i]);
-        c[i][0] = mx_byte_to_bf16x2_hw<0>(d, sf);
-        c[i][1] = mx_byte_to_bf16x2_hw<1>(d, sf);
-        c[i][2] = mx_byte_to_bf16x2_hw<2>(d, sf);
-        c[i][3] = mx_byte_to_bf16x2_hw<3>(d, sf);
-      } else {
-        c[i][0] = mx_byte_to_bf16x2_exact(d & 0xFFu, s[i]);
-        c[i][1] = mx_byte_to_bf16x2_exact((d >> 8) & 0xFFu, s[i]);
-        c[i][2] = mx_byte_to_bf16x2_exact((d >> 16) & 0xFFu, s[i]);
-        c[i][3] = mx_byte_to_bf16x2_exact(d >> 24, s[i]);
-      }
-    }
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
+      uint32_t c[8];  // c[row] = bf16x2 of codes (2j, 2j+1), j = 4q + b
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i] = dq_decode_byte<OUT, HW>(pk[i][q], b, s[i]);
       const int k = 2 * (4 * q + b);
       uint32_t ev[4], od[4];
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
-        ev[p] = pack_lo16(c[2 * p][b], c[2 * p + 1][b]);
-        od[p] = pack_hi16(c[2 * p][b], c[2 * p + 1][b]);
+        ev[p] = pack_lo16(c[2 * p], c[2 * p + 1]);
+        od[p] = pack_hi16(c[2 * p], c[2 * p + 1]);
       }
       dq_store8<OUT>(out, out_base + (size_t)k * R, ev);
       dq_store8<OUT>(out, out_base + (size_t)(k + 1) * R, od);
     }
+  }
+}
+
+// The packed bytes and scales of group g for this lane's 8 rows.
+template <bool ALIGN16>
+__device__ __forceinline__ void dq_load(const uint8_t* __restrict__ blocks, const uint8_t* __restrict__ scales,
+                                        size_t row0, int g, int G, int kp, u32x4_t (&pk)[8], uint32_t (&s)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint8_t* p = blocks + bq_off(kp, (int64_t)(row0 + i), g, G);
+    if constexpr (ALIGN16) {
+      pk[i] = *reinterpret_cast<const u32x4_t*>(p);
+    } else {
+      const uint2 a = *reinterpret_cast<const uint2*>(p);
+      const uint2 b = *reinterpret_cast<const uint2*>(p + 8);
+      pk[i] = u32x4_t{a.x, a.y, b.x, b.y};
+    }
+    s[i] = scales[(row0 + i) * G + g];
   }
 }
 
@@ -92,48 +109,28 @@ __global__ __launch_bounds__(256) void dequant_vec_kernel(const uint8_t* __restr
                                                           int row_tiles, int mode, int kp) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int e = blockIdx.x / row_tiles;
-  const int rt = blockIdx.x - e * row_tiles;
+  const int gchunks = (G + DQ_GPB - 1) / DQ_GPB;
+  const int ert = blockIdx.x / gchunks;
+  const int gc = blockIdx.x - ert * gchunks;
+  const int e = ert / row_tiles;
+  const int rt = ert - e * row_tiles;
   const int r = rt * DQ_ROWS + 8 * (lane % DQ_ROWG);
-  const int K = G * 32;
-  const int g_tiles = (G + DQ_GPW - 1) / DQ_GPW;
-  if (r >= R) return;  // R % 8 == 0, so a lane owns either 8 valid rows or none
+  const int g = gc * DQ_GPB + wave * DQ_GPW + lane / DQ_ROWG;
+  if (r >= R || g >= G) return;  // R % 8 == 0, so a lane owns either 8 valid rows or none
   const size_t row0 = (size_t)e * R + r;
-
-  for (int gt = wave; gt < g_tiles; gt += 4) {
-    const int g = gt * DQ_GPW + lane / DQ_ROWG;
-    const bool active = g < G;
-    u32x4_t pk[8];
-    uint32_t s[8];
-    bool in_range = true;
+  u32x4_t pk[8];
+  uint32_t s[8];
+  dq_load<ALIGN16>(blocks, scales, row0, g, G, kp, pk, s);
+  bool in_range = true;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (active) {
-        const size_t rg = (row0 + i) * G + g;
-        const uint8_t* p = blocks + bq_off(kp, (int64_t)(row0 + i), g, G);
-        if constexpr (ALIGN16) {
-          pk[i] = *reinterpret_cast<const u32x4_t*>(p);
-        } else {
-          const uint2 a = *reinterpret_cast<const uint2*>(p);
-          const uint2 b = *reinterpret_cast<const uint2*>(p + 8);
-          pk[i] = u32x4_t{a.x, a.y, b.x, b.y};
-        }
-        s[i] = scales[rg];
-      } else {
-        pk[i] = u32x4_t{0u, 0u, 0u, 0u};
-        s[i] = 127u;
-      }
-      in_range = in_range && mx_scale_hw_ok(s[i]);
-    }
-    const bool hw = (mode == 2) || (mode == 0 && __all(in_range));
-    if (active) {
-      const size_t out_base = ((size_t)e * K + (size_t)32 * g) * R + r;
-      if (hw && OUT != DT_F16)
-        dq_decode_store<OUT, true>(pk, s, out, out_base, R);
-      else
-        dq_decode_store<OUT, false>(pk, s, out, out_base, R);
-    }
-  }
+  for (int i = 0; i < 8; ++i) in_range = in_range && mx_scale_hw_ok(s[i]);
+  // one decoder per wave: lanes that returned above count as in range
+  const bool hw = (mode == 2) || (mode == 0 && __all(in_range));
+  const size_t out_base = ((size_t)e * G * 32 + (size_t)32 * g) * R + r;
+  if (hw && OUT != DT_F16)
+    dq_decode_store<OUT, true>(pk, s, out, out_base, R);
+  else
+    dq_decode_store<OUT, false>(pk, s, out, out_base, R);
 }
 
 // Fallback for any shape or alignment: one thread per packed byte.
@@ -188,7 +185,7 @@ static int launch_dequant(const uint8_t* blocks, const uint8_t* scales, void* ou
   }
   if (vec) {
     const int row_tiles = (int)((R + DQ_ROWS - 1) / DQ_ROWS);
-    const int64_t nblk = E * row_tiles;
+    const int64_t nblk = E * row_tiles * ((G + DQ_GPB - 1) / DQ_GPB);
     if (nblk > INT32_MAX) {
       set_error("dequant: grid too large (E=%lld R=%lld)", (long long)E, (long long)R);
       return BSA_EINVAL;
