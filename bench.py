@@ -257,9 +257,10 @@ def fp32_reference(x, idx, w, args, alpha=1.702, limit=7.0):
 
 
 def _resolved_kernel(path: str, T: int, wl: Workload) -> str:
-    """The expert GEMM kernels a forward runs for ``path`` (the library's
-    rule: automatic selection takes the MX kernels above 16 rows per expert
-    when H and I are multiples of 64 -- the bench's weights are aligned)."""
+    """The expert GEMM kernels an inference forward runs for ``path`` (the
+    library's rule: automatic selection takes the MX kernels above 16 rows
+    per expert when H and I are multiples of 64 -- the bench's weights are
+    aligned; a forward saving for the backward keeps the bf16 kernels)."""
     if path != "auto":
         return path
     if T * wl.k <= 16 * wl.E:

@@ -276,6 +276,16 @@ __device__ __forceinline__ uint32_t mx_split8(const float (&v)[8], uint32_t (&hi
   return bad ? 255u : (uint32_t)(X + 127);
 }
 
+// Where the two-term MXFP8 split of an activation matrix goes: the 128 code
+// bytes (64 hi, 64 lo) of 64-element k-tile t of row r at
+// r * q_row + t * q_kt, block g's scale byte at r * s_row + (g / 2) * s_kt +
+// g % 2.  Row-major: q_row = 2K, q_kt = 128, s_row = scale row stride, s_kt
+// = 2.  K-tile-major (the MX GEMM's operand): q_row = 128, q_kt = 128 *
+// rows, s_row = 4, s_kt = 4 * rows (two scale bytes and two spare per row).
+struct SplitLayout {
+  int64_t q_row, q_kt, s_row, s_kt;
+};
+
 // Activation / weight element types accepted by the kernels.
 enum DType : int { DT_BF16 = BSA_DTYPE_BF16, DT_F16 = BSA_DTYPE_F16, DT_F32 = BSA_DTYPE_F32 };
 

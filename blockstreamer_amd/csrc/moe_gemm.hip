@@ -48,6 +48,7 @@
 // (odd) columns (gptoss.py:131).  Every forward kernel places gate column j
 // and up column j in the same lane (or adjacent lanes), so the clamped SwiGLU
 // runs in registers.
+#include <algorithm>
 #include <mutex>
 
 #include "bsa_common.h"
@@ -63,8 +64,8 @@ int launch_combine(const float* Y, const int64_t* idx, const void* w, int w_dtyp
 int launch_bwd_prep(const void* dout, int dout_dtype, const float* y, const void* w, int w_dtype,
                     const int* pair_pos, int P, int k, int H, uint16_t* dy, float* grad_w,
                     hipStream_t st);
-int launch_quant_mxfp8_split(const void* x, int in_dtype, int64_t R, int64_t K, int64_t ldx, uint8_t* q,
-                             int64_t ldq, uint8_t* s, int64_t lds, hipStream_t st);
+int launch_quant_mxfp8_split(const void* x, int in_dtype, int64_t R, int64_t K, int64_t ldx, const int* row_map,
+                             int topk, uint8_t* q, uint8_t* s, SplitLayout L, hipStream_t st);
 
 enum Epi : int {
   EPI_SWIGLU = 0,    // out bf16 [P][N/2] = swiglu(acc + bias), optional f32 pre-activation save
@@ -73,8 +74,8 @@ enum Epi : int {
   EPI_SWIGLU_BWD = 3,  // out bf16 [P][2N] = d(gate_up) from acc = d(act) and the saved
                        // f32 pre-activations in save_pre [P][2N]
   EPI_SWIGLU_MX = 4,   // as EPI_SWIGLU, the bf16 activations then split into two MXFP8
-                       // terms: out uint8 [P][ldo] (hi/lo per 64-element k-tile, the
-                       // layout of launch_quant_mxfp8_split), out_s [P][ldos] scale bytes
+                       // terms, stored in the SplitLayout {ldo, out_kt, ldos, out_s_kt}
+                       // (codes at out, scale bytes at out_s)
 };
 
 struct GemmArgs {
@@ -97,12 +98,14 @@ struct GemmArgs {
   const int2* tiles;     // tiled kernel: (expert, first sorted row) per row tile
   const int* num_tiles;
   int n_tiles_n;         // column tiles per row tile
-  const uint8_t* Aq;     // MX path: E4M3 activations, row stride ldq bytes
-  const uint8_t* As;     // MX path: E8M0 activation scales, row stride ldas bytes (% 4 == 0)
+  const uint8_t* Aq;     // MX path: split activations, k-tile-major: k-tile kt of sorted row
+                         // pos at Aq + kt * ldq + pos * 128
+  const uint8_t* As;     // MX path: their scale bytes, at As + kt * ldas + pos * 4 (+ 0, 1)
   int64_t ldq, ldas;
   int kp;                // Bq in the k-pair layout [E][N/16][K/64][16][2][16]
   uint8_t* out_s;        // EPI_SWIGLU_MX: scale bytes of the split activations
   int64_t ldos;
+  int64_t out_kt, out_s_kt;  // EPI_SWIGLU_MX: k-tile strides of the codes and scales
 };
 
 
@@ -302,11 +305,12 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& a, const f32x16_
         const uint32_t sbyte = mx_split8(v, hq, lq);
         if (ok) {
           const int b = c0 >> 5;  // block of the row
-          uint8_t* q = static_cast<uint8_t*>(a.out) + (int64_t)(m0 + r0w + r) * a.ldo + (b >> 1) * 128 +
-                       (b & 1) * 32 + (ch & 3) * 8;
+          const int64_t row = m0 + r0w + r;
+          uint8_t* q = static_cast<uint8_t*>(a.out) + row * a.ldo + (b >> 1) * a.out_kt + (b & 1) * 32 +
+                       (ch & 3) * 8;
           *reinterpret_cast<uint2*>(q) = make_uint2(hq[0], hq[1]);
           *reinterpret_cast<uint2*>(q + 64) = make_uint2(lq[0], lq[1]);
-          if ((ch & 3) == 0) a.out_s[(int64_t)(m0 + r0w + r) * a.ldos + b] = (uint8_t)sbyte;
+          if ((ch & 3) == 0) a.out_s[row * a.ldos + (b >> 1) * a.out_s_kt + (b & 1)] = (uint8_t)sbyte;
         }
       }
     }
@@ -1409,8 +1413,9 @@ __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
 // path is limited by the number of requests, so every DMA covers contiguous
 // runs:
 //  * A stage [128][64] bf16, 8 lanes per row (128 contiguous bytes); row r's
-//    16-byte chunk c is stored at chunk c ^ (r & 7), so fragment reads are
-//    bank-conflict free;
+//    16-byte chunk c is stored at chunk c ^ ((r >> 1) & 7), so fragment reads
+//    are bank-conflict free (a ds_read_b128 pass serves 16 lanes from 64
+//    banks, 256 bytes: two rows);
 //  * B stage kept packed, [256 rows][2 groups][16 bytes], 2 lanes per row
 //    (32 contiguous bytes), the two halves of row q swapped when bit 3 of q
 //    is set (conflict-free 16-lane reads);
@@ -1533,7 +1538,7 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 8 * (4 * wave + i) + (lane >> 3);
-    const int ch = (lane & 7) ^ (r & 7);
+    const int ch = (lane & 7) ^ ((r >> 1) & 7);
     const int64_t pos = m0 + (r < rows ? r : 0);
     const int64_t src = a.row_pair ? (int64_t)(a.row_pair[pos] / a.topk) : pos;
     asrc[i] = a.A + src * a.lda + ch * 8;
@@ -1575,9 +1580,11 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
     bias[nb] = ok ? bias_at(a.bias, a.bias_dtype, (int64_t)e * a.N + n0 + bq[nb]) : 0.f;
   }
   // LDS byte offsets (within a stage) of this lane's A fragments for step
-  // (h, m): chunk 4h + 2lh + m of row l32 sits at chunk ^ (row & 7); rows
-  // mb*32 + l32 add mb * 4096.  And of its two B rows.
-  const int rsw = l32 & 7;
+  // (h, m): chunk 4h + 2lh + m of row l32 sits at chunk ^ ((row >> 1) & 7)
+  // (16 lanes of one ds_read_b128 pass then cover all 64 banks: two
+  // 128-byte rows share them); rows mb*32 + l32 add mb * 4096.  And of its
+  // two B rows.
+  const int rsw = (l32 >> 1) & 7;
   uint32_t aoff[4];
 #pragma unroll
   for (int step = 0; step < 4; ++step) {
@@ -1645,17 +1652,20 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
 // runs:
 //  * A stage [128][128 B]: per row the k-tile's 64 hi codes then 64 lo codes
 //    (the split's row layout), 8 lanes per row; row r's 16-byte chunk c sits
-//    at chunk c ^ (r & 7), so the fragment reads are bank-conflict free;
+//    at chunk c ^ ((r >> 1) & 7), so the fragment reads are bank-conflict
+//    free (ds_read_b128 serves 16 lanes a cycle from 64 banks, i.e. 256
+//    bytes: two 128-byte rows share the banks, so the swizzle pairs them);
 //  * B stage [BN rows][2 groups][16 bytes], 2 lanes per row (32 contiguous
 //    bytes, 512 in the k-pair layout), the two halves of row q swapped when
 //    bit 3 of q is set;
-//  * scales are loaded once per tile, not per k-step: the B scales of the
-//    tile's BN weight rows are one contiguous BN*G-byte span of the
-//    checkpoint tensor; the A scales come from rows padded to ldas bytes
-//    (a multiple of 16) by the quantisation kernel; lo's scale byte is hi's
-//    minus 4.
-// A WM x WN grid of waves (default 2 x 4: each wave 64 rows x 128 weight rows,
-// 2 x 4 blocks of 32 x 32, one workgroup per CU) splits the tile; 64 x 128
+//  * A scales [128][4 B] per stage: the split writes the activations
+//    k-tile-major (k-tile kt of sorted row p at kt*ldq + 128p, its two scale
+//    bytes at kt*ldas + 4p), so a stage's codes and scales are each one
+//    contiguous run; lo's scale byte is hi's minus 4;
+//  * the B scales of the tile's BN weight rows, one contiguous BN*G-byte
+//    span of the checkpoint tensor, are loaded once per tile.
+// A WM x WN grid of waves (default 2 x 2: each wave 64 rows x 128 weight rows,
+// 2 x 4 blocks of 32 x 32, two workgroups per CU) splits the tile; 64 x 128
 // per wave reads 12 LDS fragments per 16 MFMAs where 128 x 64 reads 18.
 // Bound: MFMA at the FP8 rate, two instructions per step (the bf16 rate).
 // ---------------------------------------------------------------------------
@@ -1663,33 +1673,6 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
 constexpr int MX_BM = 128;
 constexpr int MX_BK = 64;
 constexpr int MX_A_BYTES = MX_BM * MX_BK * 2;   // 16 KiB: hi and lo codes
-
-// Per-configuration sizes: WM x WN waves, wave (wm, wn) owning MB = 4/WM
-// row blocks and NB column blocks of 32 x 32 (rows 32*MB*wm .., weight rows
-// 32*NB*wn .. of the tile); BN = 32 * NB * WN weight rows per tile.
-template <int WM, int WN, int NB>
-struct MxCfg {
-  static constexpr int W = WM * WN;                   // waves
-  static constexpr int MB = 4 / WM;
-  static constexpr int WCOLS = 32 * NB;
-  static constexpr int BN = WCOLS * WN;
-  static constexpr int B_BYTES = BN * 32;
-  static constexpr int STAGE = MX_A_BYTES + B_BYTES;
-  static constexpr int A_DMA = 16 / W;                // A instructions per wave per stage
-  static constexpr int B_DMA = BN / 32 / W;           // B instructions per wave per stage
-  static constexpr int DMA_PER_TILE = A_DMA + B_DMA;
-  static constexpr int EPI_LDS = epi_lds_bytes(MB, NB);  // per-wave epilogue staging bytes
-};
-
-// LDS row stride of the A scales: an odd number of 16-byte chunks >= ldas.
-__host__ __device__ inline int mx_scale_ld(int ldas) { return (ldas / 16) % 2 ? ldas : ldas + 16; }
-
-// Dynamic LDS bytes of moe_mx_kernel with ns stages and bn weight rows per
-// tile: stages, A scales, B scales.
-inline size_t mx_smem_bytes(int ns, int bn, int K, int64_t ldas) {
-  return (size_t)ns * (MX_A_BYTES + (size_t)bn * 32) + (size_t)MX_BM * mx_scale_ld((int)ldas) +
-         (size_t)bn * (K / 32);
-}
 
 // Activation row read for sorted row r of a tile that starts at sorted row
 // m0 and holds `rows` rows (rows past the tile read the tile's first row).
@@ -1700,33 +1683,131 @@ __device__ __forceinline__ int64_t tile_src_row(const GemmArgs& a, int m0, int r
   return a.row_pair ? (int64_t)(a.row_pair[pos] / a.topk) : pos;
 }
 
-// One stage's DMA of the MX kernel (the A and B pieces of k-tile kt).  A
-// device function rather than a lambda: HIP-Clang does not emit the
-// host-side handle of these kernel templates when their bodies call a
-// capturing lambda.
+// Per-configuration sizes: WM x WN waves, wave (wm, wn) owning MB = 4/WM
+// row blocks and NB column blocks of 32 x 32 (rows 32*MB*wm .., weight rows
+// 32*NB*wn .. of the tile); BN = 32 * NB * WN weight rows per tile.  A stage
+// holds the A codes (16 KiB), the A scale bytes (4 per row) and the B codes;
+// the B scales of the tile's weight rows are loaded once per tile (per-stage
+// loads of their two bytes per row measured slower: one request per row).
+constexpr int MX_AS_BYTES = MX_BM * 4;
+template <int WM, int WN, int NB>
+struct MxCfg {
+  static constexpr int W = WM * WN;                   // waves
+  static constexpr int MB = 4 / WM;
+  static constexpr int NBLK = NB;
+  static constexpr int WCOLS = 32 * NB;
+  static constexpr int BN = WCOLS * WN;
+  static constexpr int B_BYTES = BN * 32;
+  static constexpr int B_OFF = MX_A_BYTES + MX_AS_BYTES;
+  static constexpr int STAGE = B_OFF + B_BYTES;
+  static constexpr int A_DMA = 16 / W;                // A instructions per wave per stage
+  static constexpr int AS_ROWS = MX_BM / W;           // A scale rows per wave (one dword each)
+  static constexpr int B_DMA = BN / 32 / W;           // B instructions per wave per stage
+  static constexpr int DMA_PER_TILE = A_DMA + 1 + B_DMA;
+  static constexpr int EPI_LDS = epi_lds_bytes(MB, NB);  // per-wave epilogue staging bytes
+};
+
+// Dynamic LDS bytes of moe_mx_kernel with ns stages and bn weight rows per
+// tile: the stages and the B scales.
+inline size_t mx_smem_bytes(int ns, int bn, int K) {
+  return (size_t)ns * (MX_A_BYTES + MX_AS_BYTES + (size_t)bn * 32) + (size_t)bn * (K / 32);
+}
+
+// One stage's DMA of the MX kernel (the A codes, A scales and B pieces of
+// k-tile kt).  A device function rather than a lambda: HIP-Clang does not
+// emit the host-side handle of these kernel templates when their bodies call
+// a capturing lambda.
 template <class C, int MX_NS>
-__device__ __forceinline__ void mx_issue(uint8_t* smem, int kt, int wave, const uint8_t* const* asrc,
-                                         const uint8_t* const* bsrc, int bkt) {
+__device__ __forceinline__ void mx_issue(uint8_t* smem, int kt, int wave, int lane, const uint8_t* asrc,
+                                         const uint32_t* aoff, const uint8_t* ssrc, int64_t lda_kt,
+                                         int64_t lds_kt, const uint8_t* const* bsrc, int bkt) {
   uint8_t* st = smem + (kt % MX_NS) * C::STAGE;
+  const uint8_t* a = asrc + kt * lda_kt;
 #pragma unroll
   for (int j = 0; j < C::A_DMA; ++j)
-    __builtin_amdgcn_global_load_lds(asrc[j] + kt * 2 * MX_BK, (lds_void*)(st + (C::A_DMA * wave + j) * 1024),
-                                     16, 0, 0);
+    __builtin_amdgcn_global_load_lds(a + aoff[j], (lds_void*)(st + (C::A_DMA * wave + j) * 1024), 16, 0, 0);
+  if (lane < C::AS_ROWS)
+    __builtin_amdgcn_global_load_lds(ssrc + kt * lds_kt, (lds_void*)(st + MX_A_BYTES + C::AS_ROWS * 4 * wave), 4,
+                                     0, 0);
 #pragma unroll
   for (int h = 0; h < C::B_DMA; ++h)
-    __builtin_amdgcn_global_load_lds(bsrc[h] + kt * bkt,
-                                     (lds_void*)(st + MX_A_BYTES + (C::B_DMA * wave + h) * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(bsrc[h] + kt * bkt, (lds_void*)(st + C::B_OFF + (C::B_DMA * wave + h) * 1024),
+                                     16, 0, 0);
+}
+
+// Workgroups per CU (the launch bound); two hide each other's barrier and
+// DMA waits, and the 2 x 2 wave grid's stages and B scales fit both in LDS.
+#ifndef BSA_MX_WG_PER_CU
+#define BSA_MX_WG_PER_CU 2
+#endif
+
+// One wave's operands of one 64-k step: its MB row blocks' hi and lo codes
+// with their scale bytes, its NB column blocks' packed weights and scales.
+template <int MB, int NB>
+struct MxFrags {
+  i32x8_t ahi[MB], alo[MB];
+  int sa[MB];  // hi's scale byte; lo's is max(sa - 4, 0)
+  u32x4_t b[NB];
+  int sb[NB];
+};
+
+// Read step kt's operands from stage st (offsets as set up in the kernel) for
+// the wave's first nmb row blocks, as plain LDS loads: the compiler tracks
+// each one, so the first MFMAs of a step start while the reads of the later
+// operands are still in flight.  (Reading step kt+1 into a second register
+// set during step kt's MFMAs measured slower: the second set does not fit
+// two workgroups per CU.)
+template <int MB, int NB>
+__device__ __forceinline__ void mx_read(MxFrags<MB, NB>& f, const uint8_t* st, uint32_t aoff0, uint32_t aoff1,
+                                        uint32_t aoff2, uint32_t aoff3, uint32_t asoff, uint32_t boff,
+                                        const uint8_t* sb_row, int G, int kt, int nmb) {
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    f.sb[nb] = sb_row[nb * 32 * G + 2 * kt];
+    f.b[nb] = *reinterpret_cast<const u32x4_t*>(st + boff + nb * 1024);
+  }
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    if (mb >= nmb) continue;
+    const uint8_t* ar = st + mb * 32 * 128;
+    const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(ar + aoff0);
+    const u32x4_t w1 = *reinterpret_cast<const u32x4_t*>(ar + aoff1);
+    const u32x4_t w2 = *reinterpret_cast<const u32x4_t*>(ar + aoff2);
+    const u32x4_t w3 = *reinterpret_cast<const u32x4_t*>(ar + aoff3);
+    f.ahi[mb] = i32x8_t{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3], (int)w1[0], (int)w1[1], (int)w1[2],
+                        (int)w1[3]};
+    f.alo[mb] = i32x8_t{(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3], (int)w3[0], (int)w3[1], (int)w3[2],
+                        (int)w3[3]};
+    f.sa[mb] = st[asoff + mb * 32 * 4];
+  }
+}
+
+// The MFMAs of one step for the wave's first nmb row blocks (the others hold
+// no rows of the tile; nmb is uniform across the wave).
+template <int MB, int NB>
+__device__ __forceinline__ void mx_mfma(f32x16_t (&acc)[MB][NB], const MxFrags<MB, NB>& f, int nmb = MB) {
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      if (mb >= nmb) continue;
+      const i32x8_t b = {(int)f.b[nb][0], (int)f.b[nb][1], (int)f.b[nb][2], (int)f.b[nb][3], 0, 0, 0, 0};
+      acc[mb][nb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.ahi[mb], b, acc[mb][nb], 0, 4, 0, f.sa[mb], 0,
+                                                                    f.sb[nb]);
+      acc[mb][nb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.alo[mb], b, acc[mb][nb], 0, 4, 0,
+                                                                    f.sa[mb] > 4 ? f.sa[mb] - 4 : 0, 0, f.sb[nb]);
+    }
 }
 
 template <int EPI, int MX_NS, bool SB16, int WM, int WN, int NB>
-__global__ __launch_bounds__(64 * WM * WN, (WM * WN == 4 && NB == 2) ? 2 : 1) void moe_mx_kernel(GemmArgs a) {
+__global__ __launch_bounds__(64 * WM * WN, BSA_MX_WG_PER_CU) void moe_mx_kernel(GemmArgs a) {
   using C = MxCfg<WM, WN, NB>;
   constexpr int MB = C::MB;
   constexpr int W = C::W;
   static_assert(MX_NS >= 2 && MX_NS <= 6, "pipeline depth");
   static_assert(WM * MB == 4 && (W == 4 || W == 8), "wave grid");
   static_assert(C::B_DMA * W * 32 == C::BN, "B stage split over the waves");
-  static_assert(W * C::EPI_LDS <= MX_NS * C::STAGE, "epilogue staging fits in the stages");
+  static_assert(C::AS_ROWS <= 64, "one scale DMA per wave");
   constexpr int BN = C::BN;
   extern __shared__ __align__(1024) uint8_t smem[];
   const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
@@ -1737,7 +1818,6 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN == 4 && NB == 2) ? 2 : 1) vo
   const int e = te.x;
   const int m0 = te.y;
   const int rows = min(MX_BM, a.offsets[e] + a.counts[e] - m0);
-  const int mbn = __builtin_amdgcn_readfirstlane((rows + 31) >> 5);  // 32-row blocks with rows
   const int n0 = nt * BN;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1748,46 +1828,26 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN == 4 && NB == 2) ? 2 : 1) vo
   const int KT = a.K / MX_BK;
   const int l32 = lane & 31;
   const int lh = lane >> 5;
-  // A scales in LDS: rows of an odd number of 16-byte chunks (ldas, plus one
-  // unused chunk when ldas / 16 is even), so the byte reads of 16 rows hit
-  // 16 different banks
-  const int sld = mx_scale_ld((int)a.ldas);
-  uint8_t* sas = smem + MX_NS * C::STAGE;  // [128][sld] A scales
-  uint8_t* sbs = sas + MX_BM * sld;         // [BN][G] B scales
-
-  // --- scales, once per tile ----------------------------------------------
-  {
-    preload_b_scales<SB16, BN, W>(a.Bs, e, a.N, n0, G, sbs, wave, lane);
-    // A: 128 gathered rows of ldas bytes in 16-byte chunks (a padding chunk
-    // reloads the row's first chunk)
-    const int cpr = sld / 16;
-    const int real = (int)a.ldas / 16;
-    const int nch = MX_BM * cpr;
-    for (int j = wave; j * 64 < nch; j += W) {
-      const int c = j * 64 + lane;
-      if (c < nch) {
-        const int r = c / cpr;
-        const int part = c - r * cpr;
-        __builtin_amdgcn_global_load_lds(
-            a.As + tile_src_row(a, m0, rows, r) * a.ldas + (part < real ? part : 0) * 16,
-            (lds_void*)(sas + j * 1024), 16, 0, 0);
-      }
-    }
-  }
+  uint8_t* sbs = smem + MX_NS * C::STAGE;  // [BN][G] B scales
+  preload_b_scales<SB16, BN, W>(a.Bs, e, a.N, n0, G, sbs, wave, lane);
 
   // --- per-lane stage DMA sources (every lane always issues all of them, so
   //     the per-wave vmcnt arithmetic is exact; rows or columns past the tile
-  //     read a clamped valid address and are never stored) -----------------
-  // A: instruction i = A_DMA*wave + j covers rows 8i .. 8i+7, 8 lanes per
-  // row (the k-tile's 64 hi and 64 lo codes); row r's chunk c lands in slot
-  // c ^ (r & 7)
-  const uint8_t* asrc[C::A_DMA];
+  //     are loaded from valid addresses and never stored) ------------------
+  // A: the tile's 128 sorted rows of k-tile kt are one contiguous 16 KiB run
+  // (rows past the valid ones belong to the next expert, or to the 128 spare
+  // rows at the end).  Instruction i = A_DMA*wave + j covers rows 8i .. 8i+7,
+  // 8 lanes per row; row r's chunk c lands in slot c ^ ((r >> 1) & 7).
+  const uint8_t* asrc = a.Aq + (int64_t)m0 * 128;
+  uint32_t aoff_src[C::A_DMA];
 #pragma unroll
   for (int j = 0; j < C::A_DMA; ++j) {
     const int r = 8 * (C::A_DMA * wave + j) + (lane >> 3);
-    const int ch = (lane & 7) ^ (r & 7);
-    asrc[j] = a.Aq + tile_src_row(a, m0, rows, r) * a.ldq + ch * 16;
+    aoff_src[j] = (uint32_t)(r * 128 + (((lane & 7) ^ ((r >> 1) & 7)) * 16));
   }
+  // A scales: one dword (two scale bytes, two spare) per row; wave w loads rows
+  // AS_ROWS*w .. +AS_ROWS
+  const uint8_t* ssrc = a.As + (int64_t)(m0 + C::AS_ROWS * wave + (lane < C::AS_ROWS ? lane : 0)) * 4;
   // B: instruction i = B_DMA*wave + h covers rows 32i .. 32i+31, 2 lanes per
   // row; row q's group g sits in half g ^ ((q >> 3) & 1) of its 32 bytes
   const uint8_t* bsrc[C::B_DMA];
@@ -1811,18 +1871,17 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN == 4 && NB == 2) ? 2 : 1) vo
   }
   // LDS byte offsets of this lane's A chunks in row 32*(MB*wm + mb) + l32:
   // hi codes in chunks lh and 2 + lh, lo codes in 4 + lh and 6 + lh (the
-  // row's swizzle r & 7 does not depend on the row block)
-  const int rsw = l32 & 7;
+  // row's swizzle (r >> 1) & 7 does not depend on the row block)
+  const int rsw = (l32 >> 1) & 7;
   const uint32_t abase = (uint32_t)(MB * wm * 32 * 128 + l32 * 128);
   const uint32_t aoff0 = abase + (uint32_t)((lh ^ rsw) * 16);
   const uint32_t aoff1 = abase + (uint32_t)(((2 + lh) ^ rsw) * 16);
   const uint32_t aoff2 = abase + (uint32_t)(((4 + lh) ^ rsw) * 16);
   const uint32_t aoff3 = abase + (uint32_t)(((6 + lh) ^ rsw) * 16);
+  const uint32_t asoff = (uint32_t)(MX_A_BYTES + (MB * wm * 32 + l32) * 4 + lh);  // + mb*32*4
   // B: half lh ^ bsw of row bq (bsw = bit 3 of the row, the same for every nb)
-  const uint32_t boff = (uint32_t)(bq[0] * 32 + ((lh ^ ((bq[0] >> 3) & 1)) * 16));
-  const uint8_t* sa_row = sas + (MB * wm * 32 + l32) * sld + lh;  // + mb*32*sld + 2kt
-  const uint8_t* sb_row = sbs + bq[0] * G + lh;                   // + nb*32*G + 2kt
-  const int mbw = mbn - MB * wm;  // this wave's row blocks holding rows
+  const uint32_t boff = (uint32_t)(C::B_OFF + bq[0] * 32 + ((lh ^ ((bq[0] >> 3) & 1)) * 16));
+  const uint8_t* sb_row = sbs + bq[0] * G + lh;  // + nb*32*G + 2kt
 
   f32x16_t acc[MB][NB];
 #pragma unroll
@@ -1832,44 +1891,26 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN == 4 && NB == 2) ? 2 : 1) vo
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
+  // Stage j % NS holds step j; step kt + NS - 1 is issued into the stage of
+  // step kt - 1 once every wave has passed step kt's barrier (its MFMAs of
+  // step kt - 1, and so the reads they used, are done).  Row blocks past the
+  // tile's rows are neither read nor multiplied (nmb: the wave's row blocks
+  // holding rows of the tile, uniform across the wave).
   for (int i = 0; i < MX_NS - 1; ++i)
-    if (i < KT) mx_issue<C, MX_NS>(smem, i, wave, asrc, bsrc, bkt);
+    if (i < KT) mx_issue<C, MX_NS>(smem, i, wave, lane, asrc, aoff_src, ssrc, a.ldq, a.ldas, bsrc, bkt);
+  const int nmb = min(MB, max(0, (rows - MB * wm * 32 + 31) / 32));
+  MxFrags<MB, NB> f;
   for (int kt = 0; kt < KT; ++kt) {
-    // tile kt (and, on the first pass, the scales issued before it) has
-    // landed once at most the tiles issued after it are in flight
+    // step kt (and the B scales issued first) has landed once at most the
+    // steps issued after it are in flight; a bare s_barrier (a
+    // __syncthreads() fence would wait for those too)
     wait_tiles_ahead<C::DMA_PER_TILE, MX_NS - 2>(min(MX_NS - 2, KT - 1 - kt));
     asm volatile("s_barrier" ::: "memory");
-    if (kt + MX_NS - 1 < KT) mx_issue<C, MX_NS>(smem, kt + MX_NS - 1, wave, asrc, bsrc, bkt);
-    const uint8_t* st = smem + (kt % MX_NS) * C::STAGE;
-    int sb[NB];
-    i32x8_t bop[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      sb[nb] = (int)sb_row[nb * 32 * G + 2 * kt];
-      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(st + MX_A_BYTES + boff + nb * 1024);
-      bop[nb] = i32x8_t{(int)w[0], (int)w[1], (int)w[2], (int)w[3], 0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      if (mb >= mbw) continue;  // row block past the tile's valid rows
-      const uint8_t* ar = st + mb * 32 * 128;
-      const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(ar + aoff0);
-      const u32x4_t w1 = *reinterpret_cast<const u32x4_t*>(ar + aoff1);
-      const u32x4_t w2 = *reinterpret_cast<const u32x4_t*>(ar + aoff2);
-      const u32x4_t w3 = *reinterpret_cast<const u32x4_t*>(ar + aoff3);
-      const i32x8_t ahi = {(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3],
-                           (int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
-      const i32x8_t alo = {(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3],
-                           (int)w3[0], (int)w3[1], (int)w3[2], (int)w3[3]};
-      const int sa = (int)sa_row[mb * 32 * sld + 2 * kt];
-      const int sl = sa > 4 ? sa - 4 : 0;  // lo's scale 2^max(X-4, -127)
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        acc[mb][nb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ahi, bop[nb], acc[mb][nb], 0, 4, 0,
-                                                                      sa, 0, sb[nb]);
-        acc[mb][nb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(alo, bop[nb], acc[mb][nb], 0, 4, 0,
-                                                                      sl, 0, sb[nb]);
-      }
+    if (kt + MX_NS - 1 < KT)
+      mx_issue<C, MX_NS>(smem, kt + MX_NS - 1, wave, lane, asrc, aoff_src, ssrc, a.ldq, a.ldas, bsrc, bkt);
+    if (nmb > 0) {
+      mx_read(f, smem + (kt % MX_NS) * C::STAGE, aoff0, aoff1, aoff2, aoff3, asoff, boff, sb_row, G, kt, nmb);
+      mx_mfma(acc, f, nmb);
     }
   }
 
@@ -1895,11 +1936,11 @@ struct Workspace {
   int* num_tiles;
   uint16_t* act;  // [P][I] bf16 gated activations
   float* y;       // [P][H] f32 down-projection output (before the routing weight)
-  uint8_t* hq;    // MX path: [T][2H] hi/lo E4M3 hidden (in y's bytes), [T][ldhs] scales
+  uint8_t* hq;    // MX path: split hidden rows per pair (in y's bytes) and scale bytes
   uint8_t* hs;
-  uint8_t* aq;    // MX path: [P][2I] hi/lo E4M3 activations (in act's bytes), [P][ldas] scales
+  uint8_t* aq;    // MX path: split activations (in act's bytes) and scale bytes
   uint8_t* as;
-  int64_t ldhs, ldas;
+  int64_t rows_mx;  // rows of the MX split buffers: P plus MX_BM spare
   int64_t bytes;
 };
 
@@ -1920,17 +1961,19 @@ static Workspace carve(void* base, int64_t T, int64_t H, int64_t I, int64_t E, i
   w.pair_pos = reinterpret_cast<int*>(take(P * 4));
   w.tiles = reinterpret_cast<int2*>(take(max_tiles * 8));
   w.num_tiles = reinterpret_cast<int*>(take(4));
-  w.act = reinterpret_cast<uint16_t*>(take(P * I * 2));
-  w.y = reinterpret_cast<float*>(take(P * H * 4));
-  w.ldhs = align_up(H / 32, 16);
-  w.ldas = align_up(I / 32, 16);
-  // MX path: the split hidden rows (T * 2H bytes) are dead once gate_up is
-  // done, before down writes y (P * 4H bytes) over them; the split
-  // activations (P * 2I bytes) take the place of the bf16 ones
+  // MX path: the split hidden rows (one per pair, in sorted order, with
+  // MX_BM spare rows after the last) are dead once gate_up is done, before
+  // down writes y over them; the split activations take the place of the
+  // bf16 ones.  Both are k-tile-major (SplitLayout); the scale bytes sit in
+  // their own 4-byte-per-row arrays.
+  const int64_t Pp = P + MX_BM;
+  w.act = reinterpret_cast<uint16_t*>(take(Pp * I * 2));
+  w.y = reinterpret_cast<float*>(take(std::max(P * H * 4, Pp * H * 2)));
   w.hq = reinterpret_cast<uint8_t*>(w.y);
-  w.hs = reinterpret_cast<uint8_t*>(take(T * w.ldhs));
+  w.hs = reinterpret_cast<uint8_t*>(take(Pp * (H / 64) * 4));
   w.aq = reinterpret_cast<uint8_t*>(w.act);
-  w.as = reinterpret_cast<uint8_t*>(take(P * w.ldas));
+  w.as = reinterpret_cast<uint8_t*>(take(Pp * (I / 64) * 4));
+  w.rows_mx = Pp;
   w.bytes = off;
   return w;
 }
@@ -1954,7 +1997,9 @@ static Workspace carve(void* base, int64_t T, int64_t H, int64_t I, int64_t E, i
 // v_perm: 16 conversions + 16 permutes feed 16 MFMAs (4 x 4 blocks of
 // v_mfma_f32_32x32x16_bf16), and the epilogue stores 4 contiguous columns.
 // Stage (NS of them, global_load_lds DMA only):
-//  * A [128][64] bf16, 16-byte chunk c of row r at chunk c ^ (r & 7);
+//  * A [128][64] bf16, 16-byte chunk c of row r at chunk c ^ ((r >> 1) & 7)
+//    (a ds_read_b128 pass serves 16 lanes from 64 banks: 256 bytes, two
+//    rows, so the swizzle pairs rows);
 //  * Q [64][256 B] packed weights, chunk c of row r at chunk c ^ (r & 15);
 //  * S: the 16 scale bytes of each weight row (blocks 16 nt .. 16 nt + 15,
 //    an unaligned run) as the two aligned 16-byte chunks that cover it;
@@ -1995,7 +2040,7 @@ struct BtSrc {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int r = 8 * (4 * wave + j) + (lane >> 3);
-      const int ch = (lane & 7) ^ (r & 7);
+      const int ch = (lane & 7) ^ ((r >> 1) & 7);
       asrc[j] = a.A + tile_src_row(a, m0, rows, r) * a.lda + ch * 8;
     }
     bq = a.Bq;
@@ -2152,7 +2197,7 @@ __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
   // --- fragment addresses (step s adds 4096 s to Q, 1024 s to S) -------------
   uint32_t aoff[4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) aoff[s] = (uint32_t)(c * 128 + (((2 * s + g) ^ (c & 7)) * 16));
+  for (int s = 0; s < 4; ++s) aoff[s] = (uint32_t)(c * 128 + (((2 * s + g) ^ ((c >> 1) & 7)) * 16));
   uint32_t qa[8], sa[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -2369,10 +2414,13 @@ static int launch_mx_cfg(const GemmArgs& a, int64_t P, size_t smem, hipStream_t 
 }
 
 // Block-scaled MX grouped GEMM (K % 64 == 0; 16-byte aligned blocks, 4-byte
-// aligned weight scales; a.Aq / a.As filled by launch_quant_mxfp8_split
-// with a 16-byte aligned scale buffer whose row stride is a multiple of 16).
+// aligned weight scales; a.Aq / a.As the k-tile-major split of the sorted
+// activation rows, with 128 spare rows after the last).
 // Pipeline depth BSA_MX_NS, a BSA_MX_WM x BSA_MX_WN wave grid with
-// BSA_MX_NB 32-column blocks per wave (a build-time choice).
+// BSA_MX_NB 32-column blocks per wave (a build-time choice; the defaults
+// measured fastest at the gpt-oss-120b prefill shapes: a third stage does not
+// fit two workgroups per CU, and 8-wave grids at one workgroup per CU ran
+// 7-10% slower).
 #ifndef BSA_MX_NS
 #define BSA_MX_NS 2
 #endif
@@ -2380,7 +2428,7 @@ static int launch_mx_cfg(const GemmArgs& a, int64_t P, size_t smem, hipStream_t 
 #define BSA_MX_WM 2
 #endif
 #ifndef BSA_MX_WN
-#define BSA_MX_WN 4
+#define BSA_MX_WN 2
 #endif
 #ifndef BSA_MX_NB
 #define BSA_MX_NB 4
@@ -2388,14 +2436,16 @@ static int launch_mx_cfg(const GemmArgs& a, int64_t P, size_t smem, hipStream_t 
 template <int EPI>
 static int launch_gemm_mx(const GemmArgs& a, int64_t P, hipStream_t st) {
   if (a.K % MX_BK != 0 || reinterpret_cast<uintptr_t>(a.Bq) % 16 != 0 ||
-      reinterpret_cast<uintptr_t>(a.Bs) % 4 != 0 || a.ldas % 16 != 0 || a.ldas < a.K / 32 ||
-      reinterpret_cast<uintptr_t>(a.As) % 16 != 0) {
+      reinterpret_cast<uintptr_t>(a.Bs) % 4 != 0 || a.ldas % 4 != 0 || a.ldq % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(a.Aq) % 16 != 0 || reinterpret_cast<uintptr_t>(a.As) % 4 != 0) {
     set_error("MX GEMM: needs K %% 64 == 0 (K=%d), 16-byte aligned blocks and 4-byte aligned scales",
               a.K);
     return BSA_EINVAL;
   }
   using C = MxCfg<BSA_MX_WM, BSA_MX_WN, BSA_MX_NB>;
-  const size_t smem = mx_smem_bytes(BSA_MX_NS, C::BN, a.K, a.ldas);
+  // the epilogue stages each wave's results in the (then idle) stages and
+  // B-scale buffer
+  const size_t smem = std::max(mx_smem_bytes(BSA_MX_NS, C::BN, a.K), (size_t)C::W * C::EPI_LDS);
   if (smem > 160 * 1024) {
     set_error("MX GEMM: K=%d needs %zu bytes of LDS", a.K, smem);
     return BSA_EINVAL;
@@ -2525,10 +2575,15 @@ struct MoeShape {
 // them: their gate_up stage leaves the split activations, not bf16 ones, for
 // the down stage, so the choice is made once, from both weights' alignment.
 // (The single-stage entry points see one projection only; for them automatic
-// selection stays on paths 1-2.)
+// selection stays on paths 1-2.)  A forward that saves its gate_up
+// pre-activations for the backward keeps the bf16 products: the block-scaled
+// instruction's accumulation puts ten times as many pre-activations on the
+// other side of the SwiGLU clamps from float32 (measured at the gpt-oss-120b
+// prefill shape: 246 against 26 of 189M), and each such flip moves a token's
+// input gradient by the size of its largest entries.
 static int resolve_path(int path, const MoeShape& m, const void* gu_b, const void* gu_s, const void* dn_b,
-                        const void* dn_s) {
-  if (path != PATH_AUTO) return path;
+                        const void* dn_s, bool saving) {
+  if (path != PATH_AUTO || saving) return path;
   const bool a16 = reinterpret_cast<uintptr_t>(gu_b) % 16 == 0 && reinterpret_cast<uintptr_t>(dn_b) % 16 == 0;
   const bool s4 = reinterpret_cast<uintptr_t>(gu_s) % 4 == 0 && reinterpret_cast<uintptr_t>(dn_s) % 4 == 0;
   const int64_t P = m.T * m.k;
@@ -2614,17 +2669,22 @@ static int stage_gate_up(const MoeShape& m, const void* hidden, const void* bloc
                 (long long)m.H, (long long)m.I);
       return BSA_EINVAL;
     }
-    int rc = launch_quant_mxfp8_split(hidden, DT_BF16, m.T, m.H, m.H, w.hq, 2 * m.H, w.hs, w.ldhs, st);
+    // every pair's hidden row split once, in sorted order and k-tile-major,
+    // so a tile's rows of one k-tile are one contiguous run
+    const SplitLayout hl{128, w.rows_mx * 128, 4, w.rows_mx * 4};
+    int rc = launch_quant_mxfp8_split(hidden, DT_BF16, P, m.H, m.H, w.row_pair, (int)m.k, w.hq, w.hs, hl, st);
     if (rc) return rc;
     g.Aq = w.hq;
-    g.ldq = 2 * m.H;
+    g.ldq = hl.q_kt;
     g.As = w.hs;
-    g.ldas = w.ldhs;
+    g.ldas = hl.s_kt;
     // the epilogue splits the activations for the down GEMM itself
     g.out = w.aq;
-    g.ldo = 2 * m.I;
+    g.ldo = 128;
+    g.out_kt = w.rows_mx * 128;
     g.out_s = w.as;
-    g.ldos = w.ldas;
+    g.ldos = 4;
+    g.out_s_kt = w.rows_mx * 4;
     return launch_gemm_mx<EPI_SWIGLU_MX>(g, P, st);
   }
   return launch_gemm<EPI_SWIGLU>(g, chosen, P, st);
@@ -2661,9 +2721,9 @@ static int stage_down(const MoeShape& m, const void* blocks, const void* scales,
       return BSA_EINVAL;
     }
     g.Aq = w.aq;  // written by the gate_up epilogue
-    g.ldq = 2 * m.I;
+    g.ldq = w.rows_mx * 128;
     g.As = w.as;
-    g.ldas = w.ldas;
+    g.ldas = w.rows_mx * 4;
     return launch_gemm_mx<EPI_BIAS_F32>(g, P, st);
   }
   return launch_gemm<EPI_BIAS_F32>(g, chosen, P, st);
@@ -2816,7 +2876,7 @@ static int experts_fwd(
       (rc = check_layout(blocks_layout, down_blocks, H, I, "experts fwd (down)")))
     return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  path = resolve_path(path, m, gate_up_blocks, gate_up_scales, down_blocks, down_scales);
+  path = resolve_path(path, m, gate_up_blocks, gate_up_scales, down_blocks, down_scales, save_gate_up != nullptr);
   if (noalloc) {
     workspace_bytes = carve(nullptr, T, H, I, E, k).bytes;
     BSA_REQUIRE(workspace_bytes <= NOALLOC_SCRATCH_BYTES,

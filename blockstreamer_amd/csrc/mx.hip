@@ -93,23 +93,25 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(const void* __restrict__ 
 // bfloat16 element keeps 8 significant bits, its residual at most 4, so
 // hi * 2^X + lo * 2^Xl equals x exactly for every element above about 2^-14
 // of the block maximum (E4M3 keeps 4 bits down to 2^-6).  The residual is
-// exact in float32 (x minus x rounded to 4 bits).
-// Output row layout, per 64-element k-tile t: bytes 128t .. 128t+63 the hi
-// codes of k = 64t .. 64t+63, then 64 bytes of lo codes; the scale bytes are
-// those of X (lo's is derived: max(byte - 4, 0)).  Blocks with an inf or NaN
+// exact in float32 (x minus x rounded to 4 bits).  Blocks with an inf or NaN
 // get scale byte 255, hi codes 0x7F (NaN, sign kept) and lo codes 0.
+// Output: the codes of 64-element k-tile t of row r at q + r * L.q_row +
+// t * L.q_kt, 64 hi bytes then 64 lo bytes; block g's scale byte (that of X;
+// lo's is max(byte - 4, 0)) at s + r * L.s_row + (g / 2) * L.s_kt + g % 2.
+// Row r reads input row row_map[r] / topk when row_map is given.
 template <int IN>
 __global__ __launch_bounds__(256) void mx_split_kernel(const void* __restrict__ x, int64_t ldx,
-                                                       int64_t nblk, int G, uint8_t* __restrict__ q,
-                                                       int64_t ldq, uint8_t* __restrict__ s,
-                                                       int64_t lds) {
+                                                       const int* __restrict__ row_map, int topk, int64_t nblk,
+                                                       int G, uint8_t* __restrict__ q, uint8_t* __restrict__ s,
+                                                       SplitLayout L) {
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const bool ok = (gid >> 2) < nblk;
   const int64_t blk = ok ? (gid >> 2) : nblk - 1;
   const int part = threadIdx.x & 3;
   const int64_t r = blk / G;
   const int g = (int)(blk - r * G);
-  const int64_t off = r * ldx + g * 32 + part * 8;
+  const int64_t src = row_map ? (int64_t)(row_map[r] / topk) : r;
+  const int64_t off = src * ldx + g * 32 + part * 8;
   float v[8];
   if constexpr (IN == DT_BF16) {
     const u32x4_t w = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + off);
@@ -130,10 +132,10 @@ __global__ __launch_bounds__(256) void mx_split_kernel(const void* __restrict__ 
   uint32_t h[2], l[2];
   const uint32_t sbyte = mx_split8(v, h, l);
   if (ok) {
-    uint8_t* row = q + r * ldq + (g >> 1) * 128 + (g & 1) * 32 + part * 8;
+    uint8_t* row = q + r * L.q_row + (g >> 1) * L.q_kt + (g & 1) * 32 + part * 8;
     *reinterpret_cast<uint2*>(row) = make_uint2(h[0], h[1]);
     *reinterpret_cast<uint2*>(row + 64) = make_uint2(l[0], l[1]);
-    if (part == 0) s[r * lds + g] = (uint8_t)sbyte;
+    if (part == 0) s[r * L.s_row + (g >> 1) * L.s_kt + (g & 1)] = (uint8_t)sbyte;
   }
 }
 
@@ -162,11 +164,10 @@ int launch_quant_mxfp8(const void* x, int in_dtype, int64_t R, int64_t K, int64_
   return BSA_OK;
 }
 
-// Two-term split of R rows of K (K % 64 == 0) elements into q [R][ldq]
-// (ldq >= 2K: hi and lo codes interleaved per 64-element k-tile) and scale
-// bytes s [R][lds].
-int launch_quant_mxfp8_split(const void* x, int in_dtype, int64_t R, int64_t K, int64_t ldx, uint8_t* q,
-                             int64_t ldq, uint8_t* s, int64_t lds, hipStream_t st) {
+// Two-term split of R rows of K (K % 64 == 0) elements (input row stride
+// ldx; row r reads row_map[r] / topk when row_map is given) into the layout L.
+int launch_quant_mxfp8_split(const void* x, int in_dtype, int64_t R, int64_t K, int64_t ldx, const int* row_map,
+                             int topk, uint8_t* q, uint8_t* s, SplitLayout L, hipStream_t st) {
   if (R == 0) return BSA_OK;
   const int G = (int)(K / 32);
   const int64_t nblk = R * G;
@@ -176,14 +177,14 @@ int launch_quant_mxfp8_split(const void* x, int in_dtype, int64_t R, int64_t K, 
     return BSA_EINVAL;
   }
   if (in_dtype == DT_BF16)
-    hipLaunchKernelGGL(mx_split_kernel<DT_BF16>, dim3((unsigned)grid), dim3(256), 0, st, x, ldx, nblk, G, q,
-                       ldq, s, lds);
+    hipLaunchKernelGGL(mx_split_kernel<DT_BF16>, dim3((unsigned)grid), dim3(256), 0, st, x, ldx, row_map, topk,
+                       nblk, G, q, s, L);
   else if (in_dtype == DT_F32)
-    hipLaunchKernelGGL(mx_split_kernel<DT_F32>, dim3((unsigned)grid), dim3(256), 0, st, x, ldx, nblk, G, q,
-                       ldq, s, lds);
+    hipLaunchKernelGGL(mx_split_kernel<DT_F32>, dim3((unsigned)grid), dim3(256), 0, st, x, ldx, row_map, topk,
+                       nblk, G, q, s, L);
   else
-    hipLaunchKernelGGL(mx_split_kernel<DT_F16>, dim3((unsigned)grid), dim3(256), 0, st, x, ldx, nblk, G, q,
-                       ldq, s, lds);
+    hipLaunchKernelGGL(mx_split_kernel<DT_F16>, dim3((unsigned)grid), dim3(256), 0, st, x, ldx, row_map, topk,
+                       nblk, G, q, s, L);
   BSA_LAUNCH_CHECK("mxfp8 split launch");
   return BSA_OK;
 }
@@ -202,8 +203,10 @@ extern "C" int bsa_quant_mxfp8_split(const void* x, int dtype, int64_t R, int64_
   BSA_REQUIRE(x && q && scales, "mxfp8 split: null pointer");
   BSA_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(q) % 8 == 0,
               "mxfp8 split: x must be 16-byte and q 8-byte aligned");
-  return launch_quant_mxfp8_split(x, dtype, R, K, K, static_cast<uint8_t*>(q), 2 * K,
-                                  static_cast<uint8_t*>(scales), scale_ld, static_cast<hipStream_t>(stream));
+  // row-major: row r's k-tiles one after another, its scale bytes in order
+  const SplitLayout L{2 * K, 128, scale_ld, 2};
+  return launch_quant_mxfp8_split(x, dtype, R, K, K, nullptr, 1, static_cast<uint8_t*>(q),
+                                  static_cast<uint8_t*>(scales), L, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int bsa_quant_mxfp8(const void* x, int dtype, int64_t R, int64_t K, void* q, void* scales,

@@ -340,7 +340,8 @@ def _whole_forward_path(path: str, T: int, k: int, E: int, H: int, I: int, gu_b:
     batches (more than 16 rows per expert on average) when both projections
     can run them -- H and I multiples of 64, 16-byte aligned blocks, 4-byte
     aligned scales -- because its gate_up stage leaves split activations for
-    its down stage."""
+    its down stage.  (A forward saving for the backward keeps the bf16
+    products; the stage runner never saves.)"""
     if path != "auto":
         return PATHS[path]
     ok = (T * k > 16 * E and H % 64 == 0 and I % 64 == 0 and gu_b.data_ptr() % 16 == 0

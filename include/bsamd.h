@@ -152,9 +152,9 @@ int bsa_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
  *   save_gate_up    optional float32 [T*k, 2I]: gate_up pre-activations in
  *                   expert-sorted row order, for the backward
  *   path            0 = automatic (path 3 when more than 16 rows per expert
- *                   on average and both projections can take it, else 1 up to
- *                   16 rows per expert and 2 beyond), 1 = weight-streaming
- *                   kernel, 2 = tiled kernel,
+ *                   on average, both projections can take it and
+ *                   save_gate_up is NULL, else 1 up to 16 rows per expert and
+ *                   2 beyond), 1 = weight-streaming kernel, 2 = tiled kernel,
  *                   3 = native block-scaled MX kernel (activations split into
  *                   two MXFP8 terms by bsa_quant_mxfp8_split's rule, then two
  *                   v_mfma_scale_f32_32x32x64_f8f6f4 per 64-element k-step on
@@ -193,7 +193,7 @@ int bsa_moe_experts_fwd(
  * harnesses that forbid allocation.
  *
  * Limit: the shape's bsa_moe_workspace_bytes must be at most
- * BSA_NOALLOC_SCRATCH_BYTES (16 MiB: up to 240 tokens at top-4 with
+ * BSA_NOALLOC_SCRATCH_BYTES (16 MiB: up to 226 tokens at top-4 with
  * H = I = 2880, i.e. decode batches); larger shapes return BSA_EINVAL.
  * Every call on one GPU shares that GPU's array, so calls that overlap on a
  * GPU (concurrent streams, threads) race; order them.  The array's contents

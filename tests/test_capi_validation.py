@@ -190,10 +190,10 @@ def test_workspace_sizes_grow_with_tokens():
 
 
 def test_noalloc_scratch_covers_decode_batches():
-    """The static scratch holds the 120b layer's workspace up to 240 tokens
-    (the decode batches), not 241."""
+    """The static scratch holds the 120b layer's workspace up to 226 tokens
+    (the decode batches), not 227."""
     dims = {k: v for k, v in GPTOSS.items() if k != "T"}
-    assert _ws_bytes(240, **dims) <= 16 << 20 < _ws_bytes(241, **dims)
+    assert _ws_bytes(226, **dims) <= 16 << 20 < _ws_bytes(227, **dims)
 
 
 def test_python_call_raises_value_error_with_the_message():
