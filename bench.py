@@ -272,8 +272,8 @@ def bench_moe(wl: Workload, T: int, steps: int, warmup: int, path: str = "auto",
               train: bool = False, fwd: bool = True, ref: bool = False) -> dict:
     """One MoE layer (router + dispatch + expert GEMMs + combine) of
     ``wl`` at T tokens.  ``train``: also the LoRA training use, a
-    forward saving the gate_up pre-activations followed by the input-gradient
-    backward.  ``fwd=False``: only that (the profile of the training run).
+    forward saving the SwiGLU's derivative factors followed by the
+    input-gradient backward.  ``fwd=False``: only that (the profile of the training run).
     ``ref``: also the output's relative L2 distance to a float32 reference."""
     from blockstreamer_amd import kernels
 
@@ -370,8 +370,8 @@ def bench_moe(wl: Workload, T: int, steps: int, warmup: int, path: str = "auto",
             got = kernels.moe_experts_forward(x, idx, w, *args, path=path).float()
             res["rel_l2_vs_fp32"] = round(((got - want).norm() / want.norm()).item(), 6)
     if train:
-        # the LoRA training use: forward saving the gate_up pre-activations,
-        # then the input-gradient backward (expert weights frozen)
+        # the LoRA training use: forward saving the SwiGLU's derivative
+        # factors, then the input-gradient backward (expert weights frozen)
         idx, w = route()
         g = (torch.randn(T, H, generator=torch.Generator().manual_seed(7)) * 0.1).to(torch.bfloat16).to(dev)
 

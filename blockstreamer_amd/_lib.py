@@ -15,7 +15,7 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "libbsamd.so"
 
 BSA_OK, BSA_EINVAL, BSA_EHIP = 0, 1, 2
-ABI_MAJOR = 2  # BSA_VERSION_MAJOR of include/bsamd.h: the signatures declared below
+ABI_MAJOR = 3  # BSA_VERSION_MAJOR of include/bsamd.h: the signatures declared below
 DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 _i64 = ctypes.c_int64

@@ -71,8 +71,8 @@ enum Epi : int {
   EPI_SWIGLU = 0,    // out bf16 [P][N/2] = swiglu(acc + bias), optional f32 pre-activation save
   EPI_BIAS_F32 = 1,  // out f32 [P][N] = acc + bias
   EPI_STORE = 2,     // out (out_dtype) [P][N] = acc (+ bias if given)
-  EPI_SWIGLU_BWD = 3,  // out bf16 [P][2N] = d(gate_up) from acc = d(act) and the saved
-                       // f32 pre-activations in save_pre [P][2N]
+  EPI_SWIGLU_BWD = 3,  // out bf16 [P][2N] = d(gate_up) from acc = d(act) and the forward's
+                       // saved derivative factors save_grad [P][N] (bf16 pairs)
   EPI_SWIGLU_MX = 4,   // as EPI_SWIGLU, the bf16 activations then split into two MXFP8
                        // terms, stored in the SplitLayout {ldo, out_kt, ldos, out_s_kt}
                        // (codes at out, scale bytes at out_s)
@@ -93,7 +93,8 @@ struct GemmArgs {
   void* out;
   int64_t ldo;
   int out_dtype;
-  float* save_pre;       // EPI_SWIGLU: optional f32 [P][N] pre-activation (incl. bias)
+  uint32_t* save_grad;   // EPI_SWIGLU: optional [P][N/2] bf16 pairs, the SwiGLU's derivative
+                         // factors (swiglu_fwd_grad); EPI_SWIGLU_BWD reads them [P][N]
   float alpha, limit;
   const int2* tiles;     // tiled kernel: (expert, first sorted row) per row tile
   const int* num_tiles;
@@ -156,19 +157,29 @@ __device__ __forceinline__ float swiglu(float g, float u, float alpha, float lim
   return (u + 1.0f) * (g * sig);
 }
 
-// Backward of swiglu() w.r.t. the raw gate and up pre-activations, as torch
-// autograd differentiates gptoss.py:130-135: clamp(max=limit) passes the
-// gradient where g <= limit, clamp(-limit, limit) where -limit <= u <= limit,
-// and d(x * sigmoid(a x))/dx = s + a x s (1 - s).
-__device__ __forceinline__ void swiglu_bwd(float g, float u, float dout, float alpha, float limit,
-                                           float* dg, float* du) {
+// swiglu() and, for the backward, its partial derivatives w.r.t. the raw
+// gate and up pre-activations as torch autograd differentiates
+// gptoss.py:130-135: clamp(max=limit) passes the gradient where g <= limit,
+// clamp(-limit, limit) where -limit <= u <= limit, and
+// d(x * sigmoid(a x))/dx = s + a x s (1 - s).  The factors are returned as
+// one bf16 pair (d act/d gate low, d act/d up high): the backward's
+// d(gate, up) = d(act) * factors, with the clamp decisions taken here on
+// the float32 pre-activations.
+__device__ __forceinline__ float swiglu_fwd_grad(float g, float u, float alpha, float limit,
+                                                 uint32_t* factors) {
   const float gc = fminf(g, limit);
   const float uc = fminf(fmaxf(u, -limit), limit);
   const float sg = 1.0f / (1.0f + __expf(-alpha * gc));
   const float glu = gc * sg;
-  *du = (u >= -limit && u <= limit) ? dout * glu : 0.0f;
-  const float dglu = dout * (uc + 1.0f);
-  *dg = (g <= limit) ? dglu * (sg + alpha * gc * sg * (1.0f - sg)) : 0.0f;
+  const float fu = (u >= -limit && u <= limit) ? glu : 0.0f;
+  const float fg = (g <= limit) ? (uc + 1.0f) * (sg + alpha * gc * sg * (1.0f - sg)) : 0.0f;
+  *factors = pack_bf16x2(fg, fu);
+  return (uc + 1.0f) * glu;
+}
+
+// d(gate, up) as one bf16 pair from d(act) and the saved factors.
+__device__ __forceinline__ uint32_t swiglu_bwd(uint32_t factors, float dout) {
+  return pack_bf16x2(dout * __uint_as_float(factors << 16), dout * __uint_as_float(factors & 0xFFFF0000u));
 }
 
 __device__ __forceinline__ void store_out(void* out, int dtype, int64_t i, float v) {
@@ -203,12 +214,15 @@ __device__ __forceinline__ void epilogue_swiglu(const GemmArgs& a, int64_t pos, 
                                                 float accg, float accu, float bg, float bu) {
   const float g = accg + bg;
   const float u = accu + bu;
-  if (a.save_pre) {
-    float2* sp = reinterpret_cast<float2*>(a.save_pre + pos * a.N + n_gate);
-    *sp = make_float2(g, u);
+  float act;
+  if (a.save_grad) {
+    uint32_t f;
+    act = swiglu_fwd_grad(g, u, a.alpha, a.limit, &f);
+    a.save_grad[pos * (a.N >> 1) + (n_gate >> 1)] = f;
+  } else {
+    act = swiglu(g, u, a.alpha, a.limit);
   }
-  static_cast<uint16_t*>(a.out)[pos * a.ldo + (n_gate >> 1)] =
-      (uint16_t)f32_to_bf16_bits(swiglu(g, u, a.alpha, a.limit));
+  static_cast<uint16_t*>(a.out)[pos * a.ldo + (n_gate >> 1)] = (uint16_t)f32_to_bf16_bits(act);
 }
 
 template <int EPI>
@@ -218,11 +232,8 @@ __device__ __forceinline__ void epilogue_one(const GemmArgs& a, int64_t pos, int
   if constexpr (EPI == EPI_BIAS_F32) {
     static_cast<float*>(a.out)[pos * a.ldo + n] = v;
   } else if constexpr (EPI == EPI_SWIGLU_BWD) {
-    const float2 pre = *reinterpret_cast<const float2*>(a.save_pre + pos * (2 * (int64_t)a.N) + 2 * n);
-    float dg, du;
-    swiglu_bwd(pre.x, pre.y, v, a.alpha, a.limit, &dg, &du);
     *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.out) + pos * a.ldo + 2 * n) =
-        pack_bf16x2(dg, du);
+        swiglu_bwd(a.save_grad[pos * a.N + n], v);
   } else {
     store_out(a.out, a.out_dtype, pos * a.ldo + n, v);
   }
@@ -237,8 +248,8 @@ __device__ __forceinline__ void epilogue_one(const GemmArgs& a, int64_t pos, int
 //  * EPI_SWIGLU: lanes 2j (gate) and 2j+1 (up) hold the same rows; the even
 //    lane finishes rows v < 8 and the odd lane rows v >= 8, trading halves
 //    with one shuffle; the bf16 activations of 32*MB rows x 16*NBW columns
-//    go to LDS, then out to act[m0 + r][n0w/2 ..] (optional float32
-//    pre-activation pairs are stored directly);
+//    go to LDS, then out to act[m0 + r][n0w/2 ..] (the optional saved
+//    derivative factors, one bf16 pair per activation, are stored directly);
 //  * EPI_BIAS_F32: 32 rows x 32*CB float32 at a time (CB = min(NBW, 2)).
 // Needs 16-byte aligned output rows (ldo * element size % 16 == 0).
 __host__ __device__ constexpr int epi_lds_bytes(int MB, int NBW) {
@@ -270,9 +281,15 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& a, const f32x16_
           const float u = odd ? hi : recv;
           const int vv = odd ? v + 8 : v;
           const int r = mb * 32 + 8 * (vv >> 2) + 4 * lh + (vv & 3);
-          if (a.save_pre && r0w + r < rows && ng + 1 < a.N)
-            *reinterpret_cast<float2*>(a.save_pre + (int64_t)(m0 + r0w + r) * a.N + ng) = make_float2(g, u);
-          t[r * AC + nb * 16 + (l32 >> 1)] = (uint16_t)f32_to_bf16_bits(swiglu(g, u, a.alpha, a.limit));
+          float act;
+          if (a.save_grad) {
+            uint32_t f;
+            act = swiglu_fwd_grad(g, u, a.alpha, a.limit, &f);
+            if (r0w + r < rows && ng + 1 < a.N) a.save_grad[(int64_t)(m0 + r0w + r) * (a.N >> 1) + (ng >> 1)] = f;
+          } else {
+            act = swiglu(g, u, a.alpha, a.limit);
+          }
+          t[r * AC + nb * 16 + (l32 >> 1)] = (uint16_t)f32_to_bf16_bits(act);
         }
       }
     }
@@ -2146,22 +2163,15 @@ __device__ __forceinline__ void bt_decode(const uint32_t (&raw)[8], const uint32
   }
 }
 
-// Four adjacent output columns n .. n+3 of row pos; pre holds the row's saved
-// (gate, up) pairs of those columns (EPI_SWIGLU_BWD).
+// Four adjacent output columns n .. n+3 of row pos; fac holds the row's saved
+// derivative factors of those columns (EPI_SWIGLU_BWD).
 template <int EPI>
 __device__ __forceinline__ void bt_store4(const GemmArgs& a, int64_t pos, int n, const float (&v)[4],
-                                          const f32x4_t (&pre)[2]) {
+                                          const u32x4_t& fac) {
   if constexpr (EPI == EPI_SWIGLU_BWD) {
-    const f32x4_t p0 = pre[0], p1 = pre[1];
-    const float g[4] = {p0[0], p0[2], p1[0], p1[2]};
-    const float u[4] = {p0[1], p0[3], p1[1], p1[3]};
     u32x4_t o;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float dg, du;
-      swiglu_bwd(g[j], u[j], v[j], a.alpha, a.limit, &dg, &du);
-      o[j] = pack_bf16x2(dg, du);
-    }
+    for (int j = 0; j < 4; ++j) o[j] = swiglu_bwd(fac[j], v[j]);
     *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(a.out) + pos * a.ldo + 2 * n) = o;
   } else {
     static_assert(EPI == EPI_STORE, "packed-weight backward epilogue");
@@ -2292,17 +2302,14 @@ __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
   if (n >= a.N) return;
 #pragma clang loop unroll(full)
   for (int mb = 0; mb < 4; ++mb) {
-    // one 32-row block at a time: its 16 rows' saved pre-activations are
+    // one 32-row block at a time: its 16 rows' saved derivative factors are
     // loaded together (the row loop would otherwise wait on each in turn)
-    f32x4_t pre[16][2];
+    u32x4_t fac[16];
     if constexpr (EPI == EPI_SWIGLU_BWD) {
 #pragma clang loop unroll(full)
       for (int v = 0; v < 16; ++v) {
         const int r = 32 * mb + 8 * (v >> 2) + 4 * g + (v & 3);
-        const f32x4_t* sp =
-            reinterpret_cast<const f32x4_t*>(a.save_pre + (int64_t)(m0 + min(r, rows - 1)) * (2 * (int64_t)a.N) + 2 * n);
-        pre[v][0] = sp[0];
-        pre[v][1] = sp[1];
+        fac[v] = *reinterpret_cast<const u32x4_t*>(a.save_grad + (int64_t)(m0 + min(r, rows - 1)) * a.N + n);
       }
     }
 #pragma clang loop unroll(full)
@@ -2310,7 +2317,7 @@ __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
       const int r = 32 * mb + 8 * (v >> 2) + 4 * g + (v & 3);
       if (r < rows) {
         const float o[4] = {acc[mb][0][v], acc[mb][1][v], acc[mb][2][v], acc[mb][3][v]};
-        bt_store4<EPI>(a, m0 + r, n, o, pre[v]);
+        bt_store4<EPI>(a, m0 + r, n, o, fac[v]);
       }
     }
   }
@@ -2635,7 +2642,10 @@ static int check_layout(int layout, const void* blocks, int64_t rows, int64_t K,
 
 static int stage_gate_up(const MoeShape& m, const void* hidden, const void* blocks, const void* scales,
                          const void* bias, int bias_dtype, float alpha, float limit, const Workspace& w,
-                         void* save_gate_up, int path, int layout, hipStream_t st) {
+                         void* save_swiglu_grad, int path, int layout, hipStream_t st) {
+  // the backward reads each row's factors in 16-byte pieces
+  BSA_REQUIRE(reinterpret_cast<uintptr_t>(save_swiglu_grad) % 16 == 0,
+              "gate_up: save_swiglu_grad must be 16-byte aligned");
   GemmArgs g{};
   g.kp = layout == BSA_LAYOUT_KPAIR;
   g.A = static_cast<const uint16_t*>(hidden);
@@ -2654,7 +2664,7 @@ static int stage_gate_up(const MoeShape& m, const void* hidden, const void* bloc
   g.out = w.act;
   g.ldo = m.I;
   g.out_dtype = DT_BF16;
-  g.save_pre = static_cast<float*>(save_gate_up);
+  g.save_grad = static_cast<uint32_t*>(save_swiglu_grad);
   g.alpha = alpha;
   g.limit = limit;
   g.tiles = w.tiles;
@@ -2749,7 +2759,7 @@ extern "C" int bsa_moe_dispatch(const int64_t* router_indices, int64_t T, int64_
 extern "C" int bsa_moe_gate_up(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E,
                                int64_t k, const void* blocks, const void* scales, const void* bias,
                                int bias_dtype, float alpha, float limit, void* workspace,
-                               int64_t workspace_bytes, void* save_gate_up, int path, int blocks_layout,
+                               int64_t workspace_bytes, void* save_swiglu_grad, int path, int blocks_layout,
                                void* stream) {
   clear_error();
   const MoeShape m{T, H, I, E, k};
@@ -2762,7 +2772,7 @@ extern "C" int bsa_moe_gate_up(const void* hidden, int64_t T, int64_t H, int64_t
   if ((rc = check_layout(blocks_layout, blocks, 2 * I, H, "gate_up"))) return rc;
   Workspace w;
   if ((rc = check_ws(m, workspace, workspace_bytes, &w, "gate_up"))) return rc;
-  return stage_gate_up(m, hidden, blocks, scales, bias, bias_dtype, alpha, limit, w, save_gate_up,
+  return stage_gate_up(m, hidden, blocks, scales, bias, bias_dtype, alpha, limit, w, save_swiglu_grad,
                        path, blocks_layout, static_cast<hipStream_t>(stream));
 }
 
@@ -2858,7 +2868,7 @@ static int experts_fwd(
     const void* gate_up_blocks, const void* gate_up_scales, const void* gate_up_bias,
     const void* down_blocks, const void* down_scales, const void* down_bias, int bias_dtype,
     float alpha, float limit, void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
-    void* save_gate_up, int path, int blocks_layout, void* stream) {
+    void* save_swiglu_grad, int path, int blocks_layout, void* stream) {
   const MoeShape m{T, H, I, E, k};
   int rc = check_shape(m, what);
   if (rc || T == 0) return rc;
@@ -2876,7 +2886,7 @@ static int experts_fwd(
       (rc = check_layout(blocks_layout, down_blocks, H, I, "experts fwd (down)")))
     return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  path = resolve_path(path, m, gate_up_blocks, gate_up_scales, down_blocks, down_scales, save_gate_up != nullptr);
+  path = resolve_path(path, m, gate_up_blocks, gate_up_scales, down_blocks, down_scales, save_swiglu_grad != nullptr);
   if (noalloc) {
     workspace_bytes = carve(nullptr, T, H, I, E, k).bytes;
     BSA_REQUIRE(workspace_bytes <= NOALLOC_SCRATCH_BYTES,
@@ -2889,7 +2899,7 @@ static int experts_fwd(
   if ((rc = check_ws(m, workspace, workspace_bytes, &w, what))) return rc;
   if ((rc = stage_dispatch(m, router_indices, w, st))) return rc;
   if ((rc = stage_gate_up(m, hidden, gate_up_blocks, gate_up_scales, gate_up_bias, bias_dtype, alpha,
-                          limit, w, save_gate_up, path, blocks_layout, st)))
+                          limit, w, save_swiglu_grad, path, blocks_layout, st)))
     return rc;
   if ((rc = stage_down(m, down_blocks, down_scales, down_bias, bias_dtype, w, path, blocks_layout, st)))
     return rc;
@@ -2905,11 +2915,11 @@ extern "C" int bsa_moe_experts_fwd(
     const void* gate_up_blocks, const void* gate_up_scales, const void* gate_up_bias,
     const void* down_blocks, const void* down_scales, const void* down_bias, int bias_dtype,
     float alpha, float limit, void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
-    void* save_gate_up, int path, int blocks_layout, void* stream) {
+    void* save_swiglu_grad, int path, int blocks_layout, void* stream) {
   clear_error();
   return experts_fwd("experts fwd", false, hidden, T, H, I, E, k, router_indices, routing_weights, weight_dtype,
                      gate_up_blocks, gate_up_scales, gate_up_bias, down_blocks, down_scales, down_bias,
-                     bias_dtype, alpha, limit, out, out_dtype, workspace, workspace_bytes, save_gate_up,
+                     bias_dtype, alpha, limit, out, out_dtype, workspace, workspace_bytes, save_swiglu_grad,
                      path, blocks_layout, stream);
 }
 
@@ -2918,12 +2928,12 @@ extern "C" int bsa_moe_experts_fwd_noalloc(
     const int64_t* router_indices, const void* routing_weights, int weight_dtype,
     const void* gate_up_blocks, const void* gate_up_scales, const void* gate_up_bias,
     const void* down_blocks, const void* down_scales, const void* down_bias, int bias_dtype,
-    float alpha, float limit, void* out, int out_dtype, void* save_gate_up, int path,
+    float alpha, float limit, void* out, int out_dtype, void* save_swiglu_grad, int path,
     int blocks_layout, void* stream) {
   clear_error();
   return experts_fwd("experts fwd (no-alloc)", true, hidden, T, H, I, E, k, router_indices, routing_weights,
                      weight_dtype, gate_up_blocks, gate_up_scales, gate_up_bias, down_blocks, down_scales,
-                     down_bias, bias_dtype, alpha, limit, out, out_dtype, nullptr, 0, save_gate_up, path,
+                     down_bias, bias_dtype, alpha, limit, out, out_dtype, nullptr, 0, save_swiglu_grad, path,
                      blocks_layout, stream);
 }
 
@@ -2971,7 +2981,7 @@ extern "C" int bsa_moe_experts_bwd(
     const int64_t* router_indices, const void* routing_weights, int weight_dtype,
     const void* gate_up_blocks, const void* gate_up_scales, const void* down_blocks,
     const void* down_scales, float alpha, float limit, void* workspace, int64_t workspace_bytes,
-    const void* save_gate_up, void* bwd_workspace, int64_t bwd_workspace_bytes, void* grad_hidden,
+    const void* save_swiglu_grad, void* bwd_workspace, int64_t bwd_workspace_bytes, void* grad_hidden,
     int grad_hidden_dtype, float* grad_weights, int blocks_layout, void* stream) {
   clear_error();
   const MoeShape m{T, H, I, E, k};
@@ -2981,7 +2991,7 @@ extern "C" int bsa_moe_experts_bwd(
               "experts bwd: bad dtype code");
   BSA_REQUIRE(H % 64 == 0 && I % 32 == 0, "experts bwd: needs hidden % 64 == 0 and intermediate % 32 == 0");
   BSA_REQUIRE(grad_out && router_indices && routing_weights && gate_up_blocks && gate_up_scales &&
-                  down_blocks && down_scales && save_gate_up && bwd_workspace,
+                  down_blocks && down_scales && save_swiglu_grad && bwd_workspace,
               "experts bwd: null pointer");
   Workspace w;
   if ((rc = check_ws(m, workspace, workspace_bytes, &w, "experts bwd"))) return rc;
@@ -2993,7 +3003,7 @@ extern "C" int bsa_moe_experts_bwd(
   auto al = [](const void* q, int n) { return reinterpret_cast<uintptr_t>(q) % n == 0; };
   BSA_REQUIRE(al(gate_up_blocks, 4) && al(gate_up_scales, 4) && al(down_blocks, 4) && al(down_scales, 4),
               "experts bwd: gate_up/down blocks and scales must be 4-byte aligned");
-  BSA_REQUIRE(al(save_gate_up, 16), "experts bwd: save_gate_up must be 16-byte aligned");
+  BSA_REQUIRE(al(save_swiglu_grad, 16), "experts bwd: save_swiglu_grad must be 16-byte aligned");
   if ((rc = check_layout(blocks_layout, gate_up_blocks, 2 * I, H, "experts bwd (gate_up)")) ||
       (rc = check_layout(blocks_layout, down_blocks, H, I, "experts bwd (down)")))
     return rc;
@@ -3017,7 +3027,7 @@ extern "C" int bsa_moe_experts_bwd(
   g.K = (int)H;
   g.out = b.dgu;
   g.ldo = 2 * I;
-  g.save_pre = const_cast<float*>(static_cast<const float*>(save_gate_up));
+  g.save_grad = const_cast<uint32_t*>(static_cast<const uint32_t*>(save_swiglu_grad));
   g.alpha = alpha;
   g.limit = limit;
   g.tiles = w.tiles;

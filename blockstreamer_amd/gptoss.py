@@ -94,7 +94,8 @@ class _MoEExperts(torch.autograd.Function):
     """Fused expert forward; backward gives d(hidden) and d(routing weights).
 
     Saves the packed weights (already resident as the block's staged state),
-    the inputs, the device-side dispatch and the gate_up pre-activations --
+    the inputs, the device-side dispatch and the SwiGLU's bf16 derivative
+    factors (the size of the bf16 gate_up the reference's autograd keeps) --
     never a dense weight (the rationale of block_streamer/gptoss.py:46-56).
     """
 
@@ -103,11 +104,11 @@ class _MoEExperts(torch.autograd.Function):
                 dn_blocks, dn_scales, dn_bias, alpha, limit):
         needs = ctx.needs_input_grad[0] or ctx.needs_input_grad[2]
         if needs:
-            out, ws, pre = kernels.moe_experts_forward(
+            out, ws, fac = kernels.moe_experts_forward(
                 hidden, router_indices, routing_weights, gu_blocks, gu_scales, gu_bias,
                 dn_blocks, dn_scales, dn_bias, alpha, limit, save=True)
             ctx.save_for_backward(hidden, router_indices, routing_weights, gu_blocks, gu_scales,
-                                  gu_bias, dn_blocks, dn_scales, dn_bias, ws, pre)
+                                  gu_bias, dn_blocks, dn_scales, dn_bias, ws, fac)
             ctx.alpha, ctx.limit = alpha, limit
         else:
             out = kernels.moe_experts_forward(
@@ -118,9 +119,9 @@ class _MoEExperts(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         (hidden, idx, w, gu_b, gu_s, gu_bias, dn_b, dn_s, dn_bias, ws,
-         pre) = ctx.saved_tensors
+         fac) = ctx.saved_tensors
         grad_h, grad_w = kernels.moe_experts_backward(
-            grad_out, hidden, idx, w, gu_b, gu_s, dn_b, dn_s, ws, pre, ctx.alpha, ctx.limit,
+            grad_out, hidden, idx, w, gu_b, gu_s, dn_b, dn_s, ws, fac, ctx.alpha, ctx.limit,
             need_hidden=ctx.needs_input_grad[0], need_weights=ctx.needs_input_grad[2])
         return grad_h, None, grad_w, None, None, None, None, None, None, None, None
 

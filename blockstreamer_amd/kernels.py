@@ -266,8 +266,11 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
 
     ``hidden [T, H]``, ``router_indices [T, k]``, ``routing_weights [T, k]``;
     packed experts in the checkpoint layout.  Returns ``out [T, H]`` in the
-    dtype of ``hidden``; with ``save=True`` also ``(workspace, gate_up_pre)``
-    for the input-gradient backward.  Activations enter the MFMA as bfloat16,
+    dtype of ``hidden``; with ``save=True`` also ``(workspace, swiglu_grad)``
+    for the input-gradient backward: ``swiglu_grad`` is bf16 ``[T*k, 2I]`` in
+    expert-sorted row order, per activation column j the clamped SwiGLU's
+    derivatives w.r.t. gate (column 2j) and up (2j+1) at the float32
+    pre-activations, the clamp masks applied.  Activations enter the MFMA as bfloat16,
     except on ``path="mx"`` (two MXFP8 terms, see ``PATHS``).
 
     ``noalloc=True`` runs the same kernels through
@@ -324,12 +327,12 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
         return out
     ws_bytes = moe_workspace_bytes(T, H, I, E, k)
     ws = _aligned_bytes(ws_bytes, dev)
-    save_pre = torch.empty((T * k, 2 * I), dtype=torch.float32, device=dev) if save else None
+    save_grad = torch.empty((T * k, 2 * I), dtype=torch.bfloat16, device=dev) if save else None
     with torch.cuda.device(dev):
-        _lib.call("bsa_moe_experts_fwd", *common, ws.data_ptr(), ws_bytes, ptr(save_pre), PATHS[path],
+        _lib.call("bsa_moe_experts_fwd", *common, ws.data_ptr(), ws_bytes, ptr(save_grad), PATHS[path],
                   layout, _lib.stream_handle(dev))
     if save:
-        return out, ws, save_pre
+        return out, ws, save_grad
     return out
 
 
@@ -432,7 +435,7 @@ def moe_bwd_workspace_bytes(T: int, H: int, I: int, E: int, k: int) -> int:
 def moe_experts_backward(grad_out: Tensor, hidden: Tensor, router_indices: Tensor,
                          routing_weights: Tensor, gate_up_blocks: Tensor, gate_up_scales: Tensor,
                          down_blocks: Tensor, down_scales: Tensor, workspace: Tensor,
-                         gate_up_pre: Tensor, alpha: float = 1.702, limit: float = 7.0, *,
+                         swiglu_grad: Tensor, alpha: float = 1.702, limit: float = 7.0, *,
                          need_hidden: bool = True, need_weights: bool = True):
     """Input-gradient backward of ``moe_experts_forward(..., save=True)``.
 
@@ -454,13 +457,13 @@ def moe_experts_backward(grad_out: Tensor, hidden: Tensor, router_indices: Tenso
     layout = _check_packed(gate_up_blocks, gate_up_scales, E, 2 * I, H, "gate_up_proj")
     if _check_packed(down_blocks, down_scales, E, H, I, "down_proj") != layout:
         raise ValueError("gate_up and down blocks must be in the same layout")
-    if gate_up_pre.dtype != torch.float32 or tuple(gate_up_pre.shape) != (T * k, 2 * I):
-        raise ValueError(f"gate_up_pre must be the forward's float32 [{T * k}, {2 * I}] save, "
-                         f"got {gate_up_pre.dtype} {list(gate_up_pre.shape)}")
+    if swiglu_grad.dtype != torch.bfloat16 or tuple(swiglu_grad.shape) != (T * k, 2 * I):
+        raise ValueError(f"swiglu_grad must be the forward's bfloat16 [{T * k}, {2 * I}] save, "
+                         f"got {swiglu_grad.dtype} {list(swiglu_grad.shape)}")
     ws_need = moe_workspace_bytes(T, H, I, E, k)
     if workspace.dtype != torch.uint8 or workspace.numel() < ws_need:
         raise ValueError(f"workspace must be the forward's uint8 workspace of >= {ws_need} bytes")
-    dev = _lib.require_gpu(grad_out, hidden, router_indices, routing_weights, workspace, gate_up_pre,
+    dev = _lib.require_gpu(grad_out, hidden, router_indices, routing_weights, workspace, swiglu_grad,
                            gate_up_blocks, gate_up_scales, down_blocks, down_scales)
     if T == 0:
         return (torch.zeros_like(hidden) if need_hidden else None,
@@ -471,7 +474,7 @@ def moe_experts_backward(grad_out: Tensor, hidden: Tensor, router_indices: Tenso
     w = routing_weights.contiguous()
     # the backward kernels DMA the packed weights in 16- or 4-byte pieces
     # (staging-blob views are 8-byte aligned; the k-pair layout moves in
-    # 16-byte pieces only) and the pre-activations in 16
+    # 16-byte pieces only) and the saved derivative factors in 16
     gub, gus, dnb, dns = (_as_u8(x) for x in (gate_up_blocks, gate_up_scales, down_blocks, down_scales))
     if layout == LAYOUT_KPAIR:
         _require_kpair_aligned(gub, "gate_up_proj_blocks")
@@ -479,7 +482,7 @@ def moe_experts_backward(grad_out: Tensor, hidden: Tensor, router_indices: Tenso
     else:
         gub, dnb = _aligned(gub, 4), _aligned(dnb, 4)
     gus, dns = _aligned(gus, 4), _aligned(dns, 4)
-    pre = _aligned(gate_up_pre.contiguous(), 16)
+    fac = _aligned(swiglu_grad.contiguous(), 16)
     bwd_bytes = moe_bwd_workspace_bytes(T, H, I, E, k)
     bws = _aligned_bytes(bwd_bytes, dev)
     grad_h = torch.empty((T, H), dtype=hidden.dtype, device=dev) if need_hidden else None
@@ -488,7 +491,7 @@ def moe_experts_backward(grad_out: Tensor, hidden: Tensor, router_indices: Tenso
         _lib.call("bsa_moe_experts_bwd", g.data_ptr(), g_code, T, H, I, E, k, idx.data_ptr(),
                   w.data_ptr(), _lib.dtype_code(w.dtype), gub.data_ptr(), gus.data_ptr(),
                   dnb.data_ptr(), dns.data_ptr(), float(alpha), float(limit),
-                  workspace.data_ptr(), workspace.numel(), pre.data_ptr(), bws.data_ptr(),
+                  workspace.data_ptr(), workspace.numel(), fac.data_ptr(), bws.data_ptr(),
                   bwd_bytes, grad_h.data_ptr() if grad_h is not None else None,
                   _lib.dtype_code(hidden.dtype),
                   grad_w.data_ptr() if grad_w is not None else None, layout, _lib.stream_handle(dev))

@@ -58,13 +58,15 @@ extern "C" {
 const char *bsa_last_error(void);
 
 /* ABI version of this library (major * 100 + minor).  The major number
- * changes whenever an existing signature changes: 2 inserted the
- * blocks_layout argument before the stream in bsa_moe_experts_fwd,
- * bsa_moe_gate_up, bsa_moe_down and bsa_moe_experts_bwd.  The minor number
- * counts added entry points (201: bsa_moe_experts_fwd_noalloc; 202:
- * bsa_quant_mxfp8_split, bsa_mxfp4_matmul).  A binding
- * checks the major number before its first call. */
-#define BSA_VERSION_MAJOR 2
+ * changes whenever an existing signature or the meaning of an argument
+ * changes: 2 inserted the blocks_layout argument before the stream in
+ * bsa_moe_experts_fwd, bsa_moe_gate_up, bsa_moe_down and
+ * bsa_moe_experts_bwd; 3 made the forward's save for the backward the
+ * SwiGLU's bf16 derivative factors (save_swiglu_grad) instead of float32
+ * pre-activations.  The minor number counts added entry points (the
+ * no-allocation forward, the MXFP8 split and the packed matmul came with
+ * major 2).  A binding checks the major number before its first call. */
+#define BSA_VERSION_MAJOR 3
 int bsa_version(void);
 
 /*
@@ -149,11 +151,16 @@ int bsa_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
  *   workspace       >= bsa_moe_workspace_bytes(...) bytes, 256-byte aligned;
  *                   holds the expert-sorted dispatch and intermediates, and is
  *                   what a later backward reads
- *   save_gate_up    optional float32 [T*k, 2I]: gate_up pre-activations in
- *                   expert-sorted row order, for the backward
+ *   save_swiglu_grad optional bf16 [T*k, 2I] (16-byte aligned), written for
+ *                   the backward in expert-sorted row order: per activation
+ *                   column j, d act/d gate at 2j and d act/d up at 2j+1 of
+ *                   the clamped SwiGLU at the float32 pre-activations, the
+ *                   clamp masks applied (torch autograd's derivative of
+ *                   gptoss.py:130-135; the reference's autograd keeps the
+ *                   bf16 gate_up, the same size)
  *   path            0 = automatic (path 3 when more than 16 rows per expert
  *                   on average, both projections can take it and
- *                   save_gate_up is NULL, else 1 up to 16 rows per expert and
+ *                   save_swiglu_grad is NULL, else 1 up to 16 rows per expert and
  *                   2 beyond), 1 = weight-streaming kernel, 2 = tiled kernel,
  *                   3 = native block-scaled MX kernel (activations split into
  *                   two MXFP8 terms by bsa_quant_mxfp8_split's rule, then two
@@ -179,7 +186,7 @@ int bsa_moe_experts_fwd(
     const void *gate_up_bias, const void *down_blocks, const void *down_scales,
     const void *down_bias, int bias_dtype, float alpha, float limit, void *out,
     int out_dtype, void *workspace, int64_t workspace_bytes,
-    void *save_gate_up, int path, int blocks_layout, void *stream);
+    void *save_swiglu_grad, int path, int blocks_layout, void *stream);
 
 /*
  * bsa_moe_experts_fwd without the workspace arguments: the same kernels and
@@ -206,7 +213,7 @@ int bsa_moe_experts_fwd_noalloc(
     int weight_dtype, const void *gate_up_blocks, const void *gate_up_scales,
     const void *gate_up_bias, const void *down_blocks, const void *down_scales,
     const void *down_bias, int bias_dtype, float alpha, float limit, void *out,
-    int out_dtype, void *save_gate_up, int path, int blocks_layout,
+    int out_dtype, void *save_swiglu_grad, int path, int blocks_layout,
     void *stream);
 
 /*
@@ -235,7 +242,7 @@ int bsa_moe_gate_up(const void *hidden, int64_t T, int64_t H, int64_t I,
                     int64_t E, int64_t k, const void *blocks,
                     const void *scales, const void *bias, int bias_dtype,
                     float alpha, float limit, void *workspace,
-                    int64_t workspace_bytes, void *save_gate_up, int path,
+                    int64_t workspace_bytes, void *save_swiglu_grad, int path,
                     int blocks_layout, void *stream);
 int bsa_moe_down(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
                  const void *blocks, const void *scales, const void *bias,
@@ -356,14 +363,14 @@ int bsa_moe_bwd_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
  *
  *   grad_out        grad_dtype [T, H]
  *   workspace       the forward's workspace, unchanged since that call
- *   save_gate_up    the forward's float32 [T*k, 2I] pre-activations
+ *   save_swiglu_grad the forward's bf16 [T*k, 2I] derivative factors
  *   bwd_workspace   >= bsa_moe_bwd_workspace_bytes(...) bytes, 256-aligned
  *   grad_hidden     grad_hidden_dtype [T, H], or NULL to skip
  *   grad_weights    float32 [T, k] gradient of routing_weights, or NULL
  *
  * H must be a multiple of 64.  The packed blocks and scales must be 4-byte
  * aligned (16-byte aligned ones move in 16-byte DMA pieces, others in 4-byte
- * pieces) and save_gate_up 16-byte aligned; otherwise BSA_EINVAL.  Dropped (token, slot) pairs get a zero
+ * pieces) and save_swiglu_grad 16-byte aligned; otherwise BSA_EINVAL.  Dropped (token, slot) pairs get a zero
  * routing-weight gradient.  blocks_layout is that of both blocks tensors.
  */
 int bsa_moe_experts_bwd(
@@ -372,7 +379,7 @@ int bsa_moe_experts_bwd(
     const void *routing_weights, int weight_dtype, const void *gate_up_blocks,
     const void *gate_up_scales, const void *down_blocks,
     const void *down_scales, float alpha, float limit, void *workspace,
-    int64_t workspace_bytes, const void *save_gate_up, void *bwd_workspace,
+    int64_t workspace_bytes, const void *save_swiglu_grad, void *bwd_workspace,
     int64_t bwd_workspace_bytes, void *grad_hidden, int grad_hidden_dtype,
     float *grad_weights, int blocks_layout, void *stream);
 

@@ -104,21 +104,21 @@ def test_backward_refuses_bad_arguments_before_the_gpu():
     w = torch.ones(T, k)
     gub, gus, _, dnb, dns, _ = _small_experts(E, H, I)
     ws = torch.zeros(1 << 20, dtype=torch.uint8)
-    pre = torch.zeros(T * k, 2 * I, dtype=torch.float32)
+    fac = torch.zeros(T * k, 2 * I, dtype=torch.bfloat16)
     g = torch.zeros(T, H, dtype=torch.bfloat16)
 
     def call(**over):
         args = dict(grad_out=g, hidden=h, router_indices=idx, routing_weights=w, gate_up_blocks=gub,
-                    gate_up_scales=gus, down_blocks=dnb, down_scales=dns, workspace=ws, gate_up_pre=pre)
+                    gate_up_scales=gus, down_blocks=dnb, down_scales=dns, workspace=ws, swiglu_grad=fac)
         args.update(over)
         return kernels.moe_experts_backward(**args)
 
     with pytest.raises(ValueError, match="grad_out must be"):
         call(grad_out=torch.zeros(T, H + 32, dtype=torch.bfloat16))
-    with pytest.raises(ValueError, match="gate_up_pre must be"):
-        call(gate_up_pre=pre.to(torch.bfloat16))
-    with pytest.raises(ValueError, match="gate_up_pre must be"):
-        call(gate_up_pre=pre[:-1])
+    with pytest.raises(ValueError, match="swiglu_grad must be"):
+        call(swiglu_grad=fac.float())
+    with pytest.raises(ValueError, match="swiglu_grad must be"):
+        call(swiglu_grad=fac[:-1])
     with pytest.raises(ValueError, match="down_proj_blocks must be"):
         call(down_blocks=torch.zeros(E, H, I // 32 + 1, 16, dtype=torch.uint8))
     with pytest.raises(ValueError, match="gate_up_proj_scales must be"):

@@ -180,9 +180,9 @@ def test_misaligned_k_pair_blocks_are_refused(device):
     with pytest.raises(ValueError, match="16-byte aligned"):
         kernels.dequantize_mxfp4(kp[0], kp[1])
     ws = torch.zeros(kernels.moe_workspace_bytes(T, H, I, E, k), dtype=torch.uint8, device=device)
-    pre = torch.zeros(T * k, 2 * I, dtype=torch.float32, device=device)
+    fac = torch.zeros(T * k, 2 * I, dtype=torch.bfloat16, device=device)
     with pytest.raises(ValueError, match="16-byte aligned"):
-        kernels.moe_experts_backward(t["hidden"], t["hidden"], idx, w, kp[0], kp[1], kp[3], kp[4], ws, pre)
+        kernels.moe_experts_backward(t["hidden"], t["hidden"], idx, w, kp[0], kp[1], kp[3], kp[4], ws, fac)
 
 
 @pytest.mark.parametrize("dims", [(8, 2, 256, 256, 16), (8, 2, 256, 256, 300), (4, 4, 2880, 2880, 8)],
