@@ -398,6 +398,9 @@ def bench_moe(wl: Workload, T: int, steps: int, warmup: int, path: str = "auto",
         torch.cuda.synchronize()
         fb_ms = _median_ms(pairs)
         f_ms = _median_ms(fpairs)
+        # a forward that saves for the backward keeps the bf16 kernels where
+        # automatic selection would take the MX ones
+        res["train_forward_kernel_path"] = "tiled" if path == "auto" and kernel == "mx" else kernel
         res["fwd_bwd_ms"] = round(fb_ms, 4)
         res["bwd_ms"] = round(fb_ms - f_ms, 4)
         res["bwd_TFLOP_per_s"] = round(flops / ((fb_ms - f_ms) / 1e3) / 1e12, 1)
