@@ -394,9 +394,10 @@ typedef __attribute__((address_space(3))) void lds_void;
 // (the decode weight stream): the non-temporal bit (nt).  A read-bandwidth
 // probe over 4 GiB measured 7.07 TB/s for 16-byte DMA with it against 6.27
 // without, and 6.03 against 5.64 at two workgroups per CU; the decode layer
-// at 64 tokens went from 0.262 to 0.236 ms.  The prefill and backward weight
-// tiles keep the default policy: several row tiles re-read them from L2 (nt
-// there made the prefill 45 % slower).
+// at 64 tokens went from 0.262 to 0.236 ms.  It is set on the persistent
+// decode kernel's stream.  The prefill and backward weight tiles keep the
+// default policy: several row tiles re-read them from L2 (nt there made the
+// prefill 45 % slower).
 constexpr int CPOL_STREAM = 2;
 
 // s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited on)
@@ -422,8 +423,7 @@ __device__ __forceinline__ void wait_tiles_ahead(int ahead) {
 }
 
 
-// Copy `bytes` (a multiple of 16) of a read-once weight span from global to
-// LDS.  DMA (non-temporal): gfx950
+// Copy `bytes` (a multiple of 16) from global to LDS.  DMA: gfx950
 // global_load_lds_dwordx4, each wave moving 1 KiB per instruction with every
 // load of the workgroup in flight at once (16-byte aligned source).
 // Otherwise a register copy with 8-byte loads, 8 in flight per thread.
@@ -436,7 +436,7 @@ __device__ __forceinline__ void copy_to_lds(uint8_t* dst, const uint8_t* src, in
     for (int c = wave; c < chunks; c += 4) {
       const int off = (c << 10) + lane * 16;
       if (off < bytes)
-        __builtin_amdgcn_global_load_lds(src + off, (lds_void*)(dst + (c << 10)), 16, 0, CPOL_STREAM);
+        __builtin_amdgcn_global_load_lds(src + off, (lds_void*)(dst + (c << 10)), 16, 0, 0);
     }
   } else {
     const int units = bytes >> 4;
@@ -674,7 +674,7 @@ __global__ __launch_bounds__(256, 3) void moe_stream_parts_kernel(GemmArgs a) {
     const int q = min(wave + 4 * j, SC_PIECES - 1);
     const int off = q * 1024 + lane * 16;
     __builtin_amdgcn_global_load_lds(gS + (off + 16 <= SCALE_BYTES ? off : 0), (lds_void*)(sS + q * 1024),
-                                     16, 0, CPOL_STREAM);
+                                     16, 0, 0);
   }
   // part p, piece i (2 per wave): rows 4i .. 4i+3, lane -> row 4i + lane/16,
   // slot lane%16 holding group 16p + ((lane%16) ^ (row%16)); groups past G
@@ -686,7 +686,7 @@ __global__ __launch_bounds__(256, 3) void moe_stream_parts_kernel(GemmArgs a) {
       const int row = 4 * i + (ln >> 4);
       const int g = 16 * p + ((ln & 15) ^ (row & 15));
       __builtin_amdgcn_global_load_lds(gb + bq_off(kp, row, g < G ? g : 0, G),
-                                       (lds_void*)(sb + p * PART + i * 1024), 16, 0, CPOL_STREAM);
+                                       (lds_void*)(sb + p * PART + i * 1024), 16, 0, 0);
     }
   };
 #pragma unroll
