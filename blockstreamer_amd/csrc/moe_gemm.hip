@@ -64,7 +64,7 @@ int launch_combine(const float* Y, const int64_t* idx, const void* w, int w_dtyp
 int launch_bwd_prep(const void* dout, int dout_dtype, const float* y, const void* w, int w_dtype,
                     const int* pair_pos, int P, int k, int H, uint16_t* dy, float* grad_w,
                     hipStream_t st);
-int launch_quant_mxfp8_split(const void* x, int in_dtype, int64_t R, int64_t K, int64_t ldx, const int* row_map,
+int launch_quant_mxfp8_split(const void* x, int in_dtype, int64_t R, int64_t K, int64_t ldx, const int* dest,
                              int topk, uint8_t* q, uint8_t* s, SplitLayout L, hipStream_t st);
 
 enum Epi : int {
@@ -2683,16 +2683,16 @@ static int stage_gate_up(const MoeShape& m, const void* hidden, const void* bloc
   const int64_t P = m.T * m.k;
   const int chosen = pick_path(path, P, m.E, m.H);
   if (chosen == PATH_MX) {
-    // each token's hidden row is split once, then gathered per pair
+    // each token's hidden row is split once and written to each of its pairs
     if (m.H % MX_BK != 0 || m.I % MX_BK != 0) {
       set_error("gate_up (MX path): hidden %lld and intermediate %lld must be multiples of 64",
                 (long long)m.H, (long long)m.I);
       return BSA_EINVAL;
     }
-    // every pair's hidden row split once, in sorted order and k-tile-major,
-    // so a tile's rows of one k-tile are one contiguous run
+    // every token's hidden row split once and written to its pairs' sorted
+    // rows, k-tile-major, so a tile's rows of one k-tile are one contiguous run
     const SplitLayout hl{128, w.rows_mx * 128, 4, w.rows_mx * 4};
-    int rc = launch_quant_mxfp8_split(hidden, DT_BF16, P, m.H, m.H, w.row_pair, (int)m.k, w.hq, w.hs, hl, st);
+    int rc = launch_quant_mxfp8_split(hidden, DT_BF16, m.T, m.H, m.H, w.pair_pos, (int)m.k, w.hq, w.hs, hl, st);
     if (rc) return rc;
     g.Aq = w.hq;
     g.ldq = hl.q_kt;

@@ -98,10 +98,12 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(const void* __restrict__ 
 // Output: the codes of 64-element k-tile t of row r at q + r * L.q_row +
 // t * L.q_kt, 64 hi bytes then 64 lo bytes; block g's scale byte (that of X;
 // lo's is max(byte - 4, 0)) at s + r * L.s_row + (g / 2) * L.s_kt + g % 2.
-// Row r reads input row row_map[r] / topk when row_map is given.
+// With dest (the dispatch's pair_pos), input row t is split once and written
+// to output rows dest[t * topk + j] for its topk slots j (-1: dropped), so
+// each token's row is read and split once whatever its top-k.
 template <int IN>
 __global__ __launch_bounds__(256) void mx_split_kernel(const void* __restrict__ x, int64_t ldx,
-                                                       const int* __restrict__ row_map, int topk, int64_t nblk,
+                                                       const int* __restrict__ dest, int topk, int64_t nblk,
                                                        int G, uint8_t* __restrict__ q, uint8_t* __restrict__ s,
                                                        SplitLayout L) {
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -110,8 +112,7 @@ __global__ __launch_bounds__(256) void mx_split_kernel(const void* __restrict__ 
   const int part = threadIdx.x & 3;
   const int64_t r = blk / G;
   const int g = (int)(blk - r * G);
-  const int64_t src = row_map ? (int64_t)(row_map[r] / topk) : r;
-  const int64_t off = src * ldx + g * 32 + part * 8;
+  const int64_t off = r * ldx + g * 32 + part * 8;
   float v[8];
   if constexpr (IN == DT_BF16) {
     const u32x4_t w = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + off);
@@ -131,11 +132,14 @@ __global__ __launch_bounds__(256) void mx_split_kernel(const void* __restrict__ 
   }
   uint32_t h[2], l[2];
   const uint32_t sbyte = mx_split8(v, h, l);
-  if (ok) {
-    uint8_t* row = q + r * L.q_row + (g >> 1) * L.q_kt + (g & 1) * 32 + part * 8;
+  if (!ok) return;
+  for (int j = 0; j < (dest ? topk : 1); ++j) {
+    const int64_t o = dest ? (int64_t)dest[r * topk + j] : r;
+    if (o < 0) continue;
+    uint8_t* row = q + o * L.q_row + (g >> 1) * L.q_kt + (g & 1) * 32 + part * 8;
     *reinterpret_cast<uint2*>(row) = make_uint2(h[0], h[1]);
     *reinterpret_cast<uint2*>(row + 64) = make_uint2(l[0], l[1]);
-    if (part == 0) s[r * L.s_row + (g >> 1) * L.s_kt + (g & 1)] = (uint8_t)sbyte;
+    if (part == 0) s[o * L.s_row + (g >> 1) * L.s_kt + (g & 1)] = (uint8_t)sbyte;
   }
 }
 
@@ -166,7 +170,7 @@ int launch_quant_mxfp8(const void* x, int in_dtype, int64_t R, int64_t K, int64_
 
 // Two-term split of R rows of K (K % 64 == 0) elements (input row stride
 // ldx; row r reads row_map[r] / topk when row_map is given) into the layout L.
-int launch_quant_mxfp8_split(const void* x, int in_dtype, int64_t R, int64_t K, int64_t ldx, const int* row_map,
+int launch_quant_mxfp8_split(const void* x, int in_dtype, int64_t R, int64_t K, int64_t ldx, const int* dest,
                              int topk, uint8_t* q, uint8_t* s, SplitLayout L, hipStream_t st) {
   if (R == 0) return BSA_OK;
   const int G = (int)(K / 32);
@@ -177,13 +181,13 @@ int launch_quant_mxfp8_split(const void* x, int in_dtype, int64_t R, int64_t K, 
     return BSA_EINVAL;
   }
   if (in_dtype == DT_BF16)
-    hipLaunchKernelGGL(mx_split_kernel<DT_BF16>, dim3((unsigned)grid), dim3(256), 0, st, x, ldx, row_map, topk,
+    hipLaunchKernelGGL(mx_split_kernel<DT_BF16>, dim3((unsigned)grid), dim3(256), 0, st, x, ldx, dest, topk,
                        nblk, G, q, s, L);
   else if (in_dtype == DT_F32)
-    hipLaunchKernelGGL(mx_split_kernel<DT_F32>, dim3((unsigned)grid), dim3(256), 0, st, x, ldx, row_map, topk,
+    hipLaunchKernelGGL(mx_split_kernel<DT_F32>, dim3((unsigned)grid), dim3(256), 0, st, x, ldx, dest, topk,
                        nblk, G, q, s, L);
   else
-    hipLaunchKernelGGL(mx_split_kernel<DT_F16>, dim3((unsigned)grid), dim3(256), 0, st, x, ldx, row_map, topk,
+    hipLaunchKernelGGL(mx_split_kernel<DT_F16>, dim3((unsigned)grid), dim3(256), 0, st, x, ldx, dest, topk,
                        nblk, G, q, s, L);
   BSA_LAUNCH_CHECK("mxfp8 split launch");
   return BSA_OK;

@@ -35,14 +35,11 @@ __device__ __forceinline__ void nstore(void* p, int64_t i, float v, int dt) {
     static_cast<uint16_t*>(p)[i] = (uint16_t)f32_to_f16_bits(v);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
-}
-
-// 8 elements of a 2-byte type packed in 16 bytes -> float32.
-__device__ __forceinline__ void unpack8(const u32x4_t q, int dt, float (&v)[8]) {
+// RMSNorm arithmetic of the vector path.  A row is reduced in 16-byte chunks
+// of 8 elements (bf16 or f16): lane l of a wave sums the squares of chunks
+// l, l + 64, ... in increasing index, then rms_wave_sum adds the 64 lane sums
+// by a butterfly.
+__device__ __forceinline__ void rms_unpack8(const u32x4_t q, int dt, float (&v)[8]) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     if (dt == DT_BF16) {
@@ -55,32 +52,63 @@ __device__ __forceinline__ void unpack8(const u32x4_t q, int dt, float (&v)[8]) 
   }
 }
 
-__device__ __forceinline__ u32x4_t load16(const void* p, int64_t elem) {
-  return *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p) + elem);
+__device__ __forceinline__ float rms_sumsq8(const u32x4_t q, int dt, float ss) {
+  float v[8];
+  rms_unpack8(q, dt, v);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss += v[j] * v[j];
+  return ss;
 }
 
-// weight[i .. i+8) -> float32 (i % 8 == 0, weight 16-byte aligned).
-__device__ __forceinline__ void loadw8(const void* w, int i, int wdt, float (&v)[8]) {
+__device__ __forceinline__ float rms_wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+__device__ __forceinline__ float rms_inv(float sumsq, int H, float eps) {
+  return 1.0f / sqrtf(sumsq / (float)H + eps);
+}
+
+// y = dtype(g * (x * r)) for one chunk (g: the weight as float32).
+__device__ __forceinline__ u32x4_t rms_apply8(const u32x4_t q, int dt, const float (&g)[8], float r) {
+  float v[8];
+  rms_unpack8(q, dt, v);
+  u32x4_t o;
+  if (dt == DT_BF16) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = f32_to_bf16_bits(g[2 * j] * (v[2 * j] * r)) | (f32_to_bf16_bits(g[2 * j + 1] * (v[2 * j + 1] * r)) << 16);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = f32_to_f16_bits(g[2 * j] * (v[2 * j] * r)) | (f32_to_f16_bits(g[2 * j + 1] * (v[2 * j + 1] * r)) << 16);
+  }
+  return o;
+}
+
+// weight[i .. i+8) -> float32 (i % 8 == 0; the weight 16-byte aligned).
+__device__ __forceinline__ void rms_weight8(const void* w, int64_t i, int wdt, float (&g)[8]) {
   if (wdt == DT_F32) {
     const f32x4_t a = *reinterpret_cast<const f32x4_t*>(static_cast<const float*>(w) + i);
     const f32x4_t b = *reinterpret_cast<const f32x4_t*>(static_cast<const float*>(w) + i + 4);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      v[j] = a[j];
-      v[4 + j] = b[j];
+      g[j] = a[j];
+      g[4 + j] = b[j];
     }
   } else {
-    unpack8(load16(w, i), wdt, v);
+    rms_unpack8(*reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(w) + i), wdt, g);
   }
+}
+
+__device__ __forceinline__ u32x4_t load16(const void* p, int64_t elem) {
+  return *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p) + elem);
 }
 
 __device__ __forceinline__ uint32_t pack2(float a, float b, int dt) {
   if (dt == DT_BF16) return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
   return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
-}
-
-__device__ __forceinline__ float inv_rms(float sumsq, int H, float eps) {
-  return 1.0f / sqrtf(sumsq / (float)H + eps);
 }
 
 // 16-byte chunks of a row that one lane keeps in registers on the vector
@@ -90,9 +118,11 @@ constexpr int NORM_RC = 6;
 // Vector path: x, y (dy, dx) are bf16 or f16 with 16-byte aligned rows,
 // H % 8 == 0, H / 8 <= 64 * NORM_RC, weight 16-byte aligned.  Lane l holds
 // chunks l, l + 64, ... of its wave's row.
-__global__ __launch_bounds__(256, 4) void rmsnorm_fwd_vec_kernel(const void* __restrict__ x, int dt, int T, int H,
+template <int DT>
+__global__ __launch_bounds__(256, 4) void rmsnorm_fwd_vec_kernel(const void* __restrict__ x, int T, int H,
                                                               const void* __restrict__ w, int wdt, float eps,
                                                               void* __restrict__ y) {
+  constexpr int dt = DT;
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
@@ -106,26 +136,16 @@ __global__ __launch_bounds__(256, 4) void rmsnorm_fwd_vec_kernel(const void* __r
     if (c < nc) xr[i] = load16(x, row + 8 * c);
   }
 #pragma unroll
-  for (int i = 0; i < NORM_RC; ++i) {
-    if (lane + 64 * i < nc) {
-      float v[8];
-      unpack8(xr[i], dt, v);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ss += v[j] * v[j];
-    }
-  }
-  const float r = inv_rms(wave_sum(ss), H, eps);
+  for (int i = 0; i < NORM_RC; ++i)
+    if (lane + 64 * i < nc) ss = rms_sumsq8(xr[i], dt, ss);
+  const float r = rms_inv(rms_wave_sum(ss), H, eps);
 #pragma unroll
   for (int i = 0; i < NORM_RC; ++i) {
     const int c = lane + 64 * i;
     if (c < nc) {
-      float v[8], g[8];
-      unpack8(xr[i], dt, v);
-      loadw8(w, 8 * c, wdt, g);
-      u32x4_t o;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] = pack2(g[2 * j] * (v[2 * j] * r), g[2 * j + 1] * (v[2 * j + 1] * r), dt);
-      *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(y) + row + 8 * c) = o;
+      float g[8];
+      rms_weight8(w, 8 * c, wdt, g);
+      *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(y) + row + 8 * c) = rms_apply8(xr[i], dt, g, r);
     }
   }
 }
@@ -143,7 +163,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const void* __restrict
     const float v = nload(x, row + h, dt);
     ss += v * v;
   }
-  const float r = inv_rms(wave_sum(ss), H, eps);
+  const float r = rms_inv(rms_wave_sum(ss), H, eps);
   for (int h = lane; h < H; h += 64) nstore(y, row + h, nload(w, h, wdt) * (nload(x, row + h, dt) * r), dt);
 }
 
@@ -171,9 +191,9 @@ __global__ __launch_bounds__(256, 4) void rmsnorm_bwd_vec_kernel(const void* __r
     const int c = lane + 64 * i;
     if (c < nc) {
       float v[8], d[8], g[8];
-      unpack8(xr[i], dt, v);
-      unpack8(gr[i], dt, d);
-      loadw8(w, 8 * c, wdt, g);
+      rms_unpack8(xr[i], dt, v);
+      rms_unpack8(gr[i], dt, d);
+      rms_weight8(w, 8 * c, wdt, g);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         ss += v[j] * v[j];
@@ -181,16 +201,16 @@ __global__ __launch_bounds__(256, 4) void rmsnorm_bwd_vec_kernel(const void* __r
       }
     }
   }
-  const float r = inv_rms(wave_sum(ss), H, eps);
-  const float c3 = r * r * r * wave_sum(dot) / (float)H;
+  const float r = rms_inv(rms_wave_sum(ss), H, eps);
+  const float c3 = r * r * r * rms_wave_sum(dot) / (float)H;
 #pragma unroll
   for (int i = 0; i < NORM_RC; ++i) {
     const int c = lane + 64 * i;
     if (c < nc) {
       float v[8], d[8], g[8];
-      unpack8(xr[i], dt, v);
-      unpack8(gr[i], dt, d);
-      loadw8(w, 8 * c, wdt, g);
+      rms_unpack8(xr[i], dt, v);
+      rms_unpack8(gr[i], dt, d);
+      rms_weight8(w, 8 * c, wdt, g);
       u32x4_t o;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -214,8 +234,8 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const void* __restrict
     ss += v * v;
     dot += (nload(w, h, wdt) * nload(dy, row + h, dt)) * v;
   }
-  const float r = inv_rms(wave_sum(ss), H, eps);
-  const float c3 = r * r * r * wave_sum(dot) / (float)H;
+  const float r = rms_inv(rms_wave_sum(ss), H, eps);
+  const float c3 = r * r * r * rms_wave_sum(dot) / (float)H;
   for (int h = lane; h < H; h += 64)
     nstore(dx, row + h, r * (nload(w, h, wdt) * nload(dy, row + h, dt)) - nload(x, row + h, dt) * c3, dt);
 }
@@ -244,8 +264,8 @@ extern "C" int bsa_rmsnorm_fwd(const void* x, int dtype, int64_t T, int64_t H, c
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)((T + 3) / 4));
   if (norm_vec_ok(dtype, H, {x, out, weight}))
-    hipLaunchKernelGGL(rmsnorm_fwd_vec_kernel, grid, dim3(256), 0, st, x, dtype, (int)T, (int)H, weight,
-                       weight_dtype, eps, out);
+    hipLaunchKernelGGL(dtype == DT_BF16 ? rmsnorm_fwd_vec_kernel<DT_BF16> : rmsnorm_fwd_vec_kernel<DT_F16>, grid,
+                       dim3(256), 0, st, x, (int)T, (int)H, weight, weight_dtype, eps, out);
   else
     hipLaunchKernelGGL(rmsnorm_fwd_kernel, grid, dim3(256), 0, st, x, dtype, (int)T, (int)H, weight,
                        weight_dtype, eps, out);

@@ -122,3 +122,21 @@ def test_mx_rejects_unsupported_shapes(device):
     t, idx, w = _layer(4, 2, 96, 64, 16, seed=2, device=device)   # H % 64 != 0
     with pytest.raises(ValueError, match="64"):
         kernels.moe_experts_forward(t["hidden"], idx, w, *expert_args(t), path="mx")
+
+
+def test_mx_dropped_pairs(device):
+    """Router indices outside [0, E) are dropped on the MX path too: the
+    hidden rows are split per token into the sorted rows of its kept pairs
+    only, and the layer matches the float32 oracle with those pairs' weights
+    set to zero."""
+    E, k, H, I, T = 16, 4, 512, 256, 200
+    t, idx, w = _layer(E, k, H, I, T, seed=23, device=device)
+    idx = idx.clone()
+    idx[::7, 0] = -1
+    idx[3::11, 2] = E
+    announce("MX layer with dropped pairs")
+    got = kernels.moe_experts_forward(t["hidden"], idx, w, *expert_args(t), path="mx")
+    keep = (idx >= 0) & (idx < E)
+    args = [a.cpu() for a in expert_args(t)]
+    want = oracle.experts_ref(t["hidden"].cpu(), idx.clamp(0, E - 1).cpu(), (w * keep).cpu().float(), *args)
+    assert_layer_close(got, want, "MX dropped pairs", absolute=True)
