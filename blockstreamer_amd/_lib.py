@@ -73,6 +73,19 @@ _SIGNATURES = {
     ],
     "bsa_rmsnorm_fwd": [_ptr, _int, _i64, _i64, _ptr, _int, _f32, _ptr, _ptr],
     "bsa_rmsnorm_bwd": [_ptr, _ptr, _int, _i64, _i64, _ptr, _int, _f32, _ptr, _ptr],
+    "bsa_attention_fwd": [
+        _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,  # q, q strides, k, k strides, v, v strides, sinks
+        _i64, _i64, _i64, _i64, _i64, _i64,        # B, Tq, Tk, Hq, Hkv, head_dim
+        _int, _i64, _f32,                          # causal, window, scaling
+        _ptr, _ptr, _ptr, _ptr,                    # out, out strides, lse, stream
+    ],
+    "bsa_attention_bwd": [
+        _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,  # grad_out, q, k, v (each with strides)
+        _ptr, _ptr, _ptr,                          # out, out strides, lse
+        _i64, _i64, _i64, _i64, _i64, _i64,        # B, Tq, Tk, Hq, Hkv, head_dim
+        _int, _i64, _f32,                          # causal, window, scaling
+        _ptr, _ptr, _ptr, _ptr, _ptr,              # grad_q, grad_k, grad_v, row_dot, stream
+    ],
 }
 _RESTYPE = {"bsa_last_error": ctypes.c_char_p}
 

@@ -43,6 +43,8 @@ typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+// Pointer type of the LDS operand of __builtin_amdgcn_global_load_lds.
+typedef __attribute__((address_space(3))) void lds_void;
 
 // ---------------------------------------------------------------------------
 // MXFP4 element decode.

@@ -388,8 +388,6 @@ inline size_t st_smem_bytes(int K) {
   return (b > red ? b : red) + 16;
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 // Cache-policy operand of global_load_lds for data that is read exactly once
 // (the decode weight stream): the non-temporal bit (nt).  A read-bandwidth
 // probe over 4 GiB measured 7.07 TB/s for 16-byte DMA with it against 6.27

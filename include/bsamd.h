@@ -65,7 +65,8 @@ const char *bsa_last_error(void);
  * SwiGLU's bf16 derivative factors (save_swiglu_grad) instead of float32
  * pre-activations.  The minor number counts added entry points (the
  * no-allocation forward, the MXFP8 split and the packed matmul came with
- * major 2).  A binding checks the major number before its first call. */
+ * major 2; minor 1 of major 3 added the attention entry points).  A binding
+ * checks the major number before its first call. */
 #define BSA_VERSION_MAJOR 3
 int bsa_version(void);
 
@@ -412,6 +413,55 @@ int bsa_rmsnorm_fwd(const void *x, int dtype, int64_t T, int64_t H,
 int bsa_rmsnorm_bwd(const void *grad_out, const void *x, int dtype, int64_t T,
                     int64_t H, const void *weight, int weight_dtype,
                     float eps, void *grad_x, void *stream);
+
+/*
+ * Attention core of the gpt-oss decoder layer (grouped-query attention with a
+ * per-head sink logit).  Replaces eager_attention_forward of transformers
+ * 5.15.0 models/gpt_oss/modeling_gpt_oss.py:235-264 as GptOssAttention.forward
+ * (:295-336) calls it; the streaming runner reaches it through the decoder
+ * layer (block_streamer/runners.py:327-335).
+ *   out[b, t, h] = sum_j p[t, j] v[b, j, h / G]   (G = Hq / Hkv)
+ *   p[t, :]      = softmax([q[b,t,h] . k[b,j,h/G] * scaling (visible j), sinks[h]])[:Tk]
+ * q [B, Tq, Hq, 64], k and v [B, Tk, Hkv, 64], out [B, Tq, Hq, 64]: bf16,
+ * addressed through element strides (batch, sequence, head), each a multiple
+ * of 8, the head dimension contiguous, base pointers 16-byte aligned.
+ * sinks: float32 [Hq], or null for no sink.  Masks: causal = 0 shows every
+ * key (what the eager path does with attention_mask = None); causal = 1 shows
+ * key j to query t when j <= Tk - Tq + t, and window > 0 also requires
+ * Tk - Tq + t - j < window.  lse (optional, float32 [B, Hq, Tq]) receives
+ * log2 of each row's softmax denominator (sink included) in units of
+ * scaling * log2(e) times the dot products: what bsa_attention_bwd needs.
+ * Float32 accumulation; probabilities rounded to bf16 for the value product.
+ */
+int bsa_attention_fwd(const void *q, const int64_t *q_strides, const void *k,
+                      const int64_t *k_strides, const void *v,
+                      const int64_t *v_strides, const float *sinks, int64_t B,
+                      int64_t Tq, int64_t Tk, int64_t Hq, int64_t Hkv,
+                      int64_t head_dim, int causal, int64_t window,
+                      float scaling, void *out, const int64_t *out_strides,
+                      float *lse, void *stream);
+
+/*
+ * Gradients of bsa_attention_fwd (what autograd computes through
+ * eager_attention_forward, modeling_gpt_oss.py:235-264), from its output and
+ * lse:  p = 2^(scaling log2(e) q.k - lse),  D[t] = grad_out[t] . out[t],
+ *   grad_q = scaling sum_j p (dP - D) k,  grad_k = scaling sum_t p (dP - D) q,
+ *   grad_v = sum_t p grad_out,  with dP[t, j] = grad_out[t] . v[j].
+ * grad_out and out [B, Tq, Hq, 64] and q, k, v as for the forward (strides
+ * per tensor); grad_q [B, Tq, Hq, 64], grad_k and grad_v [B, Tk, Hkv, 64]
+ * contiguous bf16; row_dot float32 [B, Hq, Tq] receives D, from which the
+ * sinks' gradient is -sum_t 2^(sink log2(e) - lse) D.  Two launches, no
+ * atomics (results are deterministic).
+ */
+int bsa_attention_bwd(const void *grad_out, const int64_t *grad_strides,
+                      const void *q, const int64_t *q_strides, const void *k,
+                      const int64_t *k_strides, const void *v,
+                      const int64_t *v_strides, const void *out,
+                      const int64_t *out_strides, const float *lse, int64_t B,
+                      int64_t Tq, int64_t Tk, int64_t Hq, int64_t Hkv,
+                      int64_t head_dim, int causal, int64_t window,
+                      float scaling, void *grad_q, void *grad_k, void *grad_v,
+                      float *row_dot, void *stream);
 
 #ifdef __cplusplus
 }

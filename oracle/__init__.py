@@ -9,6 +9,7 @@ package ``blockstreamer_amd`` never imports it.
 from .oracle import (  # noqa: F401
     FP4_VALUES,
     apply_gate_ref,
+    attention_ref,
     dequant_c,
     dequant_torch,
     bits_equal_or_both_nan,

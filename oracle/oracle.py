@@ -33,6 +33,12 @@ Pinning (how each function is checked, see ``tests/test_oracle.py``):
   weights, plus invariants (zero routing weight contributes nothing, token
   permutation commutes, a single expert with k=1 and weight 1 equals the dense
   chain of library GEMMs).
+* attention with sinks (the other half of the decoder layer): the installed
+  transformers ``eager_attention_forward`` in float64 with the masks its
+  ``masking_utils.eager_mask`` builds (none, causal, sliding window, queries
+  offset into a longer key sequence), plus closed forms: a sink of -inf gives
+  the library's ``scaled_dot_product_attention``, one visible key gives
+  ``sigmoid(s - sink) * v``, and grouped heads equal their repeated keys.
 """
 
 from __future__ import annotations
@@ -190,6 +196,40 @@ def rmsnorm_bwd_ref(grad: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, e
     H = x.shape[-1]
     r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
     return r * g - x * (r ** 3 * (g * x).sum(-1, keepdim=True) / H)
+
+
+def attention_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sinks: torch.Tensor | None,
+                  scaling: float, causal: bool = False, window: int = 0,
+                  dtype: torch.dtype = torch.float64) -> torch.Tensor:
+    """TF/models/gpt_oss/modeling_gpt_oss.py:235-264 (eager_attention_forward,
+    with repeat_kv :203-212) in ``dtype``, not rounded back.
+
+    q ``[B, Hq, Tq, D]``, k and v ``[B, Hkv, Tk, D]`` (the layout
+    GptOssAttention.forward :311-320 hands over), sinks ``[Hq]`` or None.
+    Key j is visible to query t (absolute position p = Tk - Tq + t) always
+    when ``causal`` is False (the eager path with attention_mask=None), else
+    when j <= p and, with ``window`` > 0, p - j < window (masking_utils
+    causal_mask_function and sliding_window_overlay).  Returns
+    ``[B, Tq, Hq, D]`` (:262, attn_output.transpose(1, 2))."""
+    B, Hq, Tq, D = q.shape
+    Hkv, Tk = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    k = k[:, :, None].expand(B, Hkv, G, Tk, D).reshape(B, Hq, Tk, D)
+    v = v[:, :, None].expand(B, Hkv, G, Tk, D).reshape(B, Hq, Tk, D)
+    s = torch.matmul(q, k.transpose(2, 3)) * scaling
+    if causal:
+        pos = torch.arange(Tq)[:, None] + (Tk - Tq)
+        j = torch.arange(Tk)[None, :]
+        vis = j <= pos
+        if window > 0:
+            vis = vis & (j > pos - window)
+        s = s.masked_fill(~vis, float("-inf"))
+    if sinks is not None:
+        s = torch.cat([s, sinks.to(dtype).reshape(1, Hq, 1, 1).expand(B, Hq, Tq, 1)], dim=-1)
+    s = s - s.max(dim=-1, keepdim=True).values
+    p = torch.softmax(s, dim=-1)[..., :Tk]
+    return torch.matmul(p, v).transpose(1, 2)
 
 
 def to_kpair_ref(blocks: torch.Tensor) -> torch.Tensor:
