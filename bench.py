@@ -525,6 +525,103 @@ def bench_norm(T: int, reps: int = 50) -> dict:
     return res
 
 
+# gpt-oss attention (both sizes): 64 query heads, 8 key/value heads, head_dim
+# 64, sliding window 128 on alternate layers (TF/models/gpt_oss/configuration_gpt_oss.py)
+ATTN_HQ, ATTN_HKV, ATTN_D, ATTN_WINDOW = 64, 8, 64, 128
+
+
+def attn_pairs(Tq: int, Tk: int, causal: bool, window: int) -> int:
+    """Visible (query, key) pairs of one head."""
+    if not causal:
+        return Tq * Tk
+    off = Tk - Tq
+    return sum(off + t + 1 if window <= 0 else min(off + t + 1, window) for t in range(Tq))
+
+
+def bench_attention(kind: str, steps: int, warmup: int, eager: bool = True) -> dict:
+    """The attention core of a gpt-oss layer on the HIP kernels.
+
+    prefill: one 8192-token sequence, causal (the full-attention layers) and
+    causal with the 128-token window (the sliding layers), forward and the
+    gradients of q, k, v.  decode: 64 sequences, one new token each, against
+    4096 cached keys.  Inputs in the layout the projections produce
+    ([B, T, H, 64] viewed [B, H, T, 64]), bf16, float32 sinks.
+
+    Roofline: prefill against the bf16 MFMA peak with algorithmic flops
+    (4 * 64 per visible (query, key, head) triple forward: q.k and p.v; 2.5x
+    that backward: dP, dV, dK, dQ and the recomputed S); decode against HBM
+    with its algorithmic bytes (each visible key and value row of every key
+    head read once, q read and out written once).  ``eager_*``: transformers'
+    eager_attention_forward on the same GPU, the reference's attention."""
+    from blockstreamer_amd import attention as A
+
+    dev = torch.device("cuda", 0)
+    B, Tq, Tk = (1, 8192, 8192) if kind == "prefill" else (64, 1, 4096)
+    Hq, Hkv, D = ATTN_HQ, ATTN_HKV, ATTN_D
+    scaling = D ** -0.5
+    gen = torch.Generator().manual_seed(5)
+    q = torch.randn(B, Tq, Hq, D, generator=gen).to(torch.bfloat16).to(dev).transpose(1, 2)
+    k = torch.randn(B, Tk, Hkv, D, generator=gen).to(torch.bfloat16).to(dev).transpose(1, 2)
+    v = torch.randn(B, Tk, Hkv, D, generator=gen).to(torch.bfloat16).to(dev).transpose(1, 2)
+    sinks = (torch.randn(Hq, generator=gen) * 2).to(dev)
+    dout = torch.randn(B, Tq, Hq, D, generator=gen).to(torch.bfloat16).to(dev)
+
+    def timed(fn, n):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
+    res = {"batch": B, "q_len": Tq, "kv_len": Tk, "heads": Hq, "kv_heads": Hkv, "head_dim": D}
+    for name, window in (("full", 0), ("sliding", ATTN_WINDOW)):
+        pairs = attn_pairs(Tq, Tk, True, window) * B * Hq
+        out, lse = A.attention_forward(q, k, v, sinks, scaling, True, window, return_lse=True)
+        ms = timed(lambda: A.attention_forward(q, k, v, sinks, scaling, True, window, return_lse=True), steps)
+        r = {"fwd_ms": round(ms, 4)}
+        if kind == "prefill":
+            fl = 4 * D * pairs
+            r["fwd_TFLOP_per_s"] = round(fl / (ms * 1e-3) / 1e12, 1)
+            r["fwd_roofline"] = {"bound": "mfma", "achieved": r["fwd_TFLOP_per_s"], "peak": 2500.0,
+                                 "unit": "TFLOP/s", "frac": round(r["fwd_TFLOP_per_s"] / 2500.0, 4)}
+            bms = timed(lambda: A.attention_backward(dout, q, k, v, sinks, out, lse, scaling, True, window), steps)
+            r["bwd_ms"] = round(bms, 4)
+            r["bwd_TFLOP_per_s"] = round(2.5 * fl / (bms * 1e-3) / 1e12, 1)
+            r["bwd_roofline_frac"] = round(r["bwd_TFLOP_per_s"] / 2500.0, 4)
+        else:
+            keys = min(Tk, window) if window else Tk
+            byt = B * Hkv * keys * D * 2 * 2 + 2 * B * Tq * Hq * D * 2
+            r["hbm_bytes"] = byt
+            r["GB_per_s"] = round(byt / (ms * 1e-3) / 1e9, 1)
+            r["roofline"] = {"bound": "hbm", "achieved": r["GB_per_s"], "peak": 8000.0, "unit": "GB/s",
+                             "frac": round(r["GB_per_s"] / 8000.0, 4)}
+        res[name] = r
+    if eager and kind == "prefill":
+        try:
+            from transformers.masking_utils import causal_mask_function, eager_mask
+            from transformers.models.gpt_oss.modeling_gpt_oss import eager_attention_forward
+
+            class _M(torch.nn.Module):
+                pass
+            mod = _M()
+            mod.sinks = sinks.to(torch.bfloat16)
+            mod.num_key_value_groups = Hq // Hkv
+            mask = eager_mask(B, Tq, Tk, mask_function=causal_mask_function, dtype=torch.bfloat16, device=dev)
+            with torch.no_grad():
+                ms = timed(lambda: eager_attention_forward(mod, q, k, v, mask, scaling=scaling), 2)
+            res["eager_full_fwd_ms"] = round(ms, 3)
+            del mask
+            torch.cuda.empty_cache()
+        except (ImportError, torch.OutOfMemoryError) as exc:  # noqa: PERF203
+            res["eager_full_fwd_ms"] = f"not run: {type(exc).__name__}"
+    return res
+
+
 def bench_copy(steps: int, warmup: int) -> dict:
     """torch device-to-device copy of 2 GiB: 4 GiB of HBM traffic per step."""
     dev = torch.device("cuda", 0)
@@ -545,6 +642,9 @@ def bench_copy(steps: int, warmup: int) -> dict:
 def focused(args) -> int:
     if args.workload == "copy":
         res = bench_copy(args.steps, args.warmup)
+    elif args.workload == "attention":
+        res = {"attention_prefill": bench_attention("prefill", args.steps, args.warmup),
+               "attention_decode": bench_attention("decode", args.steps, args.warmup)}
     elif args.workload == "norm":
         res = {"norm": [bench_norm(t, reps=max(args.steps, 20)) for t in (64, 8192)]}
     elif args.workload == "moe_decode":
@@ -568,12 +668,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="dequant",
                     choices=["dequant", "moe_decode", "moe_20b", "moe_prefill", "moe_prefill_train", "copy",
-                             "norm"],
+                             "norm", "attention"],
                     help="dequant: the headline line (plus MoE layer results); moe_decode / moe_20b / "
                          "moe_prefill: one MoE layer forward alone; moe_prefill_train: the 8192-token "
                          "forward that saves for the backward plus the input-gradient backward; copy: a "
                          "plain 2 GiB device copy that calibrates the HBM byte counters; norm: the "
-                         "post-attention RMSNorm, fused and eager")
+                         "post-attention RMSNorm, fused and eager; attention: the attention core "
+                         "(prefill 8192 tokens and decode), against transformers' eager attention")
     ap.add_argument("--path", default="auto", choices=["auto", "stream", "tiled", "mx"],
                     help="expert GEMM kernels for the MoE workloads (auto: weight streaming for decode, "
                          "the two-term MX kernels for prefill)")
@@ -638,6 +739,8 @@ def main() -> int:
                                                                     "gpt-oss-120b prefill batch")
         line["moe_layer"] = moe
         line["post_attention_norm"] = {"t64": bench_norm(64), "t8192": bench_norm(8192)}
+        line["attention"] = {"prefill_t8192": bench_attention("prefill", max(args.steps // 2, 5), args.warmup),
+                             "decode_b64_kv4096": bench_attention("decode", max(args.steps, 20), args.warmup)}
     print(json.dumps(line), flush=True)
     return 0
 

@@ -102,17 +102,20 @@ def attention_backward(grad_out: Tensor, query: Tensor, key: Tensor, value: Tens
     dq = torch.empty(B, Tq, Hq, D, dtype=torch.bfloat16, device=dev)
     dk = torch.empty(B, Tk, Hkv, D, dtype=torch.bfloat16, device=dev)
     dv = torch.empty_like(dk)
-    row_dot = torch.empty(B, Hq, Tq, dtype=torch.float32, device=dev)
+    # per row R = t * (Hq / Hkv) + i of key head hk: (L, D), D = grad_out . out
+    row_stats = torch.empty(B, Hkv, Tq * (Hq // Hkv), 2, dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
         _lib.call("bsa_attention_bwd",
                   g.data_ptr(), _strides(g, 1, 2), q.data_ptr(), _strides(q, 2, 1),
                   k.data_ptr(), _strides(k, 2, 1), v.data_ptr(), _strides(v, 2, 1),
                   o.data_ptr(), _strides(o, 1, 2), lse.data_ptr(),
                   B, Tq, Tk, Hq, Hkv, D, 1 if causal else 0, int(window), float(scaling),
-                  dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), row_dot.data_ptr(), _lib.stream_handle(dev))
+                  dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), row_stats.data_ptr(), _lib.stream_handle(dev))
     dsinks = None
     if sinks_grad:
         # d sink[h] = -sum_t p_sink[t] D[t], p_sink = 2^(sink log2(e) - lse)
+        G = Hq // Hkv
+        row_dot = row_stats[..., 1].reshape(B, Hkv, Tq, G).permute(0, 1, 3, 2).reshape(B, Hq, Tq)
         p_sink = torch.exp2(sinks.detach().float().reshape(1, Hq, 1) * 1.4426950408889634 - lse)
         dsinks = (-(p_sink * row_dot).sum(dim=(0, 2))).to(sinks.dtype)
     return dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2), dsinks

@@ -16,34 +16,43 @@
 //
 // The sink enters the online softmax as its starting state: running maximum
 // = sink, running sum = exp(sink - sink) = 1, accumulator = 0.  Products run
-// on bf16 MFMA with float32 accumulation; the probabilities are rounded to
-// bf16 for the P.V product (as the eager path's cast to the value dtype).
+// on bf16 MFMA (v_mfma_f32_32x32x16_bf16) with float32 accumulation; the
+// probabilities are rounded to bf16 for the P.V product (as the eager path's
+// cast to the value dtype).
 //
-// Kernel (gfx950): a workgroup takes 128 rows of one (batch, key head): row
-// R = t * G + i is query t of head G * hk + i (G = Hq / Hkv), so the G heads
-// sharing a key head read each K/V tile once.  Four waves, 32 rows each;
-// key tiles of 64 in LDS, double buffered.  Per tile a wave computes
-//   S^T = K Q^T  (v_mfma_f32_32x32x16_bf16, lane c = query c): the row max
-//                and sum of a query are one exchange between the two lane
-//                halves.  The K rows enter the MFMA permuted (pi below), so
-//                lane half g holds keys 8g .. 8g+7 and 16+8g .. 16+8g+7 of
-//                each 32-key block: exactly the B operand of
-//   O^T += V^T P^T  with V^T staged transposed in LDS.  The accumulator
-//                rows are head dimensions and its columns queries, so the
-//                online-softmax rescale of query c stays in lane c.
-// LDS tiles: K [64 keys][64 d] and V^T [64 d][64 keys], bf16, 128-byte rows
-// whose 16-byte chunk c sits at chunk c ^ ((row >> 1) & 7) (a ds_read_b128
-// pass serves 16 lanes from 64 banks, 256 bytes: two rows, so the swizzle
-// pairs rows).
+// Rows: a workgroup of the forward and of the dq backward takes 128 rows of
+// one (batch, key head); row R = t * G + i is query t of head G * hk + i
+// (G = Hq / Hkv), so the G heads sharing a key head read each K/V tile once.
+// Four waves, 32 rows each (lane c = row c of the wave), key tiles of 64.
+//
+// Orientation: S^T = K Q^T puts a query in each lane, so its row maximum and
+// sum are one exchange between the two lane halves.  The K rows enter that
+// MFMA permuted (pi below): lane half g then holds keys 8g .. 8g+7 and
+// 16 + 8g .. 16 + 8g + 7 of each 32-key block, which is exactly the B
+// operand of O^T += V^T P^T, so the probabilities never leave registers and
+// the online-softmax rescale of query c stays in lane c.
+//
+// LDS: every tile is the natural row-major copy a DMA (global_load_lds)
+// brings in: 64 rows x 128 bytes, 16-byte chunk c of row R at position
+// c ^ sw(R), sw(R) = 4 * ((R >> 1) & 1) | ((R >> 2) & 3).  Two kinds of read
+// use it: ds_read_b128 of 16 rows at one chunk (the operands K, V, Q, dO
+// with rows permuted), whose 16 (R & 1, sw) pairs are distinct, and the
+// transposing ds_read_b64_tr_b16 (V^T, K^T, Q^T, dO^T: in each 16-lane
+// group, lane s addresses 4 elements of row k0 + s/4 at column m0 + 4(s%4)
+// and lane i receives element i%4 of lanes i/4, 4 + i/4, 8 + i/4, 12 + i/4:
+// column m0 + i at rows k0 .. k0+3), whose four rows land in four different
+// 64-byte quarters of the 256-byte bank period.  Tiles stream through a ring
+// of AT_NS stages, AT_NS - 1 ahead of the computation.
 // ---------------------------------------------------------------------------
 #include "bsa_common.h"
 
 namespace bsa {
 
 constexpr int AT_D = 64;                    // head dimension
-constexpr int AT_BR = 128;                  // rows per workgroup
+constexpr int AT_BR = 128;                  // rows per workgroup (forward, dq)
 constexpr int AT_BC = 64;                   // keys per tile
 constexpr int AT_TILE = AT_BC * AT_D * 2;   // 8 KiB
+constexpr int AT_NS = 4;                    // ring stages
 
 struct AttnArgs {
   const uint16_t* q;
@@ -59,14 +68,37 @@ struct AttnArgs {
   float scale2;         // scaling * log2(e)
 };
 
-// Byte offset of 16-byte chunk `ch` of row `row` in a 128-byte-row LDS tile.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int at_sw(int row) { return (((row >> 1) & 1) << 2) | ((row >> 2) & 3); }
+
+// Byte offset of 16-byte chunk `ch` of row `row` of a tile.
 __device__ __forceinline__ uint32_t at_off(int row, int ch) {
-  return (uint32_t)(row * 128 + ((ch ^ ((row >> 1) & 7)) << 4));
+  return (uint32_t)(row * 128 + ((ch ^ at_sw(row)) << 4));
 }
 
-// MFMA row r of the S^T product takes key pi(r): with r = 8a + 4g + b
+// Transposing read: the address this lane supplies so that, for the rows
+// k0 .. k0+3 (k0 = 16 s + 8 g + 4 h, g = lane / 32) and columns m0 + 0..15
+// of its 16-lane group (m0 = 32 mb + 16 ((lane >> 4) & 1)), lane receives
+// column m0 + lane % 16 at those four rows.
+__device__ __forceinline__ uint32_t at_tr_off(int lane, int s, int h, int mb) {
+  const int sl = lane & 15;
+  const int row = 16 * s + 8 * (lane >> 5) + 4 * h + (sl >> 2);
+  const int col = 32 * mb + 16 * ((lane >> 4) & 1) + 4 * (sl & 3);
+  return (uint32_t)(row * 128 + ((((col >> 3) ^ at_sw(row)) << 4) | ((col & 7) << 1)));
+}
+
+__device__ __forceinline__ u32x4_t at_tr8(const uint8_t* tile, uint32_t o0, uint32_t o1) {
+  typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+  const s16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + o0));
+  const s16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + o1));
+  const uint2 ua = __builtin_bit_cast(uint2, a), ub = __builtin_bit_cast(uint2, b);
+  return u32x4_t{ua.x, ua.y, ub.x, ub.y};
+}
+
+// MFMA row r of S^T (or S) takes key (row) pi(r): with r = 8a + 4g + b
 // (a 0..3, g 0..1, b 0..3), pi(r) = 16 (a >> 1) + 8g + 4 (a & 1) + b, so that
-// output register v of lane half g is key 8g + v (v < 8) or 16 + 8g + v - 8.
+// output register v of lane half g is 8g + v (v < 8) or 16 + 8g + v - 8.
 __device__ __forceinline__ int at_pi(int r) {
   const int a = r >> 3, g = (r >> 2) & 1, b = r & 3;
   return 16 * (a >> 1) + 8 * g + 4 * (a & 1) + b;
@@ -77,9 +109,89 @@ __device__ __forceinline__ f32x16_t at_mfma(const u32x4_t& a, const u32x4_t& b, 
                                                  c, 0, 0, 0);
 }
 
+// Two floats -> packed bf16 (v_cvt_pk_bf16_f32: round to nearest even).
+__device__ __forceinline__ uint32_t at_pack2(float lo, float hi) {
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// max / sum of a value and its copy in lane ^ 32 (v_permlane32_swap: the
+// pair holds both halves' values; combining them symmetrically gives every
+// lane the same result, operands in the same order)
+__device__ __forceinline__ float at_max32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float at_add32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited on)
+template <int N>
+__device__ __forceinline__ void at_wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// Wait until at most min(ahead, MAXAHEAD) tiles of PER loads each are in flight.
+template <int PER, int MAXAHEAD>
+__device__ __forceinline__ void wait_vmcnt_tiles(int ahead) {
+  if constexpr (MAXAHEAD <= 0) {
+    at_wait_vmcnt<0>();
+  } else {
+    if (ahead >= MAXAHEAD) {
+      at_wait_vmcnt<MAXAHEAD * PER>();
+      return;
+    }
+    wait_vmcnt_tiles<PER, MAXAHEAD - 1>(ahead);
+  }
+}
+
+// DMA of one 64-row x 128-byte tile by four waves: instruction m of wave w
+// fills LDS bytes (256 m + 64 w + lane) * 16, i.e. row 32 m + 8 w + lane / 8,
+// position lane & 7, from source chunk position ^ sw(row) of row row0 + row
+// (clamped to rmax).
+__device__ __forceinline__ void at_dma_tile(const uint16_t* src, int64_t stride, int row0, int rmax, uint8_t* tile,
+                                            int wave, int lane) {
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const int row = 32 * m + 8 * wave + (lane >> 3);
+    const int ch = (lane & 7) ^ at_sw(row);
+    const int r = min(row0 + row, rmax);
+    __builtin_amdgcn_global_load_lds(src + (int64_t)r * stride + ch * 8, (lds_void*)(tile + (256 * m + 64 * wave) * 16),
+                                     16, 0, 0);
+  }
+}
+
+// Per-workgroup row geometry of the forward and the dq backward.
+struct AtRows {
+  int R, t, h, qpos, rows, R0, kt0, kt1, pos_first, pos_last;
+  bool live_wave;
+};
+
+__device__ __forceinline__ AtRows at_rows(int Tq, int Tk, int G, int causal, int window, int rb, int hk, int wave,
+                                          int c) {
+  AtRows r;
+  r.rows = Tq * G;
+  r.R0 = rb * AT_BR;
+  r.R = min(r.R0 + 32 * wave + c, r.rows - 1);  // rows past the end repeat the last (never stored)
+  r.t = r.R / G;
+  r.h = hk * G + (r.R - r.t * G);
+  r.qpos = Tk - Tq + r.t;
+  const int Rl = min(r.R0 + AT_BR, r.rows) - 1;
+  r.pos_first = Tk - Tq + r.R0 / G;
+  r.pos_last = Tk - Tq + Rl / G;
+  const int j_end = causal ? min(Tk, r.pos_last + 1) : Tk;
+  const int j_begin = window > 0 ? max(0, r.pos_first - window + 1) : 0;
+  r.kt0 = j_begin / AT_BC;
+  r.kt1 = (j_end + AT_BC - 1) / AT_BC;
+  r.live_wave = r.R0 + 32 * wave < r.rows;
+  return r;
+}
+
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
-  __shared__ __align__(16) uint8_t sK[2][AT_TILE];
-  __shared__ __align__(16) uint8_t sV[2][AT_TILE];
+  extern __shared__ __align__(1024) uint8_t at_smem[];  // AT_NS stages of [K tile][V tile]
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -89,82 +201,35 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   const int rb = (int)gridDim.x - 1 - (int)blockIdx.x;
   const int hk = blockIdx.y;
   const int b = blockIdx.z;
-  const int rows = a.Tq * a.G;
-  const int R0 = rb * AT_BR;
+  const AtRows rw = at_rows(a.Tq, a.Tk, a.G, a.causal, a.window, rb, hk, wave, c);
 
-  // --- this lane's query row ------------------------------------------------
-  const int R = min(R0 + 32 * wave + c, rows - 1);  // rows past the end repeat the last (never stored)
-  const int t = R / a.G;
-  const int h = hk * a.G + (R - t * a.G);
-  const int qpos = a.Tk - a.Tq + t;
-
-  // --- the workgroup's key tiles ------------------------------------------
-  const int Rl = min(R0 + AT_BR, rows) - 1;
-  const int pos_first = a.Tk - a.Tq + R0 / a.G;
-  const int pos_last = a.Tk - a.Tq + Rl / a.G;
-  const int j_end = a.causal ? min(a.Tk, pos_last + 1) : a.Tk;
-  const int j_begin = a.window > 0 ? max(0, pos_first - a.window + 1) : 0;
-  const int kt0 = j_begin / AT_BC;
-  const int kt1 = (j_end + AT_BC - 1) / AT_BC;
-
-  // --- Q fragments (B operand of S^T): d 16s + 8g .. +7 of row c -----------
-  const uint16_t* qrow = a.q + b * a.sqb + (int64_t)t * a.sqt + (int64_t)h * a.sqh;
+  // Q fragments (B operand of S^T): d 16s + 8g .. +7 of row c
+  const uint16_t* qrow = a.q + b * a.sqb + (int64_t)rw.t * a.sqt + (int64_t)rw.h * a.sqh;
   u32x4_t qf[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) qf[s] = *reinterpret_cast<const u32x4_t*>(qrow + 16 * s + 8 * g);
 
-  // --- tile loaders --------------------------------------------------------
   const uint16_t* kbase = a.k + b * a.skb + (int64_t)hk * a.skh;
   const uint16_t* vbase = a.v + b * a.svb + (int64_t)hk * a.svh;
-  // K by DMA: instruction m of wave w fills LDS bytes (256m + 64w + lane) * 16:
-  // row 32m + 8w + lane / 8, position lane & 7 (source chunk position ^ swizzle)
-  auto issue_k = [&](int kt, int buf) {
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int row = 32 * m + 8 * wave + (lane >> 3);
-      const int ch = (lane & 7) ^ ((row >> 1) & 7);
-      const int j = min(kt * AT_BC + row, a.Tk - 1);
-      __builtin_amdgcn_global_load_lds(kbase + (int64_t)j * a.skt + ch * 8,
-                                       (lds_void*)(&sK[buf][0] + (256 * m + 64 * wave) * 16), 16, 0, 0);
-    }
+  auto issue = [&](int kt) {
+    uint8_t* st = at_smem + (kt % AT_NS) * (2 * AT_TILE);
+    at_dma_tile(kbase, a.skt, kt * AT_BC, a.Tk - 1, st, wave, lane);
+    at_dma_tile(vbase, a.svt, kt * AT_BC, a.Tk - 1, st + AT_TILE, wave, lane);
   };
-  // V through registers: lane = key, wave w = head dimensions 16w .. 16w+15,
-  // written transposed
-  u32x4_t vr[2];
-  auto load_v = [&](int kt) {
-    const int j = min(kt * AT_BC + lane, a.Tk - 1);
-    const u32x4_t* p = reinterpret_cast<const u32x4_t*>(vbase + (int64_t)j * a.svt + 16 * wave);
-    vr[0] = p[0];
-    vr[1] = p[1];
-  };
-  auto store_vt = [&](int buf) {
-    uint8_t* base = &sV[buf][0];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int row = 16 * wave + i;
-      const uint32_t w = vr[i >> 3][(i & 7) >> 1];
-      const uint16_t val = (uint16_t)((i & 1) ? (w >> 16) : (w & 0xFFFFu));
-      *reinterpret_cast<uint16_t*>(base + at_off(row, lane >> 3) + (lane & 7) * 2) = val;
-    }
-  };
+  constexpr int DPT = 4;  // DMA instructions per wave per tile
 
-  // --- per-lane LDS read offsets ---------------------------------------------
-  // S^T A operand: K row 32 kb + pi(c), d chunk 2s + g
-  uint32_t koff[2][4];
+  // read offsets: K rows 32 kb + pi(c) at d chunk 2s + g (kb adds 4096);
+  // V^T via transposing reads (d block db, 16-key step s adds 2048, halves h)
+  uint32_t koff[4], voff[2][2];
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-    for (int s = 0; s < 4; ++s) koff[kb][s] = at_off(32 * kb + at_pi(c), 2 * s + g);
-  // O^T A operand: V^T row 32 db + c, key chunk 2s + g
-  uint32_t voff[2][4];
+  for (int s = 0; s < 4; ++s) koff[s] = at_off(at_pi(c), 2 * s + g);
 #pragma unroll
   for (int db = 0; db < 2; ++db)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) voff[db][s] = at_off(32 * db + c, 2 * s + g);
+    for (int h = 0; h < 2; ++h) voff[db][h] = at_tr_off(lane, 0, h, db);
 
-  // --- state -------------------------------------------------------------
   constexpr float LOG2E = 1.4426950408889634f;
-  float m = a.sinks ? a.sinks[h] * LOG2E : -INFINITY;
+  float m = a.sinks ? a.sinks[rw.h] * LOG2E : -INFINITY;
   float l = a.sinks ? 1.f : 0.f;
   f32x16_t o[2];
 #pragma unroll
@@ -172,25 +237,21 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
 
-  if (kt0 < kt1) {
-    load_v(kt0);
-    issue_k(kt0, 0);
-  }
-  for (int kt = kt0; kt < kt1; ++kt) {
-    const int buf = (kt - kt0) & 1;
-    // V^T of this tile into its buffer (last read two tiles ago, before the
-    // previous barrier), then wait for this tile's K and meet every wave
-    store_vt(buf);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();
-    if (kt + 1 < kt1) {
-      load_v(kt + 1);
-      issue_k(kt + 1, buf ^ 1);
-    }
-    const uint8_t* K = &sK[buf][0];
-    const uint8_t* V = &sV[buf][0];
+  // the Q loads above are waited for here with the first tile
+  for (int i = 0; i < AT_NS - 1; ++i)
+    if (rw.kt0 + i < rw.kt1) issue(rw.kt0 + i);
+  for (int kt = rw.kt0; kt < rw.kt1; ++kt) {
+    // tile kt has landed once at most the tiles issued after it are in
+    // flight; the barrier also certifies every wave is done with tile kt-1,
+    // whose stage takes tile kt + AT_NS - 1 (bare s_barrier: a
+    // __syncthreads() fence would wait for that DMA too)
+    wait_vmcnt_tiles<DPT, AT_NS - 2>(rw.kt1 - 1 - kt);
+    asm volatile("s_barrier" ::: "memory");
+    if (kt + AT_NS - 1 < rw.kt1) issue(kt + AT_NS - 1);
+    if (!rw.live_wave) continue;
+    const uint8_t* K = at_smem + (kt % AT_NS) * (2 * AT_TILE);
+    const uint8_t* V = K + AT_TILE;
 
-    // S^T: two 32-key blocks
     f32x16_t sc[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -198,28 +259,25 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
       for (int v = 0; v < 16; ++v) sc[kb][v] = 0.f;
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        sc[kb] = at_mfma(*reinterpret_cast<const u32x4_t*>(K + koff[kb][s]), qf[s], sc[kb]);
+        sc[kb] = at_mfma(*reinterpret_cast<const u32x4_t*>(K + koff[s] + 4096 * kb), qf[s], sc[kb]);
     }
-    // scale, mask, running maximum
     const int j0 = kt * AT_BC;
-    const bool full = j0 + AT_BC <= a.Tk && (!a.causal || j0 + AT_BC - 1 <= pos_first) &&
-                      (a.window <= 0 || j0 > pos_last - a.window);
+    const bool full = j0 + AT_BC <= a.Tk && (!a.causal || j0 + AT_BC - 1 <= rw.pos_first) &&
+                      (a.window <= 0 || j0 > rw.pos_last - a.window);
+    // the maximum of the raw products (scale2 > 0), hidden keys at -inf
     float mt = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        float x = sc[kb][v] * a.scale2;
         if (!full) {
           const int j = j0 + 32 * kb + (v < 8 ? 8 * g + v : 16 + 8 * g + v - 8);
-          const bool vis = j < a.Tk && (!a.causal || j <= qpos) && (a.window <= 0 || j > qpos - a.window);
-          x = vis ? x : -INFINITY;
+          const bool vis = j < a.Tk && (!a.causal || j <= rw.qpos) && (a.window <= 0 || j > rw.qpos - a.window);
+          sc[kb][v] = vis ? sc[kb][v] : -INFINITY;
         }
-        sc[kb][v] = x;
-        mt = fmaxf(mt, x);
+        mt = fmaxf(mt, sc[kb][v]);
       }
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
-    const float mn = fmaxf(m, mt);
+    const float mn = fmaxf(m, at_max32(mt) * a.scale2);
     // a row that has seen nothing yet (no sink, every key so far hidden) keeps 0
     const float ms = mn == -INFINITY ? 0.f : mn;
     const float alpha = __builtin_amdgcn_exp2f(m - ms);
@@ -232,13 +290,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
         float p[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          p[i] = __builtin_amdgcn_exp2f(sc[kb][8 * half + i] - ms);
+          p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][8 * half + i], a.scale2, -ms));
           rs += p[i];
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pf[2 * kb + half][i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
+        for (int i = 0; i < 4; ++i) pf[2 * kb + half][i] = at_pack2(p[2 * i], p[2 * i + 1]);
       }
-    rs += __shfl_xor(rs, 32);
+    rs = at_add32(rs);
     l = l * alpha + rs;
     m = mn;
 #pragma unroll
@@ -247,27 +305,402 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
       for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        o[db] = at_mfma(*reinterpret_cast<const u32x4_t*>(V + voff[db][s]), pf[s], o[db]);
+        o[db] = at_mfma(at_tr8(V + 2048 * s, voff[db][0], voff[db][1]), pf[s], o[db]);
     }
   }
 
-  // --- output --------------------------------------------------------------
-  if (R0 + 32 * wave + c >= rows) return;
+  if (rw.R0 + 32 * wave + c >= rw.rows) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  uint16_t* orow = a.out + b * a.sob + (int64_t)t * a.sot + (int64_t)h * a.soh;
+  uint16_t* orow = a.out + b * a.sob + (int64_t)rw.t * a.sot + (int64_t)rw.h * a.soh;
 #pragma unroll
   for (int db = 0; db < 2; ++db)
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int d = 32 * db + 8 * q4 + 4 * g;
       uint2 w;
-      w.x = pack_bf16x2(o[db][4 * q4] * inv, o[db][4 * q4 + 1] * inv);
-      w.y = pack_bf16x2(o[db][4 * q4 + 2] * inv, o[db][4 * q4 + 3] * inv);
+      w.x = at_pack2(o[db][4 * q4] * inv, o[db][4 * q4 + 1] * inv);
+      w.y = at_pack2(o[db][4 * q4 + 2] * inv, o[db][4 * q4 + 3] * inv);
       *reinterpret_cast<uint2*>(orow + d) = w;
     }
   // __builtin_amdgcn_logf is log2
-  if (a.lse && g == 0) a.lse[((int64_t)b * a.Hq + h) * a.Tq + t] = m + __builtin_amdgcn_logf(l);
+  if (a.lse && g == 0) a.lse[((int64_t)b * a.Hq + rw.h) * a.Tq + rw.t] = m + __builtin_amdgcn_logf(l);
 }
+
+// ---------------------------------------------------------------------------
+// Backward (the gradients autograd takes through eager_attention_forward,
+// modeling_gpt_oss.py:235-264), from the forward's log2 denominators L:
+//   p[t, j]  = 2^(S[t, j] * scaling * log2(e) - L[t])      (visible j, else 0)
+//   D[t]     = dO[t] . O[t]       (= sum_j p dP: the sink has no value row)
+//   dP[t, j] = dO[t] . v[j],   dS[t, j] = p (dP - D[t])
+//   dq[t] = scaling * sum_j dS k[j],  dk[j] = scaling * sum_t dS q[t],
+//   dv[j] = sum_t p[t, j] dO[t]
+//   d sink[h] = -sum_t p_sink[t] D[t],  p_sink = 2^(sink log2(e) - L[t])
+// Two kernels, no atomics: attn_bwd_dq (the forward's row blocks; it also
+// writes each row's (L, D) in row order) and attn_bwd_dkv (key blocks, every
+// row that sees them).
+// ---------------------------------------------------------------------------
+struct AttnBwdArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* o;    // forward output (strides so)
+  const uint16_t* dout; // (strides sd)
+  const float* lse;     // [B][Hq][Tq]
+  float* stats;         // [B][Hkv][Tq * G][2]: (L, D) of row R, written by attn_bwd_dq
+  uint16_t* dq;         // [B, Tq, Hq, 64] contiguous
+  uint16_t* dk;         // [B, Tk, Hkv, 64] contiguous
+  uint16_t* dv;
+  int64_t sqb, sqt, sqh, skb, skt, skh, svb, svt, svh, sob, sot, soh, sdb, sdt, sdh;
+  int Tq, Tk, Hq, Hkv, G;
+  int causal, window;
+  int kpairs;           // dk/dv workgroups take key blocks x and nblocks - 1 - x
+  float scale2, scaling;
+};
+
+// 16 bf16 of a u32x4 pair -> float dot with another pair
+__device__ __forceinline__ float at_dot8(const u32x4_t& x, const u32x4_t& y) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    s += __uint_as_float(x[i] << 16) * __uint_as_float(y[i] << 16) +
+         __uint_as_float(x[i] & 0xFFFF0000u) * __uint_as_float(y[i] & 0xFFFF0000u);
+  return s;
+}
+
+// dq: the forward's row blocks and K/V tile ring.  Per tile: S^T = K Q^T and
+// dP^T = V dO^T (K and V rows permuted), dS^T in registers, dq^T += K^T dS^T
+// (K^T by transposing reads of the K tile).
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdArgs a) {
+  extern __shared__ __align__(1024) uint8_t at_smem[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int c = lane & 31;
+  const int g = lane >> 5;
+  const int rb = (int)gridDim.x - 1 - (int)blockIdx.x;
+  const int hk = blockIdx.y;
+  const int b = blockIdx.z;
+  const AtRows rw = at_rows(a.Tq, a.Tk, a.G, a.causal, a.window, rb, hk, wave, c);
+
+  const uint16_t* qrow = a.q + b * a.sqb + (int64_t)rw.t * a.sqt + (int64_t)rw.h * a.sqh;
+  const uint16_t* drow = a.dout + b * a.sdb + (int64_t)rw.t * a.sdt + (int64_t)rw.h * a.sdh;
+  const uint16_t* orow = a.o + b * a.sob + (int64_t)rw.t * a.sot + (int64_t)rw.h * a.soh;
+  u32x4_t qf[4], df[4];
+  float D = 0.f;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    qf[s] = *reinterpret_cast<const u32x4_t*>(qrow + 16 * s + 8 * g);
+    df[s] = *reinterpret_cast<const u32x4_t*>(drow + 16 * s + 8 * g);
+    D += at_dot8(df[s], *reinterpret_cast<const u32x4_t*>(orow + 16 * s + 8 * g));
+  }
+  D = at_add32(D);
+  const float L = a.lse[((int64_t)b * a.Hq + rw.h) * a.Tq + rw.t];
+  if (g == 0 && rw.R0 + 32 * wave + c < rw.rows) {
+    const float2 st2 = {L, D};
+    *reinterpret_cast<float2*>(a.stats + (((int64_t)b * a.Hkv + hk) * rw.rows + rw.R) * 2) = st2;
+  }
+
+  const uint16_t* kbase = a.k + b * a.skb + (int64_t)hk * a.skh;
+  const uint16_t* vbase = a.v + b * a.svb + (int64_t)hk * a.svh;
+  auto issue = [&](int kt) {
+    uint8_t* st = at_smem + (kt % AT_NS) * (2 * AT_TILE);
+    at_dma_tile(kbase, a.skt, kt * AT_BC, a.Tk - 1, st, wave, lane);
+    at_dma_tile(vbase, a.svt, kt * AT_BC, a.Tk - 1, st + AT_TILE, wave, lane);
+  };
+  constexpr int DPT = 4;
+  uint32_t koff[4], toff[2][2];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) koff[s] = at_off(at_pi(c), 2 * s + g);
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) toff[db][h] = at_tr_off(lane, 0, h, db);
+
+  f32x16_t dq[2];
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) dq[db][v] = 0.f;
+
+  for (int i = 0; i < AT_NS - 1; ++i)
+    if (rw.kt0 + i < rw.kt1) issue(rw.kt0 + i);
+  for (int kt = rw.kt0; kt < rw.kt1; ++kt) {
+    wait_vmcnt_tiles<DPT, AT_NS - 2>(rw.kt1 - 1 - kt);
+    asm volatile("s_barrier" ::: "memory");
+    if (kt + AT_NS - 1 < rw.kt1) issue(kt + AT_NS - 1);
+    if (!rw.live_wave) continue;
+    const uint8_t* K = at_smem + (kt % AT_NS) * (2 * AT_TILE);
+    const uint8_t* V = K + AT_TILE;
+    f32x16_t sc[2], dp[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sc[kb][v] = dp[kb][v] = 0.f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        sc[kb] = at_mfma(*reinterpret_cast<const u32x4_t*>(K + koff[s] + 4096 * kb), qf[s], sc[kb]);
+        dp[kb] = at_mfma(*reinterpret_cast<const u32x4_t*>(V + koff[s] + 4096 * kb), df[s], dp[kb]);
+      }
+    }
+    const int j0 = kt * AT_BC;
+    const bool full = j0 + AT_BC <= a.Tk && (!a.causal || j0 + AT_BC - 1 <= rw.pos_first) &&
+                      (a.window <= 0 || j0 > rw.pos_last - a.window);
+    u32x4_t sf[4];  // dS^T operands of the four 16-key steps
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        float ds[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int v = 8 * half + i;
+          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][v], a.scale2, -L));
+          if (!full) {
+            const int j = j0 + 32 * kb + (v < 8 ? 8 * g + v : 16 + 8 * g + v - 8);
+            const bool vis = j < a.Tk && (!a.causal || j <= rw.qpos) && (a.window <= 0 || j > rw.qpos - a.window);
+            p = vis ? p : 0.f;
+          }
+          ds[i] = p * (dp[kb][v] - D);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sf[2 * kb + half][i] = at_pack2(ds[2 * i], ds[2 * i + 1]);
+      }
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) dq[db] = at_mfma(at_tr8(K + 2048 * s, toff[db][0], toff[db][1]), sf[s], dq[db]);
+  }
+
+  if (rw.R0 + 32 * wave + c >= rw.rows) return;
+  uint16_t* out = a.dq + (((int64_t)b * a.Tq + rw.t) * a.Hq + rw.h) * AT_D;
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int d = 32 * db + 8 * q4 + 4 * g;
+      uint2 w;
+      w.x = at_pack2(dq[db][4 * q4] * a.scaling, dq[db][4 * q4 + 1] * a.scaling);
+      w.y = at_pack2(dq[db][4 * q4 + 2] * a.scaling, dq[db][4 * q4 + 3] * a.scaling);
+      *reinterpret_cast<uint2*>(out + d) = w;
+    }
+}
+
+constexpr int AT_KB = 128;  // keys per dk/dv block (32 per wave)
+constexpr int AT_RT = 64;   // rows per step of the dk/dv loop (a tile)
+constexpr int AT_DKV_STAGE = 2 * AT_TILE + 4 * 512;  // q tile, dO tile, a (L, D) copy per wave
+
+// dk, dv: key blocks of 128 keys of one (batch, key head), wave w keeping
+// keys 32w .. 32w+31 (their k and v rows as the B operands of S = Q K^T and
+// dP = dO V^T, lane c = key c) and their dk^T, dv^T accumulators.  The
+// workgroup walks 64-row tiles (rows R = t * G + i as in the forward) of
+// every row that sees one of its keys, through a DMA ring: the q and dO
+// tiles (rows permuted as A operands; q^T and dO^T by transposing reads for
+// dv^T += dO^T P and dk^T += q^T dS) and the tile's (L, D) pairs.  Under a
+// causal mask without a window, workgroup x takes key block x and then block
+// nblocks - 1 - x, so every workgroup walks about the same number of rows.
+__global__ __launch_bounds__(256, 2) void attn_bwd_dkv_kernel(AttnBwdArgs a) {
+  extern __shared__ __align__(1024) uint8_t at_smem[];  // AT_NS stages
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int c = lane & 31;
+  const int g = lane >> 5;
+  const int hk = blockIdx.y;
+  const int b = blockIdx.z;
+  const int rows = a.Tq * a.G;
+  const int off = a.Tk - a.Tq;  // position of query 0
+  const int nkb = (a.Tk + AT_KB - 1) / AT_KB;
+  const uint16_t* qbase = a.q + b * a.sqb;
+  const uint16_t* dbase = a.dout + b * a.sdb;
+  const float* sbase = a.stats + ((int64_t)b * a.Hkv + hk) * rows * 2;
+
+  uint32_t aoff[4], toff[2][2][2];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) aoff[s] = at_off(at_pi(c), 2 * s + g);
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) toff[s][db][h] = at_tr_off(lane, s, h, db);
+
+  for (int pass = 0; pass < (a.kpairs ? 2 : 1); ++pass) {
+    const int kbk = pass == 0 ? (int)blockIdx.x : nkb - 1 - (int)blockIdx.x;
+    if (pass == 1 && kbk <= (int)blockIdx.x) break;  // the middle block of an odd count
+    const int j0 = kbk * AT_KB;
+    // rows that see a key of [j0, j0 + 128)
+    int t_begin = 0, t_end = a.Tq;
+    if (a.causal) {
+      t_begin = max(0, j0 - off);
+      if (a.window > 0) t_end = min(a.Tq, j0 + AT_KB - 1 + a.window - off);
+    }
+    const int r_begin = t_begin * a.G;
+    const int r_end = max(r_begin, t_end * a.G);
+    const int nt = (r_end - r_begin + AT_RT - 1) / AT_RT;
+
+    const int jk = j0 + 32 * wave + c;
+    const int jc = min(jk, a.Tk - 1);
+    const uint16_t* krow = a.k + b * a.skb + (int64_t)jc * a.skt + (int64_t)hk * a.skh;
+    const uint16_t* vrow = a.v + b * a.svb + (int64_t)jc * a.svt + (int64_t)hk * a.svh;
+    u32x4_t kf[4], vf[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      kf[s] = *reinterpret_cast<const u32x4_t*>(krow + 16 * s + 8 * g);
+      vf[s] = *reinterpret_cast<const u32x4_t*>(vrow + 16 * s + 8 * g);
+    }
+    // tile i: rows r_begin + 64 i + row -> q / dO row of (t = R / G, head
+    // hk G + R % G), each lane its own source row (lanes of a group of 8
+    // share one), clamped to the last row
+    auto issue = [&](int i) {
+      uint8_t* st = at_smem + (i % AT_NS) * AT_DKV_STAGE;
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const int row = 32 * m + 8 * wave + (lane >> 3);
+        const int ch = (lane & 7) ^ at_sw(row);
+        const int R = min(r_begin + i * AT_RT + row, rows - 1);
+        const int t = R / a.G;
+        const int h = hk * a.G + (R - t * a.G);
+        __builtin_amdgcn_global_load_lds(qbase + (int64_t)t * a.sqt + (int64_t)h * a.sqh + ch * 8,
+                                         (lds_void*)(st + (256 * m + 64 * wave) * 16), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(dbase + (int64_t)t * a.sdt + (int64_t)h * a.sdh + ch * 8,
+                                         (lds_void*)(st + AT_TILE + (256 * m + 64 * wave) * 16), 16, 0, 0);
+      }
+      // the tile's 64 (L, D) pairs: float 2 r + (lane & 1) of rows
+      // r = lane / 2 (first instruction) and 32 + lane / 2 (second), one copy
+      // per wave
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const int R = min(r_begin + i * AT_RT + 32 * m + (lane >> 1), rows - 1);
+        __builtin_amdgcn_global_load_lds(sbase + (int64_t)R * 2 + (lane & 1),
+                                         (lds_void*)(st + 2 * AT_TILE + wave * 512 + m * 256), 4, 0, 0);
+      }
+    };
+    constexpr int DPT = 6;
+
+    f32x16_t dk[2], dv[2];
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) dk[db][v] = dv[db][v] = 0.f;
+
+    // every wave is done with the previous pass's stages (and its k, v
+    // loads have landed) before they are refilled
+    __syncthreads();
+    for (int i = 0; i < AT_NS - 1; ++i)
+      if (i < nt) issue(i);
+    for (int it = 0; it < nt; ++it) {
+      wait_vmcnt_tiles<DPT, AT_NS - 2>(nt - 1 - it);
+      asm volatile("s_barrier" ::: "memory");
+      if (it + AT_NS - 1 < nt) issue(it + AT_NS - 1);
+      const uint8_t* Q = at_smem + (it % AT_NS) * AT_DKV_STAGE;
+      const uint8_t* DO = Q + AT_TILE;
+      const float* ST = reinterpret_cast<const float*>(Q + 2 * AT_TILE + wave * 512);
+      const int rbase = r_begin + it * AT_RT;
+#pragma unroll
+      for (int rh = 0; rh < 2; ++rh) {  // the tile's two 32-row halves
+        f32x16_t sc, dp;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) sc[v] = dp[v] = 0.f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          sc = at_mfma(*reinterpret_cast<const u32x4_t*>(Q + aoff[s] + 4096 * rh), kf[s], sc);
+          dp = at_mfma(*reinterpret_cast<const u32x4_t*>(DO + aoff[s] + 4096 * rh), vf[s], dp);
+        }
+        // register v: row 32 rh + 8g + v (v < 8) or 32 rh + 16 + 8g + v - 8, key c
+        u32x4_t pf[2], sf[2];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          float p[8], ds[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int r = 32 * rh + 16 * half + 8 * g + i;
+            const float2 sd = *reinterpret_cast<const float2*>(ST + 2 * r);
+            float x = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[8 * half + i], a.scale2, -sd.x));
+            const int R = rbase + r;
+            const int qp = off + R / a.G;
+            const bool vis = R < r_end && jk < a.Tk && (!a.causal || jk <= qp) && (a.window <= 0 || jk > qp - a.window);
+            x = vis ? x : 0.f;
+            p[i] = x;
+            ds[i] = x * (dp[8 * half + i] - sd.y);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            pf[half][i] = at_pack2(p[2 * i], p[2 * i + 1]);
+            sf[half][i] = at_pack2(ds[2 * i], ds[2 * i + 1]);
+          }
+        }
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            dv[db] = at_mfma(at_tr8(DO + 4096 * rh, toff[s][db][0], toff[s][db][1]), pf[s], dv[db]);
+            dk[db] = at_mfma(at_tr8(Q + 4096 * rh, toff[s][db][0], toff[s][db][1]), sf[s], dk[db]);
+          }
+      }
+    }
+
+    if (jk < a.Tk) {
+      uint16_t* okr = a.dk + (((int64_t)b * a.Tk + jk) * a.Hkv + hk) * AT_D;
+      uint16_t* ovr = a.dv + (((int64_t)b * a.Tk + jk) * a.Hkv + hk) * AT_D;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int d = 32 * db + 8 * q4 + 4 * g;
+          uint2 wk, wv;
+          wk.x = at_pack2(dk[db][4 * q4] * a.scaling, dk[db][4 * q4 + 1] * a.scaling);
+          wk.y = at_pack2(dk[db][4 * q4 + 2] * a.scaling, dk[db][4 * q4 + 3] * a.scaling);
+          wv.x = at_pack2(dv[db][4 * q4], dv[db][4 * q4 + 1]);
+          wv.y = at_pack2(dv[db][4 * q4 + 2], dv[db][4 * q4 + 3]);
+          *reinterpret_cast<uint2*>(okr + d) = wk;
+          *reinterpret_cast<uint2*>(ovr + d) = wv;
+        }
+    }
+  }
+}
+
+constexpr int AT_FWD_LDS = AT_NS * 2 * AT_TILE;        // 64 KiB
+constexpr int AT_DKV_LDS = AT_NS * AT_DKV_STAGE;       // 72 KiB
+
+static int at_allow_lds(const void* fn, int idx, int bytes) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    set_error("no current HIP device");
+    return BSA_EHIP;
+  }
+  static bool done[64][3];
+  if (!done[dev][idx]) {
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
+      set_error("attention: cannot allow %d bytes of LDS", bytes);
+      return BSA_EHIP;
+    }
+    done[dev][idx] = true;
+  }
+  return BSA_OK;
+}
+
+static int at_check_common(const char* what, int64_t B, int64_t Tq, int64_t Tk, int64_t Hq, int64_t Hkv,
+                           int64_t head_dim, int causal, int64_t window) {
+  BSA_REQUIRE(head_dim == AT_D, "%s: head_dim must be %d (got %lld)", what, AT_D, (long long)head_dim);
+  BSA_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= 64, "%s: Hq (%lld) must be a multiple of Hkv (%lld), at most 64x", what,
+              (long long)Hq, (long long)Hkv);
+  BSA_REQUIRE(window >= 0 && (window == 0 || causal), "%s: a window needs the causal mask", what);
+  BSA_REQUIRE(!causal || Tq <= Tk, "%s: causal with more queries (%lld) than keys (%lld)", what, (long long)Tq,
+              (long long)Tk);
+  BSA_REQUIRE(B < 65536 && Hkv < 65536 && Tq * (Hq / Hkv) < INT32_MAX / 2 && Tk < INT32_MAX / 2 && window < INT32_MAX,
+              "%s: too large", what);
+  return BSA_OK;
+}
+
+static int at_check_strides(const char* what, const int64_t* const* st, int n) {
+  for (int j = 0; j < n; ++j)
+    for (int i = 0; i < 3; ++i)
+      BSA_REQUIRE(st[j][i] % 8 == 0 && st[j][i] >= 0,
+                  "%s: strides (batch, sequence, head) must be non-negative multiples of 8 elements", what);
+  return BSA_OK;
+}
+
+static inline bool at_al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 }  // namespace bsa
 
@@ -282,22 +715,12 @@ extern "C" int bsa_attention_fwd(const void* q, const int64_t* q_strides, const 
   BSA_REQUIRE(B >= 0 && Tq >= 0 && Tk >= 0 && Hq > 0 && Hkv > 0, "attention: bad shape");
   if (B == 0 || Tq == 0) return BSA_OK;
   BSA_REQUIRE(Tk > 0, "attention: queries without keys");
-  BSA_REQUIRE(head_dim == AT_D, "attention: head_dim must be %d (got %lld)", AT_D, (long long)head_dim);
-  BSA_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= 64, "attention: Hq (%lld) must be a multiple of Hkv (%lld), at most 64x",
-              (long long)Hq, (long long)Hkv);
   BSA_REQUIRE(q && k && v && out && q_strides && k_strides && v_strides && out_strides, "attention: null pointer");
-  BSA_REQUIRE(window >= 0 && (window == 0 || causal), "attention: a window needs the causal mask");
-  BSA_REQUIRE(!causal || Tq <= Tk, "attention: causal with more queries (%lld) than keys (%lld)", (long long)Tq,
-              (long long)Tk);
-  BSA_REQUIRE(B < 65536 && Hkv < 65536 && Tq * (Hq / Hkv) < INT32_MAX / 2 && Tk < INT32_MAX / 2 &&
-                  window < INT32_MAX,
-              "attention: too large");
-  auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-  BSA_REQUIRE(al16(q) && al16(k) && al16(v) && al16(out), "attention: q, k, v and out must be 16-byte aligned");
-  for (int i = 0; i < 3; ++i)
-    BSA_REQUIRE(q_strides[i] % 8 == 0 && k_strides[i] % 8 == 0 && v_strides[i] % 8 == 0 && out_strides[i] % 8 == 0 &&
-                    q_strides[i] >= 0 && k_strides[i] >= 0 && v_strides[i] >= 0 && out_strides[i] >= 0,
-                "attention: strides (batch, sequence, head) must be non-negative multiples of 8 elements");
+  int rc = at_check_common("attention", B, Tq, Tk, Hq, Hkv, head_dim, causal, window);
+  if (rc) return rc;
+  BSA_REQUIRE(at_al16(q) && at_al16(k) && at_al16(v) && at_al16(out), "attention: q, k, v and out must be 16-byte aligned");
+  const int64_t* st[4] = {q_strides, k_strides, v_strides, out_strides};
+  if ((rc = at_check_strides("attention", st, 4))) return rc;
   AttnArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k);
@@ -317,426 +740,32 @@ extern "C" int bsa_attention_fwd(const void* q, const int64_t* q_strides, const 
   a.window = (int)window;
   a.scale2 = scaling * 1.4426950408889634f;
   const int64_t rblocks = (Tq * a.G + AT_BR - 1) / AT_BR;
-  BSA_REQUIRE(rblocks < INT32_MAX, "attention: too many rows");
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)rblocks, (unsigned)Hkv, (unsigned)B), dim3(256), 0,
+  if ((rc = at_allow_lds(reinterpret_cast<const void*>(attn_fwd_kernel), 0, AT_FWD_LDS))) return rc;
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)rblocks, (unsigned)Hkv, (unsigned)B), dim3(256), AT_FWD_LDS,
                      static_cast<hipStream_t>(stream), a);
   BSA_LAUNCH_CHECK("attention launch");
   return BSA_OK;
 }
-
-namespace bsa {
-
-// ---------------------------------------------------------------------------
-// Backward (the gradients autograd takes through eager_attention_forward,
-// modeling_gpt_oss.py:235-264), from the forward's log2 denominators L:
-//   p[t, j]  = 2^(S[t, j] * scaling * log2(e) - L[t])      (visible j, else 0)
-//   D[t]     = dO[t] . O[t]       (= sum_j p dP: the sink has no value row)
-//   dP[t, j] = dO[t] . v[j],   dS[t, j] = p (dP - D[t])
-//   dq[t] = scaling * sum_j dS k[j],  dk[j] = scaling * sum_t dS q[t],
-//   dv[j] = sum_t p[t, j] dO[t]
-//   d sink[h] = -sum_t p_sink[t] D[t],  p_sink = 2^(sink log2(e) - L[t])
-// Two kernels, no atomics: attn_bwd_dq (the forward's row blocks, writing D)
-// and attn_bwd_dkv (blocks of 128 keys, every row that sees them).
-// ---------------------------------------------------------------------------
-struct AttnBwdArgs {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
-  const uint16_t* o;    // forward output [B, Tq, Hq, 64] (strides so, like out)
-  const uint16_t* dout; // [B, Tq, Hq, 64] (strides sd)
-  const float* lse;     // [B][Hq][Tq]
-  float* drow;          // [B][Hq][Tq]: D, written by attn_bwd_dq, read by attn_bwd_dkv
-  uint16_t* dq;         // [B, Tq, Hq, 64] contiguous
-  uint16_t* dk;         // [B, Tk, Hkv, 64] contiguous
-  uint16_t* dv;
-  int64_t sqb, sqt, sqh, skb, skt, skh, svb, svt, svh, sob, sot, soh, sdb, sdt, sdh;
-  int Tq, Tk, Hq, Hkv, G;
-  int causal, window;
-  float scale2, scaling;
-};
-
-__device__ __forceinline__ bool at_visible(const AttnBwdArgs& a, int j, int qpos) {
-  return j < a.Tk && (!a.causal || j <= qpos) && (a.window <= 0 || j > qpos - a.window);
-}
-
-// 16 bf16 of a u32x4 pair -> float dot with another pair
-__device__ __forceinline__ float at_dot8(const u32x4_t& x, const u32x4_t& y) {
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    s += __uint_as_float(x[i] << 16) * __uint_as_float(y[i] << 16) +
-         __uint_as_float(x[i] & 0xFFFF0000u) * __uint_as_float(y[i] & 0xFFFF0000u);
-  return s;
-}
-
-// dq: the forward's row blocks.  LDS per buffer: K (S^T operand), V (dP^T
-// operand: dP^T = V dO^T, V rows permuted like K), K^T (dq^T = K^T dS^T).
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdArgs a) {
-  __shared__ __align__(16) uint8_t sK[2][AT_TILE];
-  __shared__ __align__(16) uint8_t sV[2][AT_TILE];
-  __shared__ __align__(16) uint8_t sKt[2][AT_TILE];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int c = lane & 31;
-  const int g = lane >> 5;
-  const int rb = (int)gridDim.x - 1 - (int)blockIdx.x;
-  const int hk = blockIdx.y;
-  const int b = blockIdx.z;
-  const int rows = a.Tq * a.G;
-  const int R0 = rb * AT_BR;
-  const int R = min(R0 + 32 * wave + c, rows - 1);
-  const int t = R / a.G;
-  const int h = hk * a.G + (R - t * a.G);
-  const int qpos = a.Tk - a.Tq + t;
-  const int Rl = min(R0 + AT_BR, rows) - 1;
-  const int pos_first = a.Tk - a.Tq + R0 / a.G;
-  const int pos_last = a.Tk - a.Tq + Rl / a.G;
-  const int j_end = a.causal ? min(a.Tk, pos_last + 1) : a.Tk;
-  const int j_begin = a.window > 0 ? max(0, pos_first - a.window + 1) : 0;
-  const int kt0 = j_begin / AT_BC;
-  const int kt1 = (j_end + AT_BC - 1) / AT_BC;
-
-  // row operands: q and dO (B operands, d 16s + 8g ..), D = dO . O
-  const uint16_t* qrow = a.q + b * a.sqb + (int64_t)t * a.sqt + (int64_t)h * a.sqh;
-  const uint16_t* drow_p = a.dout + b * a.sdb + (int64_t)t * a.sdt + (int64_t)h * a.sdh;
-  const uint16_t* orow = a.o + b * a.sob + (int64_t)t * a.sot + (int64_t)h * a.soh;
-  u32x4_t qf[4], df[4];
-  float D = 0.f;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    qf[s] = *reinterpret_cast<const u32x4_t*>(qrow + 16 * s + 8 * g);
-    df[s] = *reinterpret_cast<const u32x4_t*>(drow_p + 16 * s + 8 * g);
-    D += at_dot8(df[s], *reinterpret_cast<const u32x4_t*>(orow + 16 * s + 8 * g));
-  }
-  D += __shfl_xor(D, 32);
-  const int64_t rowi = ((int64_t)b * a.Hq + h) * a.Tq + t;
-  const float L = a.lse[rowi];
-  if (g == 0 && R0 + 32 * wave + c < rows) a.drow[rowi] = D;
-
-  const uint16_t* kbase = a.k + b * a.skb + (int64_t)hk * a.skh;
-  const uint16_t* vbase = a.v + b * a.svb + (int64_t)hk * a.svh;
-  auto issue_kv = [&](int kt, int buf) {
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int row = 32 * m + 8 * wave + (lane >> 3);
-      const int ch = (lane & 7) ^ ((row >> 1) & 7);
-      const int j = min(kt * AT_BC + row, a.Tk - 1);
-      __builtin_amdgcn_global_load_lds(kbase + (int64_t)j * a.skt + ch * 8,
-                                       (lds_void*)(&sK[buf][0] + (256 * m + 64 * wave) * 16), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vbase + (int64_t)j * a.svt + ch * 8,
-                                       (lds_void*)(&sV[buf][0] + (256 * m + 64 * wave) * 16), 16, 0, 0);
-    }
-  };
-  u32x4_t kr[2];
-  auto load_kt = [&](int kt) {
-    const int j = min(kt * AT_BC + lane, a.Tk - 1);
-    const u32x4_t* p = reinterpret_cast<const u32x4_t*>(kbase + (int64_t)j * a.skt + 16 * wave);
-    kr[0] = p[0];
-    kr[1] = p[1];
-  };
-  auto store_kt = [&](int buf) {
-    uint8_t* base = &sKt[buf][0];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const uint32_t w = kr[i >> 3][(i & 7) >> 1];
-      *reinterpret_cast<uint16_t*>(base + at_off(16 * wave + i, lane >> 3) + (lane & 7) * 2) =
-          (uint16_t)((i & 1) ? (w >> 16) : (w & 0xFFFFu));
-    }
-  };
-  uint32_t koff[2][4], toff[2][4];
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      koff[kb][s] = at_off(32 * kb + at_pi(c), 2 * s + g);
-      toff[kb][s] = at_off(32 * kb + c, 2 * s + g);
-    }
-
-  f32x16_t dq[2];
-#pragma unroll
-  for (int db = 0; db < 2; ++db)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) dq[db][v] = 0.f;
-
-  if (kt0 < kt1) {
-    load_kt(kt0);
-    issue_kv(kt0, 0);
-  }
-  for (int kt = kt0; kt < kt1; ++kt) {
-    const int buf = (kt - kt0) & 1;
-    store_kt(buf);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();
-    if (kt + 1 < kt1) {
-      load_kt(kt + 1);
-      issue_kv(kt + 1, buf ^ 1);
-    }
-    const uint8_t* K = &sK[buf][0];
-    const uint8_t* V = &sV[buf][0];
-    const uint8_t* Kt = &sKt[buf][0];
-    f32x16_t sc[2], dp[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) sc[kb][v] = dp[kb][v] = 0.f;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        sc[kb] = at_mfma(*reinterpret_cast<const u32x4_t*>(K + koff[kb][s]), qf[s], sc[kb]);
-        dp[kb] = at_mfma(*reinterpret_cast<const u32x4_t*>(V + koff[kb][s]), df[s], dp[kb]);
-      }
-    }
-    const int j0 = kt * AT_BC;
-    const bool full = j0 + AT_BC <= a.Tk && (!a.causal || j0 + AT_BC - 1 <= pos_first) &&
-                      (a.window <= 0 || j0 > pos_last - a.window);
-    u32x4_t sf[4];  // dS^T operands of the four 16-key steps
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        float ds[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int v = 8 * half + i;
-          float p = __builtin_amdgcn_exp2f(sc[kb][v] * a.scale2 - L);
-          if (!full) {
-            const int j = j0 + 32 * kb + (v < 8 ? 8 * g + v : 16 + 8 * g + v - 8);
-            p = at_visible(a, j, qpos) ? p : 0.f;
-          }
-          ds[i] = p * (dp[kb][v] - D);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sf[2 * kb + half][i] = pack_bf16x2(ds[2 * i], ds[2 * i + 1]);
-      }
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        dq[db] = at_mfma(*reinterpret_cast<const u32x4_t*>(Kt + toff[db][s]), sf[s], dq[db]);
-  }
-
-  if (R0 + 32 * wave + c >= rows) return;
-  uint16_t* out = a.dq + (((int64_t)b * a.Tq + t) * a.Hq + h) * AT_D;
-#pragma unroll
-  for (int db = 0; db < 2; ++db)
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int d = 32 * db + 8 * q4 + 4 * g;
-      uint2 w;
-      w.x = pack_bf16x2(dq[db][4 * q4] * a.scaling, dq[db][4 * q4 + 1] * a.scaling);
-      w.y = pack_bf16x2(dq[db][4 * q4 + 2] * a.scaling, dq[db][4 * q4 + 3] * a.scaling);
-      *reinterpret_cast<uint2*>(out + d) = w;
-    }
-}
-
-// Byte offset of 16-byte chunk `ch` of row `row` in a 64-byte-row LDS tile
-// (16 rows span 1 KiB; the swizzle spreads the four 256-byte groups).
-__device__ __forceinline__ uint32_t at_off64(int row, int ch) {
-  return (uint32_t)(row * 64 + ((ch ^ ((row >> 2) & 3)) << 4));
-}
-
-constexpr int AT_KB = 128;  // keys per dk/dv workgroup (32 per wave)
-constexpr int AT_RT = 32;   // rows per step of the dk/dv loop
-
-// dk, dv: workgroups of 128 keys of one (batch, key head); wave w keeps keys
-// 32w .. 32w+31 (their k and v rows as the B operands of S = Q K^T and
-// dP = dO V^T, lane c = key c) and their dk^T, dv^T accumulators.  The
-// workgroup walks 32-row steps (rows R = t * G + i as in the forward) of
-// every row that sees one of its keys; a step's q and dO rows are staged in
-// LDS twice: natural [32][64] (the A operands, rows permuted by pi) and
-// transposed [64][32] (dv^T += dO^T P, dk^T += q^T dS), with L and D.
-__global__ __launch_bounds__(256, 2) void attn_bwd_dkv_kernel(AttnBwdArgs a) {
-  constexpr int NAT = AT_RT * AT_D * 2;  // 4 KiB
-  __shared__ __align__(16) uint8_t sQ[2][NAT];
-  __shared__ __align__(16) uint8_t sD[2][NAT];
-  __shared__ __align__(16) uint8_t sQt[2][NAT];
-  __shared__ __align__(16) uint8_t sDt[2][NAT];
-  __shared__ __align__(16) float sL[2][AT_RT];
-  __shared__ __align__(16) float sDr[2][AT_RT];
-  __shared__ int sPos[2][AT_RT];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int c = lane & 31;
-  const int g = lane >> 5;
-  const int hk = blockIdx.y;
-  const int b = blockIdx.z;
-  const int j0 = blockIdx.x * AT_KB;
-  const int rows = a.Tq * a.G;
-  const int off = a.Tk - a.Tq;  // position of query 0
-
-  // rows that see a key of [j0, j0 + 128)
-  int t_begin = 0, t_end = a.Tq;
-  if (a.causal) {
-    t_begin = max(0, j0 - off);
-    if (a.window > 0) t_end = min(a.Tq, j0 + AT_KB - 1 + a.window - off);
-  }
-  const int r_begin = t_begin * a.G;
-  const int r_end = max(r_begin, t_end * a.G);
-  const int nsteps = (r_end - r_begin + AT_RT - 1) / AT_RT;
-
-  // this lane's key: B operands k and v (d 16s + 8g ..)
-  const int jk = j0 + 32 * wave + c;
-  const int jc = min(jk, a.Tk - 1);
-  const uint16_t* krow = a.k + b * a.skb + (int64_t)jc * a.skt + (int64_t)hk * a.skh;
-  const uint16_t* vrow = a.v + b * a.svb + (int64_t)jc * a.svt + (int64_t)hk * a.svh;
-  u32x4_t kf[4], vf[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    kf[s] = *reinterpret_cast<const u32x4_t*>(krow + 16 * s + 8 * g);
-    vf[s] = *reinterpret_cast<const u32x4_t*>(vrow + 16 * s + 8 * g);
-  }
-
-  // staging: thread = (row r = tid & 31, d chunk dc = tid >> 5), 16 bytes of q and dO
-  const int sr = tid & 31;
-  const int sdc = tid >> 5;
-  u32x4_t rq, rd;
-  float rl = 0.f, rdr = 0.f;
-  int rpos = 0;
-  auto load_rows = [&](int step) {
-    const int Rr = min(r_begin + step * AT_RT + sr, rows - 1);
-    const int tt = Rr / a.G;
-    const int hh = hk * a.G + (Rr - tt * a.G);
-    rq = *reinterpret_cast<const u32x4_t*>(a.q + b * a.sqb + (int64_t)tt * a.sqt + (int64_t)hh * a.sqh + 8 * sdc);
-    rd = *reinterpret_cast<const u32x4_t*>(a.dout + b * a.sdb + (int64_t)tt * a.sdt + (int64_t)hh * a.sdh +
-                                           8 * sdc);
-    if (sdc == 0) {
-      const int64_t ri = ((int64_t)b * a.Hq + hh) * a.Tq + tt;
-      // rows past the end get an infinite L: p = 0
-      const bool live = r_begin + step * AT_RT + sr < r_end;
-      rl = live ? a.lse[ri] : INFINITY;
-      rdr = a.drow[ri];
-      rpos = off + tt;
-    }
-  };
-  auto store_rows = [&](int buf) {
-    *reinterpret_cast<u32x4_t*>(&sQ[buf][0] + at_off(sr, sdc)) = rq;
-    *reinterpret_cast<u32x4_t*>(&sD[buf][0] + at_off(sr, sdc)) = rd;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint16_t xq = (uint16_t)((i & 1) ? (rq[i >> 1] >> 16) : (rq[i >> 1] & 0xFFFFu));
-      const uint16_t xd = (uint16_t)((i & 1) ? (rd[i >> 1] >> 16) : (rd[i >> 1] & 0xFFFFu));
-      const uint32_t o = at_off64(8 * sdc + i, sr >> 3) + (sr & 7) * 2;
-      *reinterpret_cast<uint16_t*>(&sQt[buf][0] + o) = xq;
-      *reinterpret_cast<uint16_t*>(&sDt[buf][0] + o) = xd;
-    }
-    if (sdc == 0) {
-      sL[buf][sr] = rl;
-      sDr[buf][sr] = rdr;
-      sPos[buf][sr] = rpos;
-    }
-  };
-
-  // A operands: natural rows pi(c), d chunk 2s + g; transposed rows 32db + c, row chunk s' * 2 + g
-  uint32_t aoff[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) aoff[s] = at_off(at_pi(c), 2 * s + g);
-  uint32_t toff[2][2];
-#pragma unroll
-  for (int db = 0; db < 2; ++db)
-#pragma unroll
-    for (int s = 0; s < 2; ++s) toff[db][s] = at_off64(32 * db + c, 2 * s + g);
-
-  f32x16_t dk[2], dv[2];
-#pragma unroll
-  for (int db = 0; db < 2; ++db)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) dk[db][v] = dv[db][v] = 0.f;
-
-  if (nsteps > 0) load_rows(0);
-  for (int st = 0; st < nsteps; ++st) {
-    const int buf = st & 1;
-    store_rows(buf);
-    __syncthreads();
-    if (st + 1 < nsteps) load_rows(st + 1);
-    f32x16_t sc, dp;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) sc[v] = dp[v] = 0.f;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      sc = at_mfma(*reinterpret_cast<const u32x4_t*>(&sQ[buf][0] + aoff[s]), kf[s], sc);
-      dp = at_mfma(*reinterpret_cast<const u32x4_t*>(&sD[buf][0] + aoff[s]), vf[s], dp);
-    }
-    // register v: row 8g + v (v < 8) or 16 + 8g + v - 8 of the step, key c
-    u32x4_t pf[2], sf[2];
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      float p[8], ds[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int v = 8 * half + i;
-        const int r = 16 * half + 8 * g + i;
-        float x = __builtin_amdgcn_exp2f(sc[v] * a.scale2 - sL[buf][r]);
-        const int qp = sPos[buf][r];
-        x = (jk < a.Tk && (!a.causal || jk <= qp) && (a.window <= 0 || jk > qp - a.window)) ? x : 0.f;
-        p[i] = x;
-        ds[i] = x * (dp[v] - sDr[buf][r]);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        pf[half][i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
-        sf[half][i] = pack_bf16x2(ds[2 * i], ds[2 * i + 1]);
-      }
-    }
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        dv[db] = at_mfma(*reinterpret_cast<const u32x4_t*>(&sDt[buf][0] + toff[db][s]), pf[s], dv[db]);
-        dk[db] = at_mfma(*reinterpret_cast<const u32x4_t*>(&sQt[buf][0] + toff[db][s]), sf[s], dk[db]);
-      }
-    // the next step's staging writes the other buffer; this one is rewritten
-    // two steps on, after the next barrier
-  }
-
-  if (jk >= a.Tk) return;
-  uint16_t* okr = a.dk + (((int64_t)b * a.Tk + jk) * a.Hkv + hk) * AT_D;
-  uint16_t* ovr = a.dv + (((int64_t)b * a.Tk + jk) * a.Hkv + hk) * AT_D;
-#pragma unroll
-  for (int db = 0; db < 2; ++db)
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int d = 32 * db + 8 * q4 + 4 * g;
-      uint2 wk, wv;
-      wk.x = pack_bf16x2(dk[db][4 * q4] * a.scaling, dk[db][4 * q4 + 1] * a.scaling);
-      wk.y = pack_bf16x2(dk[db][4 * q4 + 2] * a.scaling, dk[db][4 * q4 + 3] * a.scaling);
-      wv.x = pack_bf16x2(dv[db][4 * q4], dv[db][4 * q4 + 1]);
-      wv.y = pack_bf16x2(dv[db][4 * q4 + 2], dv[db][4 * q4 + 3]);
-      *reinterpret_cast<uint2*>(okr + d) = wk;
-      *reinterpret_cast<uint2*>(ovr + d) = wv;
-    }
-}
-
-}  // namespace bsa
 
 extern "C" int bsa_attention_bwd(const void* grad_out, const int64_t* grad_strides, const void* q,
                                  const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
                                  const int64_t* v_strides, const void* out, const int64_t* out_strides,
                                  const float* lse, int64_t B, int64_t Tq, int64_t Tk, int64_t Hq, int64_t Hkv,
                                  int64_t head_dim, int causal, int64_t window, float scaling, void* grad_q,
-                                 void* grad_k, void* grad_v, float* row_dot, void* stream) {
+                                 void* grad_k, void* grad_v, float* row_stats, void* stream) {
   clear_error();
   BSA_REQUIRE(B >= 0 && Tq >= 0 && Tk >= 0 && Hq > 0 && Hkv > 0, "attention bwd: bad shape");
   if (B == 0 || Tq == 0 || Tk == 0) return BSA_OK;
-  BSA_REQUIRE(head_dim == AT_D, "attention bwd: head_dim must be %d (got %lld)", AT_D, (long long)head_dim);
-  BSA_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= 64, "attention bwd: Hq must be a multiple of Hkv, at most 64x");
-  BSA_REQUIRE(grad_out && q && k && v && out && lse && grad_q && grad_k && grad_v && row_dot && grad_strides &&
+  BSA_REQUIRE(grad_out && q && k && v && out && lse && grad_q && grad_k && grad_v && row_stats && grad_strides &&
                   q_strides && k_strides && v_strides && out_strides,
               "attention bwd: null pointer");
-  BSA_REQUIRE(window >= 0 && (window == 0 || causal), "attention bwd: a window needs the causal mask");
-  BSA_REQUIRE(!causal || Tq <= Tk, "attention bwd: causal with more queries than keys");
-  BSA_REQUIRE(B < 65536 && Hkv < 65536 && Tq * (Hq / Hkv) < INT32_MAX / 2 && Tk < INT32_MAX / 2 &&
-                  window < INT32_MAX,
-              "attention bwd: too large");
-  auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-  BSA_REQUIRE(al16(grad_out) && al16(q) && al16(k) && al16(v) && al16(out) && al16(grad_q) && al16(grad_k) &&
-                  al16(grad_v),
+  int rc = at_check_common("attention bwd", B, Tq, Tk, Hq, Hkv, head_dim, causal, window);
+  if (rc) return rc;
+  BSA_REQUIRE(at_al16(grad_out) && at_al16(q) && at_al16(k) && at_al16(v) && at_al16(out) && at_al16(grad_q) &&
+                  at_al16(grad_k) && at_al16(grad_v) && at_al16(row_stats),
               "attention bwd: tensors must be 16-byte aligned");
   const int64_t* st[5] = {grad_strides, q_strides, k_strides, v_strides, out_strides};
-  for (int n = 0; n < 5; ++n)
-    for (int i = 0; i < 3; ++i)
-      BSA_REQUIRE(st[n][i] % 8 == 0 && st[n][i] >= 0,
-                  "attention bwd: strides (batch, sequence, head) must be non-negative multiples of 8 elements");
+  if ((rc = at_check_strides("attention bwd", st, 5))) return rc;
   AttnBwdArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k);
@@ -744,7 +773,7 @@ extern "C" int bsa_attention_bwd(const void* grad_out, const int64_t* grad_strid
   a.o = static_cast<const uint16_t*>(out);
   a.dout = static_cast<const uint16_t*>(grad_out);
   a.lse = lse;
-  a.drow = row_dot;
+  a.stats = row_stats;
   a.dq = static_cast<uint16_t*>(grad_q);
   a.dk = static_cast<uint16_t*>(grad_k);
   a.dv = static_cast<uint16_t*>(grad_v);
@@ -764,10 +793,18 @@ extern "C" int bsa_attention_bwd(const void* grad_out, const int64_t* grad_strid
   a.scaling = scaling;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t rblocks = (Tq * a.G + AT_BR - 1) / AT_BR;
-  hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3((unsigned)rblocks, (unsigned)Hkv, (unsigned)B), dim3(256), 0, s, a);
+  if ((rc = at_allow_lds(reinterpret_cast<const void*>(attn_bwd_dq_kernel), 1, AT_FWD_LDS))) return rc;
+  hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3((unsigned)rblocks, (unsigned)Hkv, (unsigned)B), dim3(256), AT_FWD_LDS, s,
+                     a);
   BSA_LAUNCH_CHECK("attention bwd (dq) launch");
-  const int64_t kblocks = (Tk + AT_KB - 1) / AT_KB;
-  hipLaunchKernelGGL(attn_bwd_dkv_kernel, dim3((unsigned)kblocks, (unsigned)Hkv, (unsigned)B), dim3(256), 0, s, a);
+  const int nkb = (int)((Tk + AT_KB - 1) / AT_KB);
+  // causal without a window: a key block's row count falls linearly with its
+  // index, so blocks x and nkb - 1 - x share a workgroup
+  a.kpairs = (causal && window == 0 && nkb > 1) ? 1 : 0;
+  const int kgrid = a.kpairs ? (nkb + 1) / 2 : nkb;
+  if ((rc = at_allow_lds(reinterpret_cast<const void*>(attn_bwd_dkv_kernel), 2, AT_DKV_LDS))) return rc;
+  hipLaunchKernelGGL(attn_bwd_dkv_kernel, dim3((unsigned)kgrid, (unsigned)Hkv, (unsigned)B), dim3(256), AT_DKV_LDS, s,
+                     a);
   BSA_LAUNCH_CHECK("attention bwd (dk, dv) launch");
   return BSA_OK;
 }

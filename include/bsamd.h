@@ -449,9 +449,10 @@ int bsa_attention_fwd(const void *q, const int64_t *q_strides, const void *k,
  *   grad_v = sum_t p grad_out,  with dP[t, j] = grad_out[t] . v[j].
  * grad_out and out [B, Tq, Hq, 64] and q, k, v as for the forward (strides
  * per tensor); grad_q [B, Tq, Hq, 64], grad_k and grad_v [B, Tk, Hkv, 64]
- * contiguous bf16; row_dot float32 [B, Hq, Tq] receives D, from which the
- * sinks' gradient is -sum_t 2^(sink log2(e) - lse) D.  Two launches, no
- * atomics (results are deterministic).
+ * contiguous bf16; row_stats float32 [B, Hkv, Tq * G, 2] (G = Hq / Hkv)
+ * receives (lse, D) of row R = t * G + i, query t of head G * hk + i, from
+ * which the sinks' gradient is -sum_t 2^(sink log2(e) - lse) D.  Two
+ * launches, no atomics (results are deterministic).
  */
 int bsa_attention_bwd(const void *grad_out, const int64_t *grad_strides,
                       const void *q, const int64_t *q_strides, const void *k,
@@ -461,7 +462,7 @@ int bsa_attention_bwd(const void *grad_out, const int64_t *grad_strides,
                       int64_t Tq, int64_t Tk, int64_t Hq, int64_t Hkv,
                       int64_t head_dim, int causal, int64_t window,
                       float scaling, void *grad_q, void *grad_k, void *grad_v,
-                      float *row_dot, void *stream);
+                      float *row_stats, void *stream);
 
 #ifdef __cplusplus
 }
