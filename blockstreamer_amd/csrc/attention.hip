@@ -52,7 +52,10 @@ constexpr int AT_D = 64;                    // head dimension
 constexpr int AT_BR = 128;                  // rows per workgroup (forward, dq)
 constexpr int AT_BC = 64;                   // keys per tile
 constexpr int AT_TILE = AT_BC * AT_D * 2;   // 8 KiB
-constexpr int AT_NS = 4;                    // ring stages
+#ifndef BSA_AT_NS
+#define BSA_AT_NS 2
+#endif
+constexpr int AT_NS = BSA_AT_NS;            // ring stages
 
 struct AttnArgs {
   const uint16_t* q;
@@ -485,24 +488,30 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdArgs a) {
     }
 }
 
-constexpr int AT_KB = 128;  // keys per dk/dv block (32 per wave)
+constexpr int AT_KB = 128;  // keys per dk/dv block (32 per key-wave)
 constexpr int AT_RT = 64;   // rows per step of the dk/dv loop (a tile)
-constexpr int AT_DKV_STAGE = 2 * AT_TILE + 4 * 512;  // q tile, dO tile, a (L, D) copy per wave
+constexpr int AT_DKV_STAGE = 2 * AT_TILE + 8 * 256;  // q tile, dO tile, each wave's (L, D) of its 32 rows
+constexpr int AT_DKV_RED = 4 * 64 * 32 * 4;          // row-wave 1's dk or dv partials (4 waves x 64 lanes x 32 floats)
 
-// dk, dv: key blocks of 128 keys of one (batch, key head), wave w keeping
-// keys 32w .. 32w+31 (their k and v rows as the B operands of S = Q K^T and
-// dP = dO V^T, lane c = key c) and their dk^T, dv^T accumulators.  The
-// workgroup walks 64-row tiles (rows R = t * G + i as in the forward) of
-// every row that sees one of its keys, through a DMA ring: the q and dO
-// tiles (rows permuted as A operands; q^T and dO^T by transposing reads for
-// dv^T += dO^T P and dk^T += q^T dS) and the tile's (L, D) pairs.  Under a
-// causal mask without a window, workgroup x takes key block x and then block
-// nblocks - 1 - x, so every workgroup walks about the same number of rows.
-__global__ __launch_bounds__(256, 2) void attn_bwd_dkv_kernel(AttnBwdArgs a) {
-  extern __shared__ __align__(1024) uint8_t at_smem[];  // AT_NS stages
+// dk, dv: key blocks of 128 keys of one (batch, key head); eight waves,
+// key-wave kw = w % 4 keeping keys 32 kw .. 32 kw + 31 (their k and v rows as
+// the B operands of S = Q K^T and dP = dO V^T, lane c = key c) and row-wave
+// rw = w / 4 taking rows 32 rw .. 32 rw + 31 of each 64-row tile.  The
+// workgroup walks the tiles (rows R = t * G + i as in the forward) of every
+// row that sees one of its keys, through a DMA ring: the q and dO tiles (rows
+// permuted as A operands; q^T and dO^T by transposing reads for
+// dv^T += dO^T P and dk^T += q^T dS) and (L, D) of each wave's rows.  At
+// the end the two row-waves of a key-wave add their dk^T and dv^T through
+// LDS.  Under a causal mask without a window, workgroup x takes key block x
+// and then block nblocks - 1 - x, so every workgroup walks about the same
+// number of rows.
+__global__ __launch_bounds__(512, 1) void attn_bwd_dkv_kernel(AttnBwdArgs a) {
+  extern __shared__ __align__(1024) uint8_t at_smem[];  // AT_NS stages, reused for the reduction
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int kw = wave & 3;
+  const int rw = wave >> 2;
   const int c = lane & 31;
   const int g = lane >> 5;
   const int hk = blockIdx.y;
@@ -514,15 +523,17 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_kernel(AttnBwdArgs a) {
   const uint16_t* dbase = a.dout + b * a.sdb;
   const float* sbase = a.stats + ((int64_t)b * a.Hkv + hk) * rows * 2;
 
+  // A operands: rows 32 rw + pi(c) at d chunk 2s + g; transposing reads of
+  // rows 32 rw + 16 s + ... (s the 16-row step)
   uint32_t aoff[4], toff[2][2][2];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) aoff[s] = at_off(at_pi(c), 2 * s + g);
+  for (int s = 0; s < 4; ++s) aoff[s] = at_off(32 * rw + at_pi(c), 2 * s + g);
 #pragma unroll
   for (int s = 0; s < 2; ++s)
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) toff[s][db][h] = at_tr_off(lane, s, h, db);
+      for (int h = 0; h < 2; ++h) toff[s][db][h] = at_tr_off(lane, 2 * rw + s, h, db);
 
   for (int pass = 0; pass < (a.kpairs ? 2 : 1); ++pass) {
     const int kbk = pass == 0 ? (int)blockIdx.x : nkb - 1 - (int)blockIdx.x;
@@ -538,7 +549,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_kernel(AttnBwdArgs a) {
     const int r_end = max(r_begin, t_end * a.G);
     const int nt = (r_end - r_begin + AT_RT - 1) / AT_RT;
 
-    const int jk = j0 + 32 * wave + c;
+    const int jk = j0 + 32 * kw + c;
     const int jc = min(jk, a.Tk - 1);
     const uint16_t* krow = a.k + b * a.skb + (int64_t)jc * a.skt + (int64_t)hk * a.skh;
     const uint16_t* vrow = a.v + b * a.svb + (int64_t)jc * a.svt + (int64_t)hk * a.svh;
@@ -548,34 +559,25 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_kernel(AttnBwdArgs a) {
       kf[s] = *reinterpret_cast<const u32x4_t*>(krow + 16 * s + 8 * g);
       vf[s] = *reinterpret_cast<const u32x4_t*>(vrow + 16 * s + 8 * g);
     }
-    // tile i: rows r_begin + 64 i + row -> q / dO row of (t = R / G, head
-    // hk G + R % G), each lane its own source row (lanes of a group of 8
-    // share one), clamped to the last row
+    // tile i: wave w fills rows 8w + lane / 8 of the q and dO tiles (source
+    // row of t = R / G, head hk G + R % G, clamped to the last row) and its
+    // own copy of (L, D) of rows 32 rw .. 32 rw + 31
     auto issue = [&](int i) {
       uint8_t* st = at_smem + (i % AT_NS) * AT_DKV_STAGE;
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const int row = 32 * m + 8 * wave + (lane >> 3);
-        const int ch = (lane & 7) ^ at_sw(row);
-        const int R = min(r_begin + i * AT_RT + row, rows - 1);
-        const int t = R / a.G;
-        const int h = hk * a.G + (R - t * a.G);
-        __builtin_amdgcn_global_load_lds(qbase + (int64_t)t * a.sqt + (int64_t)h * a.sqh + ch * 8,
-                                         (lds_void*)(st + (256 * m + 64 * wave) * 16), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(dbase + (int64_t)t * a.sdt + (int64_t)h * a.sdh + ch * 8,
-                                         (lds_void*)(st + AT_TILE + (256 * m + 64 * wave) * 16), 16, 0, 0);
-      }
-      // the tile's 64 (L, D) pairs: float 2 r + (lane & 1) of rows
-      // r = lane / 2 (first instruction) and 32 + lane / 2 (second), one copy
-      // per wave
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const int R = min(r_begin + i * AT_RT + 32 * m + (lane >> 1), rows - 1);
-        __builtin_amdgcn_global_load_lds(sbase + (int64_t)R * 2 + (lane & 1),
-                                         (lds_void*)(st + 2 * AT_TILE + wave * 512 + m * 256), 4, 0, 0);
-      }
+      const int row = 8 * wave + (lane >> 3);
+      const int ch = (lane & 7) ^ at_sw(row);
+      const int R = min(r_begin + i * AT_RT + row, rows - 1);
+      const int t = R / a.G;
+      const int h = hk * a.G + (R - t * a.G);
+      __builtin_amdgcn_global_load_lds(qbase + (int64_t)t * a.sqt + (int64_t)h * a.sqh + ch * 8,
+                                       (lds_void*)(st + 64 * wave * 16), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(dbase + (int64_t)t * a.sdt + (int64_t)h * a.sdh + ch * 8,
+                                       (lds_void*)(st + AT_TILE + 64 * wave * 16), 16, 0, 0);
+      const int Rs = min(r_begin + i * AT_RT + 32 * rw + (lane >> 1), rows - 1);
+      __builtin_amdgcn_global_load_lds(sbase + (int64_t)Rs * 2 + (lane & 1),
+                                       (lds_void*)(st + 2 * AT_TILE + wave * 256), 4, 0, 0);
     };
-    constexpr int DPT = 6;
+    constexpr int DPT = 3;
 
     f32x16_t dk[2], dv[2];
 #pragma unroll
@@ -583,8 +585,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_kernel(AttnBwdArgs a) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) dk[db][v] = dv[db][v] = 0.f;
 
-    // every wave is done with the previous pass's stages (and its k, v
-    // loads have landed) before they are refilled
+    // every wave is done with the previous pass's stages and reduction
+    // buffer (and its k, v loads have landed) before they are refilled
     __syncthreads();
     for (int i = 0; i < AT_NS - 1; ++i)
       if (i < nt) issue(i);
@@ -594,52 +596,83 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_kernel(AttnBwdArgs a) {
       if (it + AT_NS - 1 < nt) issue(it + AT_NS - 1);
       const uint8_t* Q = at_smem + (it % AT_NS) * AT_DKV_STAGE;
       const uint8_t* DO = Q + AT_TILE;
-      const float* ST = reinterpret_cast<const float*>(Q + 2 * AT_TILE + wave * 512);
-      const int rbase = r_begin + it * AT_RT;
+      const float* ST = reinterpret_cast<const float*>(Q + 2 * AT_TILE + wave * 256);
+      const int rbase = r_begin + it * AT_RT + 32 * rw;  // this wave's first row
+      // every row of the wave's half sees every key of the block
+      const bool full = rbase + 32 <= r_end && j0 + AT_KB <= a.Tk &&
+                        (!a.causal || off + rbase / a.G >= j0 + AT_KB - 1) &&
+                        (a.window <= 0 || off + (rbase + 31) / a.G - a.window < j0);
+      f32x16_t sc, dp;
 #pragma unroll
-      for (int rh = 0; rh < 2; ++rh) {  // the tile's two 32-row halves
-        f32x16_t sc, dp;
+      for (int v = 0; v < 16; ++v) sc[v] = dp[v] = 0.f;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) sc[v] = dp[v] = 0.f;
+      for (int s = 0; s < 4; ++s) {
+        sc = at_mfma(*reinterpret_cast<const u32x4_t*>(Q + aoff[s]), kf[s], sc);
+        dp = at_mfma(*reinterpret_cast<const u32x4_t*>(DO + aoff[s]), vf[s], dp);
+      }
+      // register v: row 8g + v (v < 8) or 16 + 8g + v - 8 of the half, key c
+      u32x4_t pf[2], sf[2];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          sc = at_mfma(*reinterpret_cast<const u32x4_t*>(Q + aoff[s] + 4096 * rh), kf[s], sc);
-          dp = at_mfma(*reinterpret_cast<const u32x4_t*>(DO + aoff[s] + 4096 * rh), vf[s], dp);
-        }
-        // register v: row 32 rh + 8g + v (v < 8) or 32 rh + 16 + 8g + v - 8, key c
-        u32x4_t pf[2], sf[2];
+      for (int half = 0; half < 2; ++half) {
+        float p[8], ds[8];
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          float p[8], ds[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int r = 32 * rh + 16 * half + 8 * g + i;
-            const float2 sd = *reinterpret_cast<const float2*>(ST + 2 * r);
-            float x = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[8 * half + i], a.scale2, -sd.x));
+        for (int i = 0; i < 8; ++i) {
+          const int r = 16 * half + 8 * g + i;
+          const float2 sd = *reinterpret_cast<const float2*>(ST + 2 * r);
+          float x = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[8 * half + i], a.scale2, -sd.x));
+          if (!full) {
             const int R = rbase + r;
             const int qp = off + R / a.G;
-            const bool vis = R < r_end && jk < a.Tk && (!a.causal || jk <= qp) && (a.window <= 0 || jk > qp - a.window);
+            const bool vis =
+                R < r_end && jk < a.Tk && (!a.causal || jk <= qp) && (a.window <= 0 || jk > qp - a.window);
             x = vis ? x : 0.f;
-            p[i] = x;
-            ds[i] = x * (dp[8 * half + i] - sd.y);
           }
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            pf[half][i] = at_pack2(p[2 * i], p[2 * i + 1]);
-            sf[half][i] = at_pack2(ds[2 * i], ds[2 * i + 1]);
-          }
+          p[i] = x;
+          ds[i] = x * (dp[8 * half + i] - sd.y);
         }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pf[half][i] = at_pack2(p[2 * i], p[2 * i + 1]);
+          sf[half][i] = at_pack2(ds[2 * i], ds[2 * i + 1]);
+        }
+      }
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          dv[db] = at_mfma(at_tr8(DO, toff[s][db][0], toff[s][db][1]), pf[s], dv[db]);
+          dk[db] = at_mfma(at_tr8(Q, toff[s][db][0], toff[s][db][1]), sf[s], dk[db]);
+        }
+    }
+
+    // row-wave 1 hands its partial sums to row-wave 0 (dk, then dv)
+    float* red = reinterpret_cast<float*>(at_smem) + (kw * 64 + lane) * 32;
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+      f32x16_t* acc = which == 0 ? dk : dv;
+      __syncthreads();  // the ring (or the previous round) is no longer read
+      if (rw == 1) {
 #pragma unroll
         for (int db = 0; db < 2; ++db)
 #pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            dv[db] = at_mfma(at_tr8(DO + 4096 * rh, toff[s][db][0], toff[s][db][1]), pf[s], dv[db]);
-            dk[db] = at_mfma(at_tr8(Q + 4096 * rh, toff[s][db][0], toff[s][db][1]), sf[s], dk[db]);
+          for (int v4 = 0; v4 < 4; ++v4)
+            *reinterpret_cast<f32x4_t*>(red + 16 * db + 4 * v4) =
+                f32x4_t{acc[db][4 * v4], acc[db][4 * v4 + 1], acc[db][4 * v4 + 2], acc[db][4 * v4 + 3]};
+      }
+      __syncthreads();
+      if (rw == 0) {
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int v4 = 0; v4 < 4; ++v4) {
+            const f32x4_t x = *reinterpret_cast<const f32x4_t*>(red + 16 * db + 4 * v4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[db][4 * v4 + e] += x[e];
           }
       }
     }
 
-    if (jk < a.Tk) {
+    if (rw == 0 && jk < a.Tk) {
       uint16_t* okr = a.dk + (((int64_t)b * a.Tk + jk) * a.Hkv + hk) * AT_D;
       uint16_t* ovr = a.dv + (((int64_t)b * a.Tk + jk) * a.Hkv + hk) * AT_D;
 #pragma unroll
@@ -659,8 +692,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_kernel(AttnBwdArgs a) {
   }
 }
 
-constexpr int AT_FWD_LDS = AT_NS * 2 * AT_TILE;        // 64 KiB
-constexpr int AT_DKV_LDS = AT_NS * AT_DKV_STAGE;       // 72 KiB
+constexpr int AT_FWD_LDS = AT_NS * 2 * AT_TILE;
+constexpr int AT_DKV_LDS = AT_NS * AT_DKV_STAGE > AT_DKV_RED ? AT_NS * AT_DKV_STAGE : AT_DKV_RED;
 
 static int at_allow_lds(const void* fn, int idx, int bytes) {
   int dev = 0;
@@ -803,7 +836,7 @@ extern "C" int bsa_attention_bwd(const void* grad_out, const int64_t* grad_strid
   a.kpairs = (causal && window == 0 && nkb > 1) ? 1 : 0;
   const int kgrid = a.kpairs ? (nkb + 1) / 2 : nkb;
   if ((rc = at_allow_lds(reinterpret_cast<const void*>(attn_bwd_dkv_kernel), 2, AT_DKV_LDS))) return rc;
-  hipLaunchKernelGGL(attn_bwd_dkv_kernel, dim3((unsigned)kgrid, (unsigned)Hkv, (unsigned)B), dim3(256), AT_DKV_LDS, s,
+  hipLaunchKernelGGL(attn_bwd_dkv_kernel, dim3((unsigned)kgrid, (unsigned)Hkv, (unsigned)B), dim3(512), AT_DKV_LDS, s,
                      a);
   BSA_LAUNCH_CHECK("attention bwd (dk, dv) launch");
   return BSA_OK;
