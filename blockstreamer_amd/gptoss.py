@@ -341,6 +341,30 @@ def install_fused_post_attention_norm(model: nn.Module) -> int:
     return replaced
 
 
+def install_native_attention(model: nn.Module) -> int:
+    """Run every GptOssAttention of ``model`` on the HIP attention kernels:
+    registers ``blockstreamer_amd.attention.gpt_oss_attention`` with
+    transformers' attention-function interface (eager-style masks) and selects
+    it in ``model.config``, the switch GptOssAttention.forward reads
+    (modeling_gpt_oss.py:322-324).
+
+    No counterpart in the reference, which runs transformers' eager attention.
+    No parameter changes.  Returns the number of attention modules switched.
+    """
+    from transformers.models.gpt_oss import modeling_gpt_oss as gpt_oss
+
+    from . import attention
+
+    attention.register()
+    model.config._attn_implementation = attention.NAME
+    count = 0
+    for mod in model.modules():
+        if isinstance(mod, gpt_oss.GptOssAttention):
+            mod.config._attn_implementation = attention.NAME
+            count += 1
+    return count
+
+
 def install_mxfp4_router(model: nn.Module, config, dtype=torch.bfloat16) -> int:
     """Swap every ``GptOssTopKRouter`` for the fused ``MXFP4TopKRouter``.
 

@@ -183,6 +183,42 @@ def test_decoder_layer_recompute_backward(device):
         assert rel_l2 <= 1e-2
 
 
+@pytest.mark.parametrize("mask", ["runner", "model"])
+def test_decoder_layer_native_attention(device, mask):
+    """The layer on the HIP attention as well, called as the streaming runner
+    calls it (attention_mask=None: every key visible, runners.py:327-335) or
+    with the model's own causal / sliding-window masks; forward and the
+    recompute backward against the float32 layer (eager attention) with our
+    routing."""
+    cfg, ref, ref32, ours, packs = _build(device)
+    assert gptoss.install_native_attention(ours) == L
+    x = (torch.randn(1, S, H, generator=torch.Generator().manual_seed(5)) * 0.5).to(torch.bfloat16).to(device)
+    calls = _capture_layer_inputs(ref, x)
+    g = (torch.randn(1, S, H, generator=torch.Generator().manual_seed(6)) * 0.1).to(torch.bfloat16).to(device)
+    announce(f"decoder layer on the native attention, mask {mask}")
+    for i, (args, kwargs) in enumerate(calls):
+        kw = dict(kwargs)
+        if mask == "runner":
+            kw["attention_mask"] = None
+        state = _layer_state(ref.model.layers[i], packs[i])
+        h = args[0].detach().clone().requires_grad_(True)
+        out, seen = _run_layer(ours.model.layers[i], state, (h,), kw, grad=True)
+        (gh,) = torch.autograd.grad(out, [h], g)
+        lyr32 = copy.deepcopy(ref32.model.layers[i])
+        lyr32.mlp.router = _FixedRouting(lyr32.mlp.router, seen["route"][1])
+        kw32 = {k: (tuple(t.float() for t in v) if k == "position_embeddings" else
+                    v.float() if torch.is_tensor(v) and v.is_floating_point() else v)
+                for k, v in kw.items()}
+        h32 = args[0].detach().float().requires_grad_(True)
+        out32 = lyr32(h32, **kw32)
+        (gh32,) = torch.autograd.grad(out32, [h32], g.float())
+        rel_o, _, _ = errors(out, out32)
+        rel_g, _, _ = errors(gh, gh32)
+        print(f"layer {i} ({mask}): out rel_l2={rel_o:.3e}  d hidden rel_l2={rel_g:.3e}")
+        assert torch.isfinite(out).all() and torch.isfinite(gh).all()
+        assert rel_o <= 1e-2 and rel_g <= 1e-2
+
+
 def test_whole_model_with_fused_router_through_functional_call(device):
     """Both drop-ins (experts and fused router) in the model, every parameter
     bound by one functional_call: runs, leaves the staged tensors alone, and
