@@ -53,7 +53,34 @@ def _bwd_args(T=4, H=2880, I=2880, E=128, k=4, gdt=BF16, blocks=FAKE, save=FAKE,
             save, bwd_ws, bwd_bytes, FAKE, ghdt, FAKE, layout, None)
 
 
+_ST = (ctypes.c_int64 * 3)(64 * 64 * 8, 64 * 64, 64)      # [B, T, H, 64] strides of a 64-head tensor
+_ST_BAD = (ctypes.c_int64 * 3)(64 * 64 * 8, 64 * 64, 60)  # a head stride that is not a multiple of 8
+
+
+def _attn_args(B=1, Tq=8, Tk=8, Hq=64, Hkv=8, D=64, causal=1, window=0, q=FAKE, st=_ST):
+    return (q, st, FAKE, _ST, FAKE, _ST, None, B, Tq, Tk, Hq, Hkv, D, causal, window, 0.125, FAKE, _ST, None, None)
+
+
+def _attn_bwd_args(B=1, Tq=8, Tk=8, Hq=64, Hkv=8, D=64, causal=1, window=0, gq=FAKE, stats=FAKE):
+    return (FAKE, _ST, FAKE, _ST, FAKE, _ST, FAKE, _ST, FAKE, _ST, FAKE, B, Tq, Tk, Hq, Hkv, D, causal, window,
+            0.125, gq, FAKE, FAKE, stats, None)
+
+
 CASES = [
+    ("attn head_dim", "bsa_attention_fwd", _attn_args(D=128), _lib.BSA_EINVAL, b"head_dim"),
+    ("attn groups", "bsa_attention_fwd", _attn_args(Hkv=6), _lib.BSA_EINVAL, b"multiple of Hkv"),
+    ("attn window without causal", "bsa_attention_fwd", _attn_args(causal=0, window=16), _lib.BSA_EINVAL,
+     b"window needs the causal"),
+    ("attn causal Tq > Tk", "bsa_attention_fwd", _attn_args(Tq=9, Tk=8), _lib.BSA_EINVAL, b"more queries"),
+    ("attn null", "bsa_attention_fwd", _attn_args(q=None), _lib.BSA_EINVAL, b"null"),
+    ("attn alignment", "bsa_attention_fwd", _attn_args(q=FAKE + 8), _lib.BSA_EINVAL, b"16-byte aligned"),
+    ("attn strides", "bsa_attention_fwd", _attn_args(st=_ST_BAD), _lib.BSA_EINVAL, b"multiples of 8"),
+    ("attn no keys", "bsa_attention_fwd", _attn_args(Tk=0, causal=0), _lib.BSA_EINVAL, b"without keys"),
+    ("attn B = 0", "bsa_attention_fwd", _attn_args(B=0, q=None), _lib.BSA_OK, None),
+    ("attn bwd head_dim", "bsa_attention_bwd", _attn_bwd_args(D=32), _lib.BSA_EINVAL, b"head_dim"),
+    ("attn bwd null", "bsa_attention_bwd", _attn_bwd_args(stats=None), _lib.BSA_EINVAL, b"null"),
+    ("attn bwd alignment", "bsa_attention_bwd", _attn_bwd_args(gq=FAKE + 4), _lib.BSA_EINVAL, b"16-byte"),
+    ("attn bwd Tq = 0", "bsa_attention_bwd", _attn_bwd_args(Tq=0), _lib.BSA_OK, None),
     # name, entry point, arguments, expected status, message fragment
     ("ws size null", "bsa_moe_workspace_bytes", (4, 64, 64, 8, 2, None), _lib.BSA_EINVAL, b"null"),
     ("ws size shape", "bsa_moe_workspace_bytes", (4, 0, 64, 8, 2, OUT), _lib.BSA_EINVAL, b"bad shape"),
