@@ -2148,10 +2148,11 @@ __device__ __forceinline__ void bt_read_q(const uint8_t* st, int s, const uint32
   }
 }
 
-// The four 32-row A fragments of one 16-k step (aoff: the step's offset).
-__device__ __forceinline__ void bt_read_a(const uint8_t* st, uint32_t aoff, s16x8_t (&af)[4]) {
+// The NMB 32-row A fragments of one 16-k step (aoff: the step's offset).
+template <int NMB>
+__device__ __forceinline__ void bt_read_a(const uint8_t* st, uint32_t aoff, s16x8_t (&af)[NMB]) {
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) af[mb] = *reinterpret_cast<const s16x8_t*>(st + aoff + mb * 4096);
+  for (int mb = 0; mb < NMB; ++mb) af[mb] = *reinterpret_cast<const s16x8_t*>(st + aoff + mb * 4096);
 }
 
 // 8 rows x 4 columns of E2M1 codes -> the 4 columns' B fragments (8 k values
@@ -2188,17 +2189,11 @@ __device__ __forceinline__ void bt_store4(const GemmArgs& a, int64_t pos, int n,
   }
 }
 
-template <int EPI, bool QW4, bool SW4>
-__global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
-  extern __shared__ __align__(1024) uint8_t smem[];  // BT_NS stages
-  const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
-  if (L < 0) return;
-  const int tile = L / a.n_tiles_n;
-  const int nt = L - tile * a.n_tiles_n;
-  const int2 te = a.tiles[tile];
-  const int e = te.x;
-  const int m0 = te.y;
-  const int rows = min(BT_BM, a.offsets[e] + a.counts[e] - m0);
+// One tile with NMB live 32-row blocks (rows <= 32 NMB): the A reads, MFMAs,
+// accumulators and epilogue of the blocks past them are left out (an
+// expert's last row tile often holds a few rows only).
+template <int EPI, bool QW4, bool SW4, int NMB>
+__device__ __forceinline__ void bt_tile(const GemmArgs& a, uint8_t* smem, int e, int m0, int rows, int nt) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -2225,9 +2220,9 @@ __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
     sa[i] = (uint32_t)(BT_A_BYTES + BT_Q_BYTES + rr * 32 + run + 4 * wave + (c >> 3));
   }
 
-  f32x16_t acc[4][4];
+  f32x16_t acc[NMB][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < NMB; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -2245,11 +2240,11 @@ __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
   wait_tiles_ahead<DPT, BT_NS - 2>(min(BT_NS - 2, KT - 1));
   asm volatile("s_barrier" ::: "memory");
   uint32_t raw0[8], sb0[8], raw1[8], sb1[8];
-  s16x8_t af[4];
+  s16x8_t af[NMB];
   u32x4_t bq[4];
   bt_read_q(smem, 0, qa, sa, raw0, sb0);
   bt_read_q(smem, 1, qa, sa, raw1, sb1);
-  bt_read_a(smem, aoff[0], af);
+  bt_read_a<NMB>(smem, aoff[0], af);
   bt_decode(raw0, sb0, bq);
   for (int kt = 0; kt < KT; ++kt) {
     // tile kt+1 has landed once at most the tiles issued after it are in
@@ -2262,14 +2257,14 @@ __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
     const uint8_t* sn = smem + ((kt + 1) % BT_NS) * BT_STAGE;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      s16x8_t afn[4];
-      bt_read_a(s < 3 ? st : sn, aoff[(s + 1) & 3], afn);
+      s16x8_t afn[NMB];
+      bt_read_a<NMB>(s < 3 ? st : sn, aoff[(s + 1) & 3], afn);
       if (s % 2 == 0)
         bt_read_q(s < 2 ? st : sn, (s + 2) & 3, qa, sa, raw0, sb0);
       else
         bt_read_q(s < 2 ? st : sn, (s + 2) & 3, qa, sa, raw1, sb1);
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
+      for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           acc[mb][j] = mfma32(af[mb], __builtin_bit_cast(s16x8_t, bq[j]), acc[mb][j]);
@@ -2279,6 +2274,8 @@ __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
       else
         bt_decode(raw0, sb0, bqn);
       // interleave: each MFMA followed by 2-3 decode VALU ops and 1-2 LDS reads
+      // (the full tile; partial tiles take the compiler's schedule)
+      if constexpr (NMB == 4) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -2297,8 +2294,9 @@ __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
         __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
+      }
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) af[mb] = afn[mb];
+      for (int mb = 0; mb < NMB; ++mb) af[mb] = afn[mb];
 #pragma unroll
       for (int j = 0; j < 4; ++j) bq[j] = bqn[j];
     }
@@ -2309,7 +2307,7 @@ __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
   const int n = nt * BT_BN + 128 * wave + 4 * c;
   if (n >= a.N) return;
 #pragma clang loop unroll(full)
-  for (int mb = 0; mb < 4; ++mb) {
+  for (int mb = 0; mb < NMB; ++mb) {
     // one 32-row block at a time: its 16 rows' saved derivative factors are
     // loaded together (the row loop would otherwise wait on each in turn)
     u32x4_t fac[16];
@@ -2328,6 +2326,25 @@ __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
         bt_store4<EPI>(a, m0 + r, n, o, fac[v]);
       }
     }
+  }
+}
+
+template <int EPI, bool QW4, bool SW4>
+__global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
+  extern __shared__ __align__(1024) uint8_t smem[];  // BT_NS stages
+  const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
+  if (L < 0) return;
+  const int tile = L / a.n_tiles_n;
+  const int nt = L - tile * a.n_tiles_n;
+  const int2 te = a.tiles[tile];
+  const int e = te.x;
+  const int m0 = te.y;
+  const int rows = min(BT_BM, a.offsets[e] + a.counts[e] - m0);
+  switch ((rows + 31) >> 5) {
+    case 1: bt_tile<EPI, QW4, SW4, 1>(a, smem, e, m0, rows, nt); break;
+    case 2: bt_tile<EPI, QW4, SW4, 2>(a, smem, e, m0, rows, nt); break;
+    case 3: bt_tile<EPI, QW4, SW4, 3>(a, smem, e, m0, rows, nt); break;
+    default: bt_tile<EPI, QW4, SW4, 4>(a, smem, e, m0, rows, nt); break;
   }
 }
 
