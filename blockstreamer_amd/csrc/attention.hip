@@ -55,7 +55,11 @@ constexpr int AT_TILE = AT_BC * AT_D * 2;   // 8 KiB
 #ifndef BSA_AT_NS
 #define BSA_AT_NS 2
 #endif
-constexpr int AT_NS = BSA_AT_NS;            // ring stages
+constexpr int AT_NS = BSA_AT_NS;            // ring stages (forward, dq)
+#ifndef BSA_AT_NS_DKV
+#define BSA_AT_NS_DKV 2
+#endif
+constexpr int AT_NS_DKV = BSA_AT_NS_DKV;    // ring stages of dk/dv (2, 3, 4 and 6 measured; 2 fastest)
 
 struct AttnArgs {
   const uint16_t* q;
@@ -280,7 +284,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
         }
         mt = fmaxf(mt, sc[kb][v]);
       }
-    const float mn = fmaxf(m, at_max32(mt) * a.scale2);
+    // the accumulator is rescaled only when some row's maximum moved (every
+    // other row has alpha = 1 exactly, or an accumulator still 0)
+    const float mt2 = at_max32(mt) * a.scale2;
+    const bool grow = mt2 > m;
+    const float mn = grow ? mt2 : m;
     // a row that has seen nothing yet (no sink, every key so far hidden) keeps 0
     const float ms = mn == -INFINITY ? 0.f : mn;
     const float alpha = __builtin_amdgcn_exp2f(m - ms);
@@ -302,14 +310,17 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     rs = at_add32(rs);
     l = l * alpha + rs;
     m = mn;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
 #pragma unroll
-    for (int db = 0; db < 2; ++db) {
+      for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
+        for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
+    }
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
 #pragma unroll
       for (int s = 0; s < 4; ++s)
         o[db] = at_mfma(at_tr8(V + 2048 * s, voff[db][0], voff[db][1]), pf[s], o[db]);
-    }
   }
 
   if (rw.R0 + 32 * wave + c >= rw.rows) return;
@@ -506,7 +517,7 @@ constexpr int AT_DKV_RED = 4 * 64 * 32 * 4;          // row-wave 1's dk or dv pa
 // and then block nblocks - 1 - x, so every workgroup walks about the same
 // number of rows.
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_kernel(AttnBwdArgs a) {
-  extern __shared__ __align__(1024) uint8_t at_smem[];  // AT_NS stages, reused for the reduction
+  extern __shared__ __align__(1024) uint8_t at_smem[];  // AT_NS_DKV stages, reused for the reduction
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -563,7 +574,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_kernel(AttnBwdArgs a) {
     // row of t = R / G, head hk G + R % G, clamped to the last row) and its
     // own copy of (L, D) of rows 32 rw .. 32 rw + 31
     auto issue = [&](int i) {
-      uint8_t* st = at_smem + (i % AT_NS) * AT_DKV_STAGE;
+      uint8_t* st = at_smem + (i % AT_NS_DKV) * AT_DKV_STAGE;
       const int row = 8 * wave + (lane >> 3);
       const int ch = (lane & 7) ^ at_sw(row);
       const int R = min(r_begin + i * AT_RT + row, rows - 1);
@@ -588,13 +599,13 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_kernel(AttnBwdArgs a) {
     // every wave is done with the previous pass's stages and reduction
     // buffer (and its k, v loads have landed) before they are refilled
     __syncthreads();
-    for (int i = 0; i < AT_NS - 1; ++i)
+    for (int i = 0; i < AT_NS_DKV - 1; ++i)
       if (i < nt) issue(i);
     for (int it = 0; it < nt; ++it) {
-      wait_vmcnt_tiles<DPT, AT_NS - 2>(nt - 1 - it);
+      wait_vmcnt_tiles<DPT, AT_NS_DKV - 2>(nt - 1 - it);
       asm volatile("s_barrier" ::: "memory");
-      if (it + AT_NS - 1 < nt) issue(it + AT_NS - 1);
-      const uint8_t* Q = at_smem + (it % AT_NS) * AT_DKV_STAGE;
+      if (it + AT_NS_DKV - 1 < nt) issue(it + AT_NS_DKV - 1);
+      const uint8_t* Q = at_smem + (it % AT_NS_DKV) * AT_DKV_STAGE;
       const uint8_t* DO = Q + AT_TILE;
       const float* ST = reinterpret_cast<const float*>(Q + 2 * AT_TILE + wave * 256);
       const int rbase = r_begin + it * AT_RT + 32 * rw;  // this wave's first row
@@ -693,7 +704,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_kernel(AttnBwdArgs a) {
 }
 
 constexpr int AT_FWD_LDS = AT_NS * 2 * AT_TILE;
-constexpr int AT_DKV_LDS = AT_NS * AT_DKV_STAGE > AT_DKV_RED ? AT_NS * AT_DKV_STAGE : AT_DKV_RED;
+constexpr int AT_DKV_LDS = AT_NS_DKV * AT_DKV_STAGE > AT_DKV_RED ? AT_NS_DKV * AT_DKV_STAGE : AT_DKV_RED;
 
 static int at_allow_lds(const void* fn, int idx, int bytes) {
   int dev = 0;
