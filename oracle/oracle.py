@@ -219,8 +219,8 @@ def attention_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sinks: torc
     v = v[:, :, None].expand(B, Hkv, G, Tk, D).reshape(B, Hq, Tk, D)
     s = torch.matmul(q, k.transpose(2, 3)) * scaling
     if causal:
-        pos = torch.arange(Tq)[:, None] + (Tk - Tq)
-        j = torch.arange(Tk)[None, :]
+        pos = torch.arange(Tq, device=q.device)[:, None] + (Tk - Tq)
+        j = torch.arange(Tk, device=q.device)[None, :]
         vis = j <= pos
         if window > 0:
             vis = vis & (j > pos - window)

@@ -204,3 +204,64 @@ def test_mask_kind_rejects_padding(device):
     m[..., 0] = torch.finfo(torch.float32).min  # a padded first key
     with pytest.raises(ValueError):
         A.mask_kind(m, 8, 8, None)
+
+
+@pytest.mark.parametrize("window", [0, 128])
+def test_forward_gptoss_prefill_8192_sampled_rows(device, window):
+    """The full 8192-token gpt-oss prefill (64 query heads, 8 key heads), causal
+    or windowed: sampled query rows of every head against float64."""
+    announce(f"attention fwd T=8192 window={window}")
+    B, Hq, Hkv, T = 1, 64, 8, 8192
+    q, k, v, s = _inputs(B, Hq, Hkv, T, T, device, seed=77 + window)
+    got = A.attention_forward(q, k, v, s, 0.125, True, window)
+    torch.cuda.synchronize()
+    rows = torch.tensor([0, 1, 63, 64, 127, 128, 129, 4095, 4096, 8000, 8190, 8191])
+    kd = k.double().cpu().repeat_interleave(Hq // Hkv, dim=1)
+    vd = v.double().cpu().repeat_interleave(Hq // Hkv, dim=1)
+    qd = q.double().cpu()[:, :, rows]
+    z = (qd @ kd.transpose(2, 3)) * 0.125                      # [1, Hq, rows, T]
+    j = torch.arange(T)[None, :]
+    vis = j <= rows[:, None]
+    if window:
+        vis &= j > rows[:, None] - window
+    z = z.masked_fill(~vis, float("-inf"))
+    z = torch.cat([z, s.double().cpu().reshape(1, Hq, 1, 1).expand(1, Hq, len(rows), 1)], -1)
+    p = torch.softmax(z - z.max(-1, keepdim=True).values, -1)[..., :T]
+    want = (p @ vd).transpose(1, 2)                             # [1, rows, Hq, 64]
+    rel = _rel_l2(got[:, rows], want)
+    mx = float((got[:, rows].double().cpu() - want).abs().max())
+    print(f"T=8192 window={window}: sampled rows rel_l2={rel:.3e} max_abs={mx:.3e}")
+    assert rel <= FWD_REL_L2 and mx <= FWD_MAX_ABS * max(1.0, float(want.abs().max()))
+
+
+@pytest.mark.parametrize("window", [0, 128])
+def test_forward_backward_2048_vs_float32(device, window):
+    """2048 tokens at the gpt-oss head shape, forward and gradients against a
+    float32 torch reference on the GPU (the oracle's arithmetic in float32)."""
+    announce(f"attention fwd+bwd T=2048 window={window} vs float32")
+    B, Hq, Hkv, T = 1, 64, 8, 2048
+    q, k, v, s = _inputs(B, Hq, Hkv, T, T, device, seed=55 + window)
+    dout = torch.randn(B, T, Hq, 64, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16).to(device)
+    qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    sg = s.detach().clone().requires_grad_(True)
+    out = A.attention(qg, kg, vg, sg, 0.125, True, window)
+    out.backward(dout)
+    qr, kr, vr = (t.detach().float().requires_grad_(True) for t in (q, k, v))
+    sr = s.detach().float().requires_grad_(True)
+    ref = oracle.attention_ref(qr, kr, vr, sr, 0.125, causal=True, window=window, dtype=torch.float32)
+    ref.backward(dout.float())
+    torch.cuda.synchronize()
+    rel = _rel_l2(out, ref)
+    print(f"T=2048 window={window}: out rel_l2={rel:.3e}")
+    assert rel <= FWD_REL_L2
+    for name, got, want in (("dq", qg.grad, qr.grad), ("dk", kg.grad, kr.grad), ("dv", vg.grad, vr.grad),
+                            ("dsinks", sg.grad, sr.grad)):
+        r = _rel_l2(got, want)
+        print(f"  {name}: rel_l2={r:.3e}")
+        assert r <= BWD_REL_L2, name
+    # the same call again gives the same bits
+    q2, k2, v2 = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    out2 = A.attention(q2, k2, v2, s, 0.125, True, window)
+    out2.backward(dout)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2) and torch.equal(qg.grad, q2.grad) and torch.equal(kg.grad, k2.grad)
