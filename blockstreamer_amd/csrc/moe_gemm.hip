@@ -1273,8 +1273,7 @@ __global__ __launch_bounds__(256 * TEAMS, 3 - TEAMS) void moe_stream_persist_ker
 // only known on the device, the grid is sized for the maximum) are split
 // into 8 equal contiguous chunks, one per XCD (workgroups are dispatched
 // round-robin over the 8 XCDs): every XCD gets the same share of the work,
-// and the column tiles of one row tile (and the row tiles of one expert)
-// stay on one XCD's L2.  -1: no tile for this workgroup.  Needs a grid that
+// and the tiles of one expert (tile_of orders them) stay on one XCD's L2.  -1: no tile for this workgroup.  Needs a grid that
 // is a multiple of 8 and at least the live tile count.
 __device__ __forceinline__ int xcd_tile_index(int live) {
   const int chunk = (live + 7) >> 3;
@@ -1282,6 +1281,34 @@ __device__ __forceinline__ int xcd_tile_index(int live) {
   if (slot >= chunk) return -1;
   const int L = (int)(blockIdx.x & 7) * chunk + slot;
   return L < live ? L : -1;
+}
+
+#ifndef BSA_TILE_ORDER
+#define BSA_TILE_ORDER 1
+#endif
+
+// Row tile and column tile of logical tile L.  The dispatch lists expert e's
+// row tiles consecutively (tiles[t0 + j] = (e, offsets[e] + BM*j), j < c =
+// ceil(counts[e] / BM)), so positions [t0*NT, (t0+c)*NT) belong to e; inside
+// that run the c row tiles of one column tile come next to each other.  The
+// workgroups that read one weight column tile then run together on one XCD
+// and the later ones find it in that XCD's L2 (column tiles fastest would put
+// NT - 1 other tiles between them).
+template <int BM>
+__device__ __forceinline__ void tile_of(const GemmArgs& a, int L, int& tile, int& nt) {
+  const int NT = a.n_tiles_n;
+#if BSA_TILE_ORDER
+  const int tq = L / NT;
+  const int2 q = a.tiles[tq];
+  const int t0 = tq - (q.y - a.offsets[q.x]) / BM;
+  const int c = (a.counts[q.x] + BM - 1) / BM;
+  const int r = L - t0 * NT;
+  nt = r / c;
+  tile = t0 + (r - nt * c);
+#else
+  tile = L / NT;
+  nt = L - tile * NT;
+#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -1299,8 +1326,8 @@ __global__ __launch_bounds__(256, 2) void moe_tiled_kernel(GemmArgs a) {
 
   const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
   if (L < 0) return;
-  const int tile = L / a.n_tiles_n;
-  const int nt = L - tile * a.n_tiles_n;
+  int tile, nt;
+  tile_of<TL_BM>(a, L, tile, nt);
   const int2 te = a.tiles[tile];
   const int e = te.x;
   const int m0 = te.y;
@@ -1541,8 +1568,8 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
   extern __shared__ __align__(1024) uint8_t smem[];  // T2_NS stages, then [256][G] B scales
   const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
   if (L < 0) return;
-  const int tile = L / a.n_tiles_n;
-  const int nt = L - tile * a.n_tiles_n;
+  int tile, nt;
+  tile_of<TL_BM>(a, L, tile, nt);
   const int2 te = a.tiles[tile];
   const int e = te.x;
   const int m0 = te.y;
@@ -1837,8 +1864,8 @@ __global__ __launch_bounds__(64 * WM * WN, BSA_MX_WG_PER_CU) void moe_mx_kernel(
   extern __shared__ __align__(1024) uint8_t smem[];
   const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
   if (L < 0) return;
-  const int tile = L / a.n_tiles_n;
-  const int nt = L - tile * a.n_tiles_n;
+  int tile, nt;
+  tile_of<TL_BM>(a, L, tile, nt);
   const int2 te = a.tiles[tile];
   const int e = te.x;
   const int m0 = te.y;
@@ -2034,6 +2061,8 @@ static Workspace carve(void* base, int64_t T, int64_t H, int64_t I, int64_t E, i
 // rows (64 * N/32 is a multiple of 16), so it is computed once per tile.
 // ---------------------------------------------------------------------------
 constexpr int BT_BM = 128;
+static_assert(T2_BM == TL_BM && MX_BM == TL_BM && BT_BM == TL_BM,
+              "tile_of and the dispatch's tile list use TL_BM rows per tile");
 constexpr int BT_BN = 512;
 constexpr int BT_BK = 64;
 constexpr int BT_A_BYTES = BT_BM * BT_BK * 2;  // 16 KiB
@@ -2334,8 +2363,8 @@ __global__ __launch_bounds__(256, 1) void moe_bwd_packed_kernel(GemmArgs a) {
   extern __shared__ __align__(1024) uint8_t smem[];  // BT_NS stages
   const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
   if (L < 0) return;
-  const int tile = L / a.n_tiles_n;
-  const int nt = L - tile * a.n_tiles_n;
+  int tile, nt;
+  tile_of<TL_BM>(a, L, tile, nt);
   const int2 te = a.tiles[tile];
   const int e = te.x;
   const int m0 = te.y;
