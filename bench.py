@@ -538,25 +538,29 @@ def attn_pairs(Tq: int, Tk: int, causal: bool, window: int) -> int:
     return sum(off + t + 1 if window <= 0 else min(off + t + 1, window) for t in range(Tq))
 
 
-def bench_attention(kind: str, steps: int, warmup: int, eager: bool = True) -> dict:
+def bench_attention(kind: str, steps: int, warmup: int, eager: bool = True, batch: int = 64) -> dict:
     """The attention core of a gpt-oss layer on the HIP kernels.
 
     prefill: one 8192-token sequence, causal (the full-attention layers) and
     causal with the 128-token window (the sliding layers), forward and the
-    gradients of q, k, v.  decode: 64 sequences, one new token each, against
-    4096 cached keys.  Inputs in the layout the projections produce
+    gradients of q, k, v.  decode: ``batch`` sequences (64 by default), one new
+    token each, against 4096 cached keys; below 512 (row block, key head,
+    sequence) workgroups the forward splits each sequence's keys over several
+    workgroups (``single_launch_fwd_ms``: the unsplit launch beside it).  Inputs in the layout the projections produce
     ([B, T, H, 64] viewed [B, H, T, 64]), bf16, float32 sinks.
 
     Roofline: prefill against the bf16 MFMA peak with algorithmic flops
     (4 * 64 per visible (query, key, head) triple forward: q.k and p.v; 2.5x
     that backward: dP, dV, dK, dQ and the recomputed S); decode against HBM
     with its algorithmic bytes (each visible key and value row of every key
-    head read once, q read and out written once).  ``eager_*``: transformers'
+    head read once, q read and out written once); ``fwd_graph_us`` is the
+    decode forward's GPU time from a replayed HIP graph (no host launch cost),
+    ``graph_GB_per_s`` its rate.  ``eager_*``: transformers'
     eager_attention_forward on the same GPU, the reference's attention."""
     from blockstreamer_amd import attention as A
 
     dev = torch.device("cuda", 0)
-    B, Tq, Tk = (1, 8192, 8192) if kind == "prefill" else (64, 1, 4096)
+    B, Tq, Tk = (1, 8192, 8192) if kind == "prefill" else (batch, 1, 4096)
     Hq, Hkv, D = ATTN_HQ, ATTN_HKV, ATTN_D
     scaling = D ** -0.5
     gen = torch.Generator().manual_seed(5)
@@ -600,6 +604,41 @@ def bench_attention(kind: str, steps: int, warmup: int, eager: bool = True) -> d
             r["GB_per_s"] = round(byt / (ms * 1e-3) / 1e9, 1)
             r["roofline"] = {"bound": "hbm", "achieved": r["GB_per_s"], "peak": 8000.0, "unit": "GB/s",
                              "frac": round(r["GB_per_s"] / 8000.0, 4)}
+            from blockstreamer_amd import _lib
+            r["key_splits_workspace_bytes"] = int(_lib.lib().bsa_attention_split_workspace_bytes(
+                B, Tq, Tk, Hq, Hkv, 1, window))
+            if r["key_splits_workspace_bytes"]:
+                o1 = torch.empty(B, Tq, Hq, D, dtype=torch.bfloat16, device=dev)
+                s32 = sinks.float().contiguous()
+
+                def single():
+                    _lib.call("bsa_attention_fwd", q.data_ptr(), A._strides(q, 2, 1), k.data_ptr(),
+                              A._strides(k, 2, 1), v.data_ptr(), A._strides(v, 2, 1), s32.data_ptr(), B, Tq, Tk,
+                              Hq, Hkv, D, 1, window, scaling, o1.data_ptr(), A._strides(o1, 1, 2), None,
+                              _lib.stream_handle(dev))
+                r["single_launch_fwd_ms"] = round(timed(single, steps), 4)
+            # GPU time without the host: ten calls captured in one HIP graph, replayed
+            def graph_us(fn):
+                fn()
+                torch.cuda.synchronize()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    for _ in range(10):
+                        fn()
+                g.replay()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(5):
+                    g.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                return e0.elapsed_time(e1) / 50 * 1e3
+            gus = graph_us(lambda: A.attention_forward(q, k, v, sinks, scaling, True, window))
+            r["fwd_graph_us"] = round(gus, 2)
+            r["graph_GB_per_s"] = round(byt / (gus * 1e-6) / 1e9, 1)
+            if r["key_splits_workspace_bytes"]:
+                r["single_launch_graph_us"] = round(graph_us(single), 2)
         res[name] = r
     if eager and kind == "prefill":
         try:
@@ -644,7 +683,9 @@ def focused(args) -> int:
         res = bench_copy(args.steps, args.warmup)
     elif args.workload == "attention":
         res = {"attention_prefill": bench_attention("prefill", args.steps, args.warmup),
-               "attention_decode": bench_attention("decode", args.steps, args.warmup)}
+               "attention_decode": bench_attention("decode", args.steps, args.warmup),
+               "attention_decode_b1": bench_attention("decode", args.steps, args.warmup, batch=1),
+               "attention_decode_b8": bench_attention("decode", args.steps, args.warmup, batch=8)}
     elif args.workload == "norm":
         res = {"norm": [bench_norm(t, reps=max(args.steps, 20)) for t in (64, 8192)]}
     elif args.workload == "moe_decode":
@@ -740,7 +781,9 @@ def main() -> int:
         line["moe_layer"] = moe
         line["post_attention_norm"] = {"t64": bench_norm(64), "t8192": bench_norm(8192)}
         line["attention"] = {"prefill_t8192": bench_attention("prefill", max(args.steps // 2, 5), args.warmup),
-                             "decode_b64_kv4096": bench_attention("decode", max(args.steps, 20), args.warmup)}
+                             "decode_b64_kv4096": bench_attention("decode", max(args.steps, 20), args.warmup),
+                             "decode_b1_kv4096": bench_attention("decode", max(args.steps, 20), args.warmup,
+                                                                 batch=1)}
     print(json.dumps(line), flush=True)
     return 0
 

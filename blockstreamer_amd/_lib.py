@@ -79,6 +79,13 @@ _SIGNATURES = {
         _int, _i64, _f32,                          # causal, window, scaling
         _ptr, _ptr, _ptr, _ptr,                    # out, out strides, lse, stream
     ],
+    "bsa_attention_split_workspace_bytes": [_i64, _i64, _i64, _i64, _i64, _int, _i64],
+    "bsa_attention_fwd_split": [
+        _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,  # q, q strides, k, k strides, v, v strides, sinks
+        _i64, _i64, _i64, _i64, _i64, _i64,        # B, Tq, Tk, Hq, Hkv, head_dim
+        _int, _i64, _f32,                          # causal, window, scaling
+        _ptr, _ptr, _ptr, _ptr, _i64, _ptr,        # out, out strides, lse, workspace, bytes, stream
+    ],
     "bsa_attention_bwd": [
         _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,  # grad_out, q, k, v (each with strides)
         _ptr, _ptr, _ptr,                          # out, out strides, lse
@@ -87,7 +94,7 @@ _SIGNATURES = {
         _ptr, _ptr, _ptr, _ptr, _ptr,              # grad_q, grad_k, grad_v, row_dot, stream
     ],
 }
-_RESTYPE = {"bsa_last_error": ctypes.c_char_p}
+_RESTYPE = {"bsa_last_error": ctypes.c_char_p, "bsa_attention_split_workspace_bytes": ctypes.c_int64}
 
 _lib = None
 

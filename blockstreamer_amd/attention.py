@@ -24,6 +24,7 @@ the calls raise.
 from __future__ import annotations
 
 import ctypes
+import functools
 
 import torch
 from torch import Tensor
@@ -42,6 +43,12 @@ def _strides(t: Tensor, seq_dim: int, head_dim_idx: int) -> "ctypes.Array":
 def _usable(t: Tensor) -> bool:
     return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
             and all(s % 8 == 0 and s >= 0 for s in t.stride()[:-1]))
+
+
+@functools.lru_cache(maxsize=256)
+def _split_bytes(B: int, Tq: int, Tk: int, Hq: int, Hkv: int, causal: int, window: int) -> int:
+    """Workspace of the key-split forward for a shape (0: not split), a function of the shape."""
+    return int(_lib.lib().bsa_attention_split_workspace_bytes(B, Tq, Tk, Hq, Hkv, causal, window))
 
 
 def attention_forward(query: Tensor, key: Tensor, value: Tensor, sinks: Tensor | None, scaling: float,
@@ -73,13 +80,18 @@ def attention_forward(query: Tensor, key: Tensor, value: Tensor, sinks: Tensor |
         s = sinks.detach().to(torch.float32).contiguous()
     out = torch.empty(B, Tq, Hq, D, dtype=torch.bfloat16, device=dev)
     lse = torch.empty(B, Hq, Tq, dtype=torch.float32, device=dev) if return_lse else None
+    # short query grids (decoding) split each row block's keys over several
+    # workgroups; the library says from the shape whether, and how much
+    # workspace that takes
+    ws_bytes = _split_bytes(B, Tq, Tk, Hq, Hkv, 1 if causal else 0, int(window))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
     with torch.cuda.device(dev):
-        _lib.call("bsa_attention_fwd",
+        _lib.call("bsa_attention_fwd_split",
                   q.data_ptr(), _strides(q, 2, 1), k.data_ptr(), _strides(k, 2, 1),
                   v.data_ptr(), _strides(v, 2, 1), s.data_ptr() if s is not None else None,
                   B, Tq, Tk, Hq, Hkv, D, 1 if causal else 0, int(window), float(scaling),
                   out.data_ptr(), _strides(out, 1, 2), lse.data_ptr() if lse is not None else None,
-                  _lib.stream_handle(dev))
+                  ws.data_ptr() if ws is not None else None, ws_bytes, _lib.stream_handle(dev))
     return (out, lse) if return_lse else out
 
 

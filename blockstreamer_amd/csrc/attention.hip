@@ -24,6 +24,9 @@
 // one (batch, key head); row R = t * G + i is query t of head G * hk + i
 // (G = Hq / Hkv), so the G heads sharing a key head read each K/V tile once.
 // Four waves, 32 rows each (lane c = row c of the wave), key tiles of 64.
+// Short query grids (decoding: one row block per sequence and key head) split
+// each row block's key tiles over several workgroups that write unnormalised
+// partial sums; attn_split_combine_kernel merges them (bsa_attention_fwd_split).
 //
 // Orientation: S^T = K Q^T puts a query in each lane, so its row maximum and
 // sum are one exchange between the two lane halves.  The K rows enter that
@@ -73,6 +76,14 @@ struct AttnArgs {
   int Tq, Tk, Hq, G;
   int causal, window;
   float scale2;         // scaling * log2(e)
+  // key-split forward (nsplit > 1): workgroup x = row block * nsplit + split
+  // takes a contiguous share of the row block's key tiles and writes its rows'
+  // unnormalised accumulators and (running max, sum) to part_o / part_ml at
+  // row ((split * B + b) * Hkv + hk) * (Tq * G) + R; attn_split_combine_kernel
+  // merges them
+  int nsplit;
+  float* part_o;        // [nsplit][B][Hkv][Tq * G][64]
+  float* part_ml;       // [nsplit][B][Hkv][Tq * G][2]
 };
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
@@ -205,10 +216,19 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   const int c = lane & 31;
   const int g = lane >> 5;
   // the last row blocks have the most keys under a causal mask: start them first
-  const int rb = (int)gridDim.x - 1 - (int)blockIdx.x;
+  const int nsplit = a.nsplit > 1 ? a.nsplit : 1;
+  const int sp = (int)blockIdx.x % nsplit;
+  const int rb = (int)gridDim.x / nsplit - 1 - (int)blockIdx.x / nsplit;
   const int hk = blockIdx.y;
   const int b = blockIdx.z;
   const AtRows rw = at_rows(a.Tq, a.Tk, a.G, a.causal, a.window, rb, hk, wave, c);
+  // this workgroup's key tiles: all of the row block's, or split sp's share
+  int kt_lo = rw.kt0, kt_hi = rw.kt1;
+  if (nsplit > 1) {
+    const int per = (rw.kt1 - rw.kt0 + nsplit - 1) / nsplit;
+    kt_lo = min(rw.kt1, rw.kt0 + sp * per);
+    kt_hi = min(rw.kt1, kt_lo + per);
+  }
 
   // Q fragments (B operand of S^T): d 16s + 8g .. +7 of row c
   const uint16_t* qrow = a.q + b * a.sqb + (int64_t)rw.t * a.sqt + (int64_t)rw.h * a.sqh;
@@ -236,8 +256,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     for (int h = 0; h < 2; ++h) voff[db][h] = at_tr_off(lane, 0, h, db);
 
   constexpr float LOG2E = 1.4426950408889634f;
-  float m = a.sinks ? a.sinks[rw.h] * LOG2E : -INFINITY;
-  float l = a.sinks ? 1.f : 0.f;
+  // the sink is the starting state of split 0 only
+  float m = a.sinks && sp == 0 ? a.sinks[rw.h] * LOG2E : -INFINITY;
+  float l = a.sinks && sp == 0 ? 1.f : 0.f;
   f32x16_t o[2];
 #pragma unroll
   for (int db = 0; db < 2; ++db)
@@ -246,15 +267,15 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
 
   // the Q loads above are waited for here with the first tile
   for (int i = 0; i < AT_NS - 1; ++i)
-    if (rw.kt0 + i < rw.kt1) issue(rw.kt0 + i);
-  for (int kt = rw.kt0; kt < rw.kt1; ++kt) {
+    if (kt_lo + i < kt_hi) issue(kt_lo + i);
+  for (int kt = kt_lo; kt < kt_hi; ++kt) {
     // tile kt has landed once at most the tiles issued after it are in
     // flight; the barrier also certifies every wave is done with tile kt-1,
     // whose stage takes tile kt + AT_NS - 1 (bare s_barrier: a
     // __syncthreads() fence would wait for that DMA too)
-    wait_vmcnt_tiles<DPT, AT_NS - 2>(rw.kt1 - 1 - kt);
+    wait_vmcnt_tiles<DPT, AT_NS - 2>(kt_hi - 1 - kt);
     asm volatile("s_barrier" ::: "memory");
-    if (kt + AT_NS - 1 < rw.kt1) issue(kt + AT_NS - 1);
+    if (kt + AT_NS - 1 < kt_hi) issue(kt + AT_NS - 1);
     if (!rw.live_wave) continue;
     const uint8_t* K = at_smem + (kt % AT_NS) * (2 * AT_TILE);
     const uint8_t* V = K + AT_TILE;
@@ -324,6 +345,20 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   }
 
   if (rw.R0 + 32 * wave + c >= rw.rows) return;
+  if (nsplit > 1) {
+    const int64_t pidx = (((int64_t)sp * gridDim.z + b) * gridDim.y + hk) * rw.rows + rw.R;
+    float* po = a.part_o + pidx * AT_D;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = 32 * db + 8 * q4 + 4 * g;
+        *reinterpret_cast<f32x4_t*>(po + d) =
+            f32x4_t{o[db][4 * q4], o[db][4 * q4 + 1], o[db][4 * q4 + 2], o[db][4 * q4 + 3]};
+      }
+    if (g == 0) *reinterpret_cast<float2*>(a.part_ml + pidx * 2) = make_float2(m, l);
+    return;
+  }
   const float inv = l > 0.f ? 1.f / l : 0.f;
   uint16_t* orow = a.out + b * a.sob + (int64_t)rw.t * a.sot + (int64_t)rw.h * a.soh;
 #pragma unroll
@@ -338,6 +373,55 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     }
   // __builtin_amdgcn_logf is log2
   if (a.lse && g == 0) a.lse[((int64_t)b * a.Hq + rw.h) * a.Tq + rw.t] = m + __builtin_amdgcn_logf(l);
+}
+
+// Merge of the key splits, one wave per row (lane = d): with M = max_s m_s,
+// w_s = 2^(m_s - M), out = sum_s w_s o_s / sum_s w_s l_s and lse = M +
+// log2(sum_s w_s l_s), the splits added in split order (deterministic).
+__global__ __launch_bounds__(256) void attn_split_combine_kernel(AttnArgs a, int B, int Hkv) {
+  const int lane = threadIdx.x & 63;
+  const int rows = a.Tq * a.G;
+  const int64_t q = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (b, hk, R)
+  if (q >= (int64_t)B * Hkv * rows) return;
+  const int R = (int)(q % rows);
+  const int64_t bh = q / rows;
+  const int hk = (int)(bh % Hkv);
+  const int b = (int)(bh / Hkv);
+  const int ns = a.nsplit;  // <= 64
+  const int64_t stride = (int64_t)B * Hkv * rows;  // rows per split
+  float ms = -INFINITY, ls = 0.f;
+  if (lane < ns) {
+    const float2 v = *reinterpret_cast<const float2*>(a.part_ml + (lane * stride + q) * 2);
+    ms = v.x;
+    ls = v.y;
+  }
+  float mt = ms;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mt = fmaxf(mt, __shfl_xor(mt, off));
+  const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - mt);
+  float lt = w * ls;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) lt += __shfl_xor(lt, off);
+  // eight splits' loads in flight at a time (added in split order); a split
+  // with weight 0 holds zeros
+  float acc = 0.f;
+  const float* po = a.part_o + q * AT_D + lane;
+  const int wi = __builtin_bit_cast(int, w);
+  int sp = 0;
+  for (; sp + 8 <= ns; sp += 8) {
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = po[(sp + j) * stride * AT_D];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc += __builtin_bit_cast(float, __builtin_amdgcn_readlane(wi, sp + j)) * x[j];
+  }
+  for (; sp < ns; ++sp) acc += __builtin_bit_cast(float, __builtin_amdgcn_readlane(wi, sp)) * po[sp * stride * AT_D];
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  const int t = R / a.G;
+  const int h = hk * a.G + (R - t * a.G);
+  const __bf16 y = (__bf16)(acc * inv);
+  a.out[b * a.sob + (int64_t)t * a.sot + (int64_t)h * a.soh + lane] = __builtin_bit_cast(uint16_t, y);
+  if (a.lse && lane == 0) a.lse[((int64_t)b * a.Hq + h) * a.Tq + t] = mt + __builtin_amdgcn_logf(lt);
 }
 
 // ---------------------------------------------------------------------------
@@ -746,18 +830,41 @@ static int at_check_strides(const char* what, const int64_t* const* st, int n) {
 
 static inline bool at_al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
-}  // namespace bsa
+// Key splits of the forward for a shape: enough workgroups for the chip
+// (about AT_SPLIT_TARGET in all) when the (row block, key head, batch) grid
+// alone is short of it and a row block sees at least AT_SPLIT_MIN_TILES key
+// tiles; at least two tiles per split, at most 64 splits.  A function of the
+// shape only, so results do not depend on the device.
+constexpr int64_t AT_SPLIT_TARGET = 512;
+constexpr int64_t AT_SPLIT_MIN_TILES = 8;
+static int at_split_count(int64_t B, int64_t Tq, int64_t Tk, int64_t Hq, int64_t Hkv, int causal, int64_t window) {
+  if (B <= 0 || Tq <= 0 || Tk <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv) return 1;
+  const int64_t G = Hq / Hkv;
+  const int64_t base = (Tq * G + AT_BR - 1) / AT_BR * Hkv * B;
+  if (base >= AT_SPLIT_TARGET) return 1;
+  // key tiles of the row block that sees the most keys
+  const int64_t keys = causal && window > 0 ? std::min<int64_t>(Tk, window + std::min<int64_t>(Tq, AT_BR)) : Tk;
+  const int64_t tiles = (keys + AT_BC - 1) / AT_BC + (causal && window > 0 ? 1 : 0);
+  if (tiles < AT_SPLIT_MIN_TILES) return 1;  // the merge launch costs more than a short range saves
+  int64_t n = std::min<int64_t>((AT_SPLIT_TARGET + base - 1) / base, tiles / 2);
+  n = std::min<int64_t>(n, 64);
+  return n >= 2 ? (int)n : 1;
+}
 
-using namespace bsa;
+// Workspace layout of the key-split forward: part_o, then part_ml at a
+// 256-byte boundary.
+static int64_t at_split_bytes(int64_t nsplit, int64_t B, int64_t Tq, int64_t Hq) {
+  if (nsplit <= 1) return 0;
+  const int64_t rows = nsplit * B * Hq * Tq;  // = nsplit * B * Hkv * (Tq * G)
+  const int64_t o = (rows * AT_D * 4 + 255) / 256 * 256;
+  return o + (rows * 2 * 4 + 255) / 256 * 256;
+}
 
-extern "C" int bsa_attention_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
-                                 const void* v, const int64_t* v_strides, const float* sinks, int64_t B,
-                                 int64_t Tq, int64_t Tk, int64_t Hq, int64_t Hkv, int64_t head_dim, int causal,
-                                 int64_t window, float scaling, void* out, const int64_t* out_strides, float* lse,
-                                 void* stream) {
-  clear_error();
-  BSA_REQUIRE(B >= 0 && Tq >= 0 && Tk >= 0 && Hq > 0 && Hkv > 0, "attention: bad shape");
-  if (B == 0 || Tq == 0) return BSA_OK;
+// Shared checks and arguments of the two forward entry points.
+static int at_fwd_args(AttnArgs& a, const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                       const void* v, const int64_t* v_strides, const float* sinks, int64_t B, int64_t Tq,
+                       int64_t Tk, int64_t Hq, int64_t Hkv, int64_t head_dim, int causal, int64_t window,
+                       float scaling, void* out, const int64_t* out_strides, float* lse) {
   BSA_REQUIRE(Tk > 0, "attention: queries without keys");
   BSA_REQUIRE(q && k && v && out && q_strides && k_strides && v_strides && out_strides, "attention: null pointer");
   int rc = at_check_common("attention", B, Tq, Tk, Hq, Hkv, head_dim, causal, window);
@@ -765,7 +872,7 @@ extern "C" int bsa_attention_fwd(const void* q, const int64_t* q_strides, const 
   BSA_REQUIRE(at_al16(q) && at_al16(k) && at_al16(v) && at_al16(out), "attention: q, k, v and out must be 16-byte aligned");
   const int64_t* st[4] = {q_strides, k_strides, v_strides, out_strides};
   if ((rc = at_check_strides("attention", st, 4))) return rc;
-  AttnArgs a{};
+  a = AttnArgs{};
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k);
   a.v = static_cast<const uint16_t*>(v);
@@ -783,12 +890,75 @@ extern "C" int bsa_attention_fwd(const void* q, const int64_t* q_strides, const 
   a.causal = causal ? 1 : 0;
   a.window = (int)window;
   a.scale2 = scaling * 1.4426950408889634f;
-  const int64_t rblocks = (Tq * a.G + AT_BR - 1) / AT_BR;
-  if ((rc = at_allow_lds(reinterpret_cast<const void*>(attn_fwd_kernel), 0, AT_FWD_LDS))) return rc;
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)rblocks, (unsigned)Hkv, (unsigned)B), dim3(256), AT_FWD_LDS,
-                     static_cast<hipStream_t>(stream), a);
-  BSA_LAUNCH_CHECK("attention launch");
+  a.nsplit = 1;
   return BSA_OK;
+}
+
+static int at_fwd_launch(const AttnArgs& a, int64_t B, int64_t Hkv, hipStream_t st) {
+  const int64_t rblocks = ((int64_t)a.Tq * a.G + AT_BR - 1) / AT_BR;
+  int rc = at_allow_lds(reinterpret_cast<const void*>(attn_fwd_kernel), 0, AT_FWD_LDS);
+  if (rc) return rc;
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)(rblocks * a.nsplit), (unsigned)Hkv, (unsigned)B), dim3(256),
+                     AT_FWD_LDS, st, a);
+  BSA_LAUNCH_CHECK("attention launch");
+  if (a.nsplit > 1) {
+    const int64_t nrow = B * Hkv * (int64_t)a.Tq * a.G;
+    hipLaunchKernelGGL(attn_split_combine_kernel, dim3((unsigned)((nrow + 3) / 4)), dim3(256), 0, st, a, (int)B,
+                       (int)Hkv);
+    BSA_LAUNCH_CHECK("attention split combine launch");
+  }
+  return BSA_OK;
+}
+
+}  // namespace bsa
+
+using namespace bsa;
+
+extern "C" int bsa_attention_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                                 const void* v, const int64_t* v_strides, const float* sinks, int64_t B,
+                                 int64_t Tq, int64_t Tk, int64_t Hq, int64_t Hkv, int64_t head_dim, int causal,
+                                 int64_t window, float scaling, void* out, const int64_t* out_strides, float* lse,
+                                 void* stream) {
+  clear_error();
+  BSA_REQUIRE(B >= 0 && Tq >= 0 && Tk >= 0 && Hq > 0 && Hkv > 0, "attention: bad shape");
+  if (B == 0 || Tq == 0) return BSA_OK;
+  AttnArgs a;
+  int rc = at_fwd_args(a, q, q_strides, k, k_strides, v, v_strides, sinks, B, Tq, Tk, Hq, Hkv, head_dim, causal,
+                       window, scaling, out, out_strides, lse);
+  if (rc) return rc;
+  return at_fwd_launch(a, B, Hkv, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t bsa_attention_split_workspace_bytes(int64_t B, int64_t Tq, int64_t Tk, int64_t Hq, int64_t Hkv,
+                                                       int causal, int64_t window) {
+  return at_split_bytes(at_split_count(B, Tq, Tk, Hq, Hkv, causal, window), B, Tq, Hq);
+}
+
+extern "C" int bsa_attention_fwd_split(const void* q, const int64_t* q_strides, const void* k,
+                                       const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                                       const float* sinks, int64_t B, int64_t Tq, int64_t Tk, int64_t Hq,
+                                       int64_t Hkv, int64_t head_dim, int causal, int64_t window, float scaling,
+                                       void* out, const int64_t* out_strides, float* lse, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
+  clear_error();
+  BSA_REQUIRE(B >= 0 && Tq >= 0 && Tk >= 0 && Hq > 0 && Hkv > 0, "attention: bad shape");
+  if (B == 0 || Tq == 0) return BSA_OK;
+  AttnArgs a;
+  int rc = at_fwd_args(a, q, q_strides, k, k_strides, v, v_strides, sinks, B, Tq, Tk, Hq, Hkv, head_dim, causal,
+                       window, scaling, out, out_strides, lse);
+  if (rc) return rc;
+  const int ns = at_split_count(B, Tq, Tk, Hq, Hkv, causal, window);
+  if (ns > 1) {
+    const int64_t need = at_split_bytes(ns, B, Tq, Hq);
+    BSA_REQUIRE(workspace && reinterpret_cast<uintptr_t>(workspace) % 256 == 0 && workspace_bytes >= need,
+                "attention: the key-split forward needs a 256-byte aligned workspace of %lld bytes (got %lld)",
+                (long long)need, (long long)workspace_bytes);
+    const int64_t rows = (int64_t)ns * B * Hq * Tq;
+    a.nsplit = ns;
+    a.part_o = static_cast<float*>(workspace);
+    a.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + (rows * AT_D * 4 + 255) / 256 * 256);
+  }
+  return at_fwd_launch(a, B, Hkv, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int bsa_attention_bwd(const void* grad_out, const int64_t* grad_strides, const void* q,

@@ -20,4 +20,4 @@ void clear_error() { g_last_error[0] = '\0'; }
 
 extern "C" const char* bsa_last_error(void) { return bsa::g_last_error; }
 
-extern "C" int bsa_version(void) { return 301; }
+extern "C" int bsa_version(void) { return 302; }

@@ -65,7 +65,8 @@ const char *bsa_last_error(void);
  * SwiGLU's bf16 derivative factors (save_swiglu_grad) instead of float32
  * pre-activations.  The minor number counts added entry points (the
  * no-allocation forward, the MXFP8 split and the packed matmul came with
- * major 2; minor 1 of major 3 added the attention entry points).  A binding
+ * major 2; minor 1 of major 3 added the attention entry points, minor 2 the
+ * key-split forward and its workspace query).  A binding
  * checks the major number before its first call. */
 #define BSA_VERSION_MAJOR 3
 int bsa_version(void);
@@ -440,6 +441,40 @@ int bsa_attention_fwd(const void *q, const int64_t *q_strides, const void *k,
                       int64_t head_dim, int causal, int64_t window,
                       float scaling, void *out, const int64_t *out_strides,
                       float *lse, void *stream);
+
+/*
+ * Workspace bytes bsa_attention_fwd_split needs for a shape (0: the shape is
+ * not split and the workspace may be null).  Splitting is chosen from the
+ * shape alone: when the (128-row block, key head, batch) grid has fewer than
+ * about 512 workgroups -- decoding, or short prompts over a long cache -- and
+ * a row block sees at least 512 keys, the keys of each row block are split
+ * over up to 64 workgroups of at least two 64-key tiles each.  Replaces no reference interface: the eager path
+ * (modeling_gpt_oss.py:235-264) has no such knob.
+ */
+int64_t bsa_attention_split_workspace_bytes(int64_t B, int64_t Tq, int64_t Tk,
+                                            int64_t Hq, int64_t Hkv, int causal,
+                                            int64_t window);
+
+/*
+ * bsa_attention_fwd for short query grids (the same arguments and meaning,
+ * modeling_gpt_oss.py:235-264): each workgroup takes a contiguous share of a
+ * row block's keys and writes its rows' unnormalised float32 sums and
+ * (running maximum, sum) to the workspace (>= the query above, 256-byte
+ * aligned), and a second launch merges the shares in a fixed order
+ * (deterministic).  Shapes that are not split run bsa_attention_fwd's single
+ * launch.  The sum order differs from the single launch, so the results agree
+ * with it to float rounding, not bit for bit.
+ */
+int bsa_attention_fwd_split(const void *q, const int64_t *q_strides,
+                            const void *k, const int64_t *k_strides,
+                            const void *v, const int64_t *v_strides,
+                            const float *sinks, int64_t B, int64_t Tq,
+                            int64_t Tk, int64_t Hq, int64_t Hkv,
+                            int64_t head_dim, int causal, int64_t window,
+                            float scaling, void *out,
+                            const int64_t *out_strides, float *lse,
+                            void *workspace, int64_t workspace_bytes,
+                            void *stream);
 
 /*
  * Gradients of bsa_attention_fwd (what autograd computes through

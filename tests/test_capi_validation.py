@@ -66,6 +66,12 @@ def _attn_bwd_args(B=1, Tq=8, Tk=8, Hq=64, Hkv=8, D=64, causal=1, window=0, gq=F
             0.125, gq, FAKE, FAKE, stats, None)
 
 
+def _attn_split_args(B=1, Tq=1, Tk=4096, D=64, q=FAKE, ws=FAKE, ws_bytes=1 << 20):
+    """A decode shape (one query over 4096 keys of 8 key heads): split over 32 workgroups per head."""
+    return (q, _ST, FAKE, _ST, FAKE, _ST, None, B, Tq, Tk, 64, 8, D, 1, 0, 0.125, FAKE, _ST, None, ws, ws_bytes,
+            None)
+
+
 CASES = [
     ("attn head_dim", "bsa_attention_fwd", _attn_args(D=128), _lib.BSA_EINVAL, b"head_dim"),
     ("attn groups", "bsa_attention_fwd", _attn_args(Hkv=6), _lib.BSA_EINVAL, b"multiple of Hkv"),
@@ -77,6 +83,15 @@ CASES = [
     ("attn strides", "bsa_attention_fwd", _attn_args(st=_ST_BAD), _lib.BSA_EINVAL, b"multiples of 8"),
     ("attn no keys", "bsa_attention_fwd", _attn_args(Tk=0, causal=0), _lib.BSA_EINVAL, b"without keys"),
     ("attn B = 0", "bsa_attention_fwd", _attn_args(B=0, q=None), _lib.BSA_OK, None),
+    ("attn split no workspace", "bsa_attention_fwd_split", _attn_split_args(ws=None, ws_bytes=0), _lib.BSA_EINVAL,
+     b"workspace"),
+    ("attn split small workspace", "bsa_attention_fwd_split", _attn_split_args(ws_bytes=4096), _lib.BSA_EINVAL,
+     b"workspace"),
+    ("attn split misaligned workspace", "bsa_attention_fwd_split", _attn_split_args(ws=FAKE + 128),
+     _lib.BSA_EINVAL, b"256-byte"),
+    ("attn split head_dim", "bsa_attention_fwd_split", _attn_split_args(D=128), _lib.BSA_EINVAL, b"head_dim"),
+    ("attn split B = 0", "bsa_attention_fwd_split", _attn_split_args(B=0, q=None, ws=None, ws_bytes=0),
+     _lib.BSA_OK, None),
     ("attn bwd head_dim", "bsa_attention_bwd", _attn_bwd_args(D=32), _lib.BSA_EINVAL, b"head_dim"),
     ("attn bwd null", "bsa_attention_bwd", _attn_bwd_args(stats=None), _lib.BSA_EINVAL, b"null"),
     ("attn bwd alignment", "bsa_attention_bwd", _attn_bwd_args(gq=FAKE + 4), _lib.BSA_EINVAL, b"16-byte"),
@@ -226,3 +241,19 @@ def test_noalloc_scratch_covers_decode_batches():
 def test_python_call_raises_value_error_with_the_message():
     with pytest.raises(ValueError, match="top-k"):
         _lib.call("bsa_moe_experts_fwd", *_fwd_args(k=17))
+
+
+def test_attention_split_workspace_follows_the_shape():
+    """Decode grids split (32 shares of 4096 keys x 64 heads x 66 floats, two 256-byte aligned parts);
+    prefill grids and short key ranges do not (no workspace)."""
+    f = _lib.lib().bsa_attention_split_workspace_bytes
+    assert f(1, 1, 4096, 64, 8, 1, 0) == 32 * 64 * 64 * 4 + 32 * 64 * 2 * 4
+    assert f(64, 1, 4096, 64, 8, 1, 0) == 0          # 512 workgroups already
+    assert f(1, 8192, 8192, 64, 8, 1, 0) == 0        # prefill
+    assert f(1, 1, 100, 64, 8, 1, 0) == 0            # two key tiles: nothing to split
+    # a window bounds the keys a row block sees: 128 + 1 keys -> 4 tiles, too few to split; 1000 -> 17 tiles
+    assert f(1, 1, 4096, 64, 8, 1, 128) == 0
+    assert f(1, 1, 4096, 64, 8, 1, 1000) == 8 * 64 * 64 * 4 + 8 * 64 * 2 * 4
+    assert f(1, 1, 448, 64, 8, 1, 0) == 0             # 7 key tiles: too few
+    assert f(1, 1, 449, 64, 8, 1, 0) == 4 * 64 * 64 * 4 + 4 * 64 * 2 * 4  # 8 tiles: 4 shares
+    assert f(2, 4, 1000, 64, 8, 1, 0) > 0
