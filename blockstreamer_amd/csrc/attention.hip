@@ -835,7 +835,10 @@ static inline bool at_al16(const void* p) { return reinterpret_cast<uintptr_t>(p
 // alone is short of it and a row block sees at least AT_SPLIT_MIN_TILES key
 // tiles; at least two tiles per split, at most 64 splits.  A function of the
 // shape only, so results do not depend on the device.
-constexpr int64_t AT_SPLIT_TARGET = 512;
+#ifndef BSA_AT_SPLIT_TARGET
+#define BSA_AT_SPLIT_TARGET 512
+#endif
+constexpr int64_t AT_SPLIT_TARGET = BSA_AT_SPLIT_TARGET;
 constexpr int64_t AT_SPLIT_MIN_TILES = 8;
 static int at_split_count(int64_t B, int64_t Tq, int64_t Tk, int64_t Hq, int64_t Hkv, int causal, int64_t window) {
   if (B <= 0 || Tq <= 0 || Tk <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv) return 1;
