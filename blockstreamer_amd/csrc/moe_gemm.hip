@@ -52,6 +52,7 @@
 #include <mutex>
 
 #include "bsa_common.h"
+#include "dispatch.h"
 
 namespace bsa {
 
@@ -107,6 +108,19 @@ struct GemmArgs {
   uint8_t* out_s;        // EPI_SWIGLU_MX: scale bytes of the split activations
   int64_t ldos;
   int64_t out_kt, out_s_kt;  // EPI_SWIGLU_MX: k-tile strides of the codes and scales
+  // decode gate_up with the dispatch folded in (moe_stream_persist_kernel):
+  // non-null fuse_idx makes every workgroup first build the dispatch of its
+  // fuse_P router indices (row tiles of fuse_bm) and write it -- every
+  // workgroup the same values -- to the arrays counts / offsets / row_pair
+  // above point to, and to pair_pos and the tile list, for the later launches
+  const int64_t* fuse_idx;
+  int fuse_P, fuse_bm;
+  int* fuse_counts;
+  int* fuse_offsets;
+  int* fuse_row_pair;
+  int* fuse_pair_pos;
+  int2* fuse_tiles;
+  int* fuse_num_tiles;
 };
 
 
@@ -1076,6 +1090,17 @@ __global__ __launch_bounds__(256 * TEAMS, 3 - TEAMS) void moe_stream_persist_ker
   int* sHPre = sScan + NT + 2;                               // prologue: passes before entry h
 
   const int tid = threadIdx.x;
+  if (a.fuse_idx) {
+    // the dispatch, in the ring's LDS before any DMA lands there (E <= NT)
+    int* s_cnt = reinterpret_cast<int*>(ring);
+    int* s_off = s_cnt + NT;
+    int* s_run = s_off + NT;
+    int* s_dsc = s_run + NT;
+    uint8_t(*s_wc)[NT] = reinterpret_cast<uint8_t(*)[NT]>(s_dsc + 2 * (NT / 64));
+    dispatch_block<NT, NT>(a.fuse_idx, a.fuse_P, a.E, a.fuse_bm, a.fuse_counts, a.fuse_offsets, a.fuse_row_pair,
+                           a.fuse_pair_pos, a.fuse_tiles, a.fuse_num_tiles, s_cnt, s_off, s_run, s_dsc, s_wc);
+    __syncthreads();  // this workgroup's writes are visible to its reads below
+  }
   const int lane = tid & 63;
   const int team = TEAMS == 2 ? __builtin_amdgcn_readfirstlane(tid >> 8) : 0;
   const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);   // wave within the team
@@ -2527,13 +2552,23 @@ static int cu_count() {
   return cus[dev];
 }
 
+// Whether the decode path's GEMM with these arguments runs the persistent
+// kernel (else the one-workgroup-per-slice stream kernel).
+static bool persist_ok(const GemmArgs& a, int64_t P) {
+  auto al16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+  return a.K == 2880 && a.N % 16 == 0 && a.E <= 256 * PS_TEAMS && al16(a.Bq) && al16(a.Bs) && al16(a.bias) &&
+         al16(a.A) && a.lda % 8 == 0 && P <= (1 << 19) && cu_count() > 0;
+}
+
+// Pairs up to which the decode gate_up folds the dispatch into its prologue
+// (each persistent workgroup then places PS_FUSE_MAX_P / 256 rounds of pairs).
+constexpr int64_t PS_FUSE_MAX_P = 1024;
+
 template <int EPI>
 static int launch_gemm(const GemmArgs& a, int path, int64_t P, hipStream_t st) {
   const bool align16 = (reinterpret_cast<uintptr_t>(a.Bq) % 16) == 0;
   const int cus = cu_count();
-  if (path == PATH_STREAM && a.K == 2880 && a.N % 16 == 0 && a.E <= 256 * PS_TEAMS && align16 &&
-      reinterpret_cast<uintptr_t>(a.Bs) % 16 == 0 && reinterpret_cast<uintptr_t>(a.bias) % 16 == 0 &&
-      reinterpret_cast<uintptr_t>(a.A) % 16 == 0 && a.lda % 8 == 0 && P <= (1 << 19) && cus > 0) {
+  if (path == PATH_STREAM && persist_ok(a, P)) {
     // the gpt-oss hidden / intermediate size: persistent workgroups, 512
     // threads per CU
     constexpr int ring = PS_TEAMS * PS_TEAM_NB * PsCfg<90>::SLOT;
@@ -2694,9 +2729,14 @@ static int check_layout(int layout, const void* blocks, int64_t rows, int64_t K,
   return BSA_OK;
 }
 
+// dispatch_idx: the router indices when the dispatch has not run yet (it then
+// runs here: folded into the decode GEMM's prologue when that GEMM is the
+// persistent kernel and the batch is small, else as its own launch first);
+// null when the caller ran it.
 static int stage_gate_up(const MoeShape& m, const void* hidden, const void* blocks, const void* scales,
                          const void* bias, int bias_dtype, float alpha, float limit, const Workspace& w,
-                         void* save_swiglu_grad, int path, int layout, hipStream_t st) {
+                         void* save_swiglu_grad, int path, int layout, hipStream_t st,
+                         const int64_t* dispatch_idx = nullptr) {
   // the backward reads each row's factors in 16-byte pieces
   BSA_REQUIRE(reinterpret_cast<uintptr_t>(save_swiglu_grad) % 16 == 0,
               "gate_up: save_swiglu_grad must be 16-byte aligned");
@@ -2726,6 +2766,22 @@ static int stage_gate_up(const MoeShape& m, const void* hidden, const void* bloc
   g.n_tiles_n = (int)((2 * m.I + TL_BN - 1) / TL_BN);
   const int64_t P = m.T * m.k;
   const int chosen = pick_path(path, P, m.E, m.H);
+  if (dispatch_idx) {
+    if (chosen == PATH_STREAM && P <= PS_FUSE_MAX_P && persist_ok(g, P)) {
+      g.fuse_idx = dispatch_idx;
+      g.fuse_P = (int)P;
+      g.fuse_bm = TL_BM;
+      g.fuse_counts = w.counts;
+      g.fuse_offsets = w.offsets;
+      g.fuse_row_pair = w.row_pair;
+      g.fuse_pair_pos = w.pair_pos;
+      g.fuse_tiles = w.tiles;
+      g.fuse_num_tiles = w.num_tiles;
+    } else {
+      int rc = stage_dispatch(m, dispatch_idx, w, st);
+      if (rc) return rc;
+    }
+  }
   if (chosen == PATH_MX) {
     // each token's hidden row is split once and written to each of its pairs
     if (m.H % MX_BK != 0 || m.I % MX_BK != 0) {
@@ -2951,9 +3007,8 @@ static int experts_fwd(
   }
   Workspace w;
   if ((rc = check_ws(m, workspace, workspace_bytes, &w, what))) return rc;
-  if ((rc = stage_dispatch(m, router_indices, w, st))) return rc;
   if ((rc = stage_gate_up(m, hidden, gate_up_blocks, gate_up_scales, gate_up_bias, bias_dtype, alpha,
-                          limit, w, save_swiglu_grad, path, blocks_layout, st)))
+                          limit, w, save_swiglu_grad, path, blocks_layout, st, router_indices)))
     return rc;
   if ((rc = stage_down(m, down_blocks, down_scales, down_bias, bias_dtype, w, path, blocks_layout, st)))
     return rc;

@@ -72,3 +72,45 @@ def test_dispatch_matches_restatement(device, T, E, k):
     assert torch.equal(pair_pos, rp)
     assert ntiles == rt.shape[0]
     assert torch.equal(tiles[:ntiles], rt)
+
+
+@pytest.mark.parametrize("T", [1, 8, 64, 256])
+def test_dispatch_folded_into_the_decode_gemm(device, T):
+    """At decode batches the forward folds the dispatch into the persistent
+    gate_up launch (every workgroup builds it and writes the same arrays).
+    The workspace then holds exactly the dispatch of the restatement, dropped
+    pairs included, and the layer equals the staged call (dispatch kernel,
+    then the GEMMs) bit for bit."""
+    from blockstreamer_amd import synthetic
+    from tests.moe_util import expert_args
+
+    E, k, H, I = 128, 4, 2880, 2880
+    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=31, scale_lo=116, scale_hi=120,
+                            device=device)
+    idx, w = synthetic.random_routing(T, E, k, seed=32, device=device)
+    idx = idx.clone()
+    idx[::5, 1] = -1           # dropped pairs
+    idx = idx.contiguous()
+    announce(f"folded dispatch T={T}")
+    gu_b, gu_s, gu_bias, dn_b, dn_s, dn_bias = expert_args(t)
+    x = t["hidden"].contiguous()
+    out = torch.empty(T, H, dtype=x.dtype, device=device)
+    nb = kernels.moe_workspace_bytes(T, H, I, E, k)
+    ws = kernels._aligned_bytes(nb, device)
+    ws.fill_(0xFF)             # nothing left over from an earlier call
+    bias_code = _lib.dtype_code(gu_bias.dtype)
+    _lib.call("bsa_moe_experts_fwd", x.data_ptr(), T, H, I, E, k, idx.data_ptr(), w.data_ptr(),
+              _lib.dtype_code(w.dtype), gu_b.data_ptr(), gu_s.data_ptr(), gu_bias.data_ptr(), dn_b.data_ptr(),
+              dn_s.data_ptr(), dn_bias.data_ptr(), bias_code, 1.702, 7.0, out.data_ptr(), _lib.dtype_code(x.dtype),
+              ws.data_ptr(), nb, None, 1, 0, _lib.stream_handle(device))  # path 1: the decode kernels
+    staged = kernels.MoEStages(x, idx, w, gu_b, gu_s, gu_bias, dn_b, dn_s, dn_bias, path="stream").run()
+    torch.cuda.synchronize()
+    counts, offsets, row_pair, pair_pos, tiles, ntiles = _read_workspace(ws, T, E, k)
+    rc, ro, rr, rp, rt = _reference(idx.cpu(), E)
+    assert torch.equal(counts, rc)
+    assert torch.equal(offsets, ro)
+    assert torch.equal(row_pair[: rr.numel()], rr)
+    assert torch.equal(pair_pos, rp)
+    assert ntiles == rt.shape[0]
+    assert torch.equal(tiles[:ntiles], rt)
+    assert torch.equal(out.view(torch.int16), staged.view(torch.int16))
