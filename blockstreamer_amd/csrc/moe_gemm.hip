@@ -2562,7 +2562,10 @@ static bool persist_ok(const GemmArgs& a, int64_t P) {
 
 // Pairs up to which the decode gate_up folds the dispatch into its prologue
 // (each persistent workgroup then places PS_FUSE_MAX_P / 256 rounds of pairs).
-constexpr int64_t PS_FUSE_MAX_P = 1024;
+#ifndef BSA_FUSE_DISPATCH
+#define BSA_FUSE_DISPATCH 1
+#endif
+constexpr int64_t PS_FUSE_MAX_P = BSA_FUSE_DISPATCH ? 1024 : 0;
 
 template <int EPI>
 static int launch_gemm(const GemmArgs& a, int path, int64_t P, hipStream_t st) {
