@@ -114,3 +114,39 @@ def test_dispatch_folded_into_the_decode_gemm(device, T):
     assert ntiles == rt.shape[0]
     assert torch.equal(tiles[:ntiles], rt)
     assert torch.equal(out.view(torch.int16), staged.view(torch.int16))
+
+
+@pytest.mark.parametrize("T", [1, 64])
+def test_decode_with_every_pair_dropped(device, T):
+    """Every router index outside [0, E) (the masking index E and -1): the
+    folded dispatch leaves every expert empty, every persistent workgroup
+    returns right after writing it, and the layer is zero, as the reference
+    adds nothing to its zeros (gptoss.py:143-176); the staged call agrees."""
+    from blockstreamer_amd import synthetic
+    from tests.moe_util import expert_args
+
+    E, k, H, I = 128, 4, 2880, 2880
+    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=41, scale_lo=116, scale_hi=120,
+                            device=device)
+    idx = torch.full((T, k), -1, dtype=torch.int64, device=device)
+    idx[:, 1::2] = E
+    w = torch.full((T, k), 0.25, dtype=torch.float32, device=device)
+    announce(f"every pair dropped T={T}")
+    gu_b, gu_s, gu_bias, dn_b, dn_s, dn_bias = expert_args(t)
+    x = t["hidden"].contiguous()
+    out = torch.full((T, H), 7.0, dtype=x.dtype, device=device)
+    nb = kernels.moe_workspace_bytes(T, H, I, E, k)
+    ws = kernels._aligned_bytes(nb, device)
+    ws.fill_(0xFF)
+    _lib.call("bsa_moe_experts_fwd", x.data_ptr(), T, H, I, E, k, idx.data_ptr(), w.data_ptr(),
+              _lib.dtype_code(w.dtype), gu_b.data_ptr(), gu_s.data_ptr(), gu_bias.data_ptr(), dn_b.data_ptr(),
+              dn_s.data_ptr(), dn_bias.data_ptr(), _lib.dtype_code(gu_bias.dtype), 1.702, 7.0, out.data_ptr(),
+              _lib.dtype_code(x.dtype), ws.data_ptr(), nb, None, 1, 0, _lib.stream_handle(device))
+    staged = kernels.MoEStages(x, idx, w, gu_b, gu_s, gu_bias, dn_b, dn_s, dn_bias, path="stream").run()
+    torch.cuda.synchronize()
+    counts, offsets, _, pair_pos, _, ntiles = _read_workspace(ws, T, E, k)
+    assert int(counts.abs().sum()) == 0 and int(offsets.abs().sum()) == 0
+    assert torch.equal(pair_pos, torch.full_like(pair_pos, -1))
+    assert ntiles == 0
+    assert int(torch.count_nonzero(out)) == 0
+    assert torch.equal(out.view(torch.int16), staged.view(torch.int16))
