@@ -25,6 +25,7 @@ from __future__ import annotations
 
 import ctypes
 import functools
+import weakref
 
 import torch
 from torch import Tensor
@@ -136,6 +137,13 @@ def attention_backward(grad_out: Tensor, query: Tensor, key: Tensor, value: Tens
 # ---------------------------------------------------------------------------
 # transformers attention-function interface
 # ---------------------------------------------------------------------------
+# Verdicts of mask_kind, keyed by (id(mask), sliding_window) and holding a
+# weak reference to the mask itself: a hit needs the very same tensor object
+# (alive, so its address cannot have been handed to another tensor) at the
+# same version.  transformers builds one mask per forward and passes it to
+# every layer, so one check serves the whole model.  A mask written through
+# ``.data`` (which bypasses the version counter) between two calls with the
+# same tensor object is not seen.
 _mask_cache: dict = {}
 
 
@@ -161,10 +169,10 @@ def mask_kind(attention_mask: Tensor | None, Tq: int, Tk: int, sliding_window: i
         return False, 0
     if attention_mask.dim() != 4 or attention_mask.shape[1] != 1 or tuple(attention_mask.shape[2:]) != (Tq, Tk):
         raise ValueError(f"attention: mask of shape {tuple(attention_mask.shape)}; expected [B, 1, {Tq}, {Tk}]")
-    key = (attention_mask.data_ptr(), tuple(attention_mask.shape), attention_mask._version, sliding_window)
+    key = (id(attention_mask), sliding_window)
     hit = _mask_cache.get(key)
-    if hit is not None:
-        return hit
+    if hit is not None and hit[0]() is attention_mask and hit[1] == attention_mask._version:
+        return hit[2]
     vis = _visible(attention_mask)
     result = None
     for window in ([sliding_window] if sliding_window else []) + [0]:
@@ -175,7 +183,7 @@ def mask_kind(attention_mask: Tensor | None, Tq: int, Tk: int, sliding_window: i
         raise ValueError("attention: only the causal and sliding-window causal masks (no padding) are supported")
     if len(_mask_cache) > 64:
         _mask_cache.clear()
-    _mask_cache[key] = result
+    _mask_cache[key] = (weakref.ref(attention_mask), attention_mask._version, result)
     return result
 
 

@@ -3043,6 +3043,12 @@ extern "C" int bsa_moe_experts_fwd_noalloc(
     float alpha, float limit, void* out, int out_dtype, void* save_swiglu_grad, int path,
     int blocks_layout, void* stream) {
   clear_error();
+  // the backward reads the forward's workspace (the dispatch arrays), which
+  // here is the shared scratch that the next call overwrites: nothing saved
+  // by this entry point could be consumed safely
+  BSA_REQUIRE(save_swiglu_grad == nullptr,
+              "experts fwd (no-alloc): save_swiglu_grad must be null (the backward needs the forward's "
+              "workspace, and this entry point's is the shared static scratch)");
   return experts_fwd("experts fwd (no-alloc)", true, hidden, T, H, I, E, k, router_indices, routing_weights,
                      weight_dtype, gate_up_blocks, gate_up_scales, gate_up_bias, down_blocks, down_scales,
                      down_bias, bias_dtype, alpha, limit, out, out_dtype, nullptr, 0, save_swiglu_grad, path,

@@ -242,13 +242,13 @@ class MXFP4TopKRouter(nn.Module):
     names (``weight [E, H]``, ``bias [E]``) and return value
     ``(logits, scores, indices)``."""
 
-    def __init__(self, config, dtype: torch.dtype = torch.bfloat16) -> None:
+    def __init__(self, config, dtype: torch.dtype = torch.bfloat16, device=None) -> None:
         super().__init__()
         self.top_k = config.num_experts_per_tok
         self.num_experts = config.num_local_experts
         self.hidden_dim = config.hidden_size
-        self.weight = nn.Parameter(torch.zeros(self.num_experts, self.hidden_dim, dtype=dtype))
-        self.bias = nn.Parameter(torch.zeros(self.num_experts, dtype=dtype))
+        self.weight = nn.Parameter(torch.zeros(self.num_experts, self.hidden_dim, dtype=dtype, device=device))
+        self.bias = nn.Parameter(torch.zeros(self.num_experts, dtype=dtype, device=device))
 
     def forward(self, hidden_states: Tensor):
         flat = hidden_states.reshape(-1, self.hidden_dim)
@@ -365,12 +365,14 @@ def install_native_attention(model: nn.Module) -> int:
     return count
 
 
-def install_mxfp4_router(model: nn.Module, config, dtype=torch.bfloat16) -> int:
+def install_mxfp4_router(model: nn.Module, config, dtype: torch.dtype | None = None) -> int:
     """Swap every ``GptOssTopKRouter`` for the fused ``MXFP4TopKRouter``.
 
     No counterpart in the reference, which keeps the transformers router;
     parameter names are unchanged, so checkpoints and shards bind as before.
-    Returns the number of layers changed.
+    Each new router lives on the old one's device (meta stays meta) and, unless
+    ``dtype`` is given, keeps its dtype; its weight and bias are copied over,
+    as is their ``requires_grad``.  Returns the number of layers changed.
     """
     from transformers.models.gpt_oss import modeling_gpt_oss as gpt_oss
 
@@ -378,20 +380,23 @@ def install_mxfp4_router(model: nn.Module, config, dtype=torch.bfloat16) -> int:
     for layer in model.model.layers:
         if isinstance(layer.mlp.router, gpt_oss.GptOssTopKRouter):
             old = layer.mlp.router
-            new = MXFP4TopKRouter(config, dtype)
+            new = MXFP4TopKRouter(config, dtype or old.weight.dtype, device=old.weight.device)
             if old.weight.device.type != "meta":
                 with torch.no_grad():
                     new.weight.copy_(old.weight)
                     new.bias.copy_(old.bias)
+            new.weight.requires_grad_(old.weight.requires_grad)
+            new.bias.requires_grad_(old.bias.requires_grad)
             layer.mlp.router = new
             replaced += 1
     return replaced
 
 
 def install_mxfp4_experts(model: nn.Module, config, dtype=torch.bfloat16) -> int:
-    """Swap every dense GptOssExperts for the packed, fused version.
+    """Put an ``MXFP4Experts`` (packed weights, fused HIP kernels) in place of
+    each layer's dense ``GptOssExperts``.
 
-    block_streamer/gptoss.py:180-189; returns the number of layers replaced.
+    block_streamer/gptoss.py:180-189; returns how many layers changed.
     """
     from transformers.models.gpt_oss import modeling_gpt_oss as gpt_oss
 

@@ -261,7 +261,7 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
                         gate_up_blocks: Tensor, gate_up_scales: Tensor, gate_up_bias: Tensor | None,
                         down_blocks: Tensor, down_scales: Tensor, down_bias: Tensor | None,
                         alpha: float = 1.702, limit: float = 7.0, *, save: bool = False,
-                        path: str = "auto", noalloc: bool = False):
+                        path: str = "auto", noalloc: bool = False, out_dtype: torch.dtype | None = None):
     """Fused MoE experts forward (block_streamer/gptoss.py:137-177).
 
     ``hidden [T, H]``, ``router_indices [T, k]``, ``routing_weights [T, k]``;
@@ -272,6 +272,9 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
     derivatives w.r.t. gate (column 2j) and up (2j+1) at the float32
     pre-activations, the clamp masks applied.  Activations enter the MFMA as bfloat16,
     except on ``path="mx"`` (two MXFP8 terms, see ``PATHS``).
+
+    ``out_dtype`` (default: that of ``hidden``) is the dtype the combine
+    writes, e.g. float32 to see the layer before its final rounding.
 
     ``noalloc=True`` runs the same kernels through
     ``bsa_moe_experts_fwd_noalloc``, whose workspace is the library's static
@@ -297,7 +300,7 @@ def moe_experts_forward(hidden: Tensor, router_indices: Tensor, routing_weights:
     _check_bias(down_bias, E, H, "down_proj")
     dev = _lib.require_gpu(hidden, router_indices, routing_weights, gate_up_blocks,
                            gate_up_scales, down_blocks, down_scales, gate_up_bias, down_bias)
-    out_dtype = hidden.dtype
+    out_dtype = out_dtype or hidden.dtype
     out_code = _lib.dtype_code(out_dtype)
     x = hidden if hidden.dtype == torch.bfloat16 else hidden.to(torch.bfloat16)
     x = x.contiguous()

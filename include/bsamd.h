@@ -207,6 +207,9 @@ int bsa_moe_experts_fwd(
  * Every call on one GPU shares that GPU's array, so calls that overlap on a
  * GPU (concurrent streams, threads) race; order them.  The array's contents
  * after a call are those of the last call; no call relies on them.
+ * save_swiglu_grad must be null (BSA_EINVAL otherwise): the backward also
+ * reads the forward's workspace, which here the next call overwrites, so
+ * this entry point serves inference only.
  */
 #define BSA_NOALLOC_SCRATCH_BYTES (16ll << 20)
 int bsa_moe_experts_fwd_noalloc(

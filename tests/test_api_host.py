@@ -133,3 +133,90 @@ def test_backward_refuses_bad_arguments_before_the_gpu():
     # well-formed arguments get as far as the device check
     with pytest.raises(ValueError, match="GPU only"):
         call()
+
+
+def _causal_additive(T: int) -> torch.Tensor:
+    vis = torch.ones(T, T, dtype=torch.bool).tril()
+    return torch.where(vis, 0.0, torch.finfo(torch.float32).min).reshape(1, 1, T, T)
+
+
+def test_mask_kind_does_not_reuse_a_verdict_at_a_reused_address():
+    """A causal mask is checked, then dropped; a padded mask of the same shape
+    is then built in the same storage without a version bump (written
+    through ``.data``), so it has the freed mask's address, shape and
+    version.  It must still be refused: the verdict belongs to the checked
+    tensor object, not to its address."""
+    from blockstreamer_amd import attention
+
+    buf = torch.empty(1, 1, 8, 8)
+    buf.data.copy_(_causal_additive(8))
+    first = buf.view(1, 1, 8, 8)
+    assert attention.mask_kind(first, 8, 8, None) == (True, 0)
+    ptr, version = first.data_ptr(), first._version
+    del first
+    padded = _causal_additive(8)
+    padded[..., 0] = torch.finfo(torch.float32).min  # the first key is padding
+    buf.data.copy_(padded)
+    second = buf.view(1, 1, 8, 8)
+    assert (second.data_ptr(), second._version) == (ptr, version)
+    with pytest.raises(ValueError, match="no padding"):
+        attention.mask_kind(second, 8, 8, None)
+
+
+def test_mask_kind_verdict_is_reused_for_the_same_mask_and_dropped_on_change():
+    from blockstreamer_amd import attention
+
+    m = _causal_additive(8)
+    assert attention.mask_kind(m, 8, 8, None) == (True, 0)
+    assert attention.mask_kind(m, 8, 8, None) == (True, 0)  # the cached verdict
+    m[..., 0] = torch.finfo(torch.float32).min              # an in-place edit bumps the version
+    with pytest.raises(ValueError):
+        attention.mask_kind(m, 8, 8, None)
+
+
+def _tiny_gptoss(dtype):
+    transformers = pytest.importorskip("transformers")
+    from transformers.models.gpt_oss.configuration_gpt_oss import GptOssConfig
+    from transformers.models.gpt_oss.modeling_gpt_oss import GptOssForCausalLM
+
+    cfg = GptOssConfig(vocab_size=64, hidden_size=64, intermediate_size=64, num_hidden_layers=2,
+                       num_attention_heads=4, num_key_value_heads=2, head_dim=16, num_local_experts=4,
+                       num_experts_per_tok=2, sliding_window=16, max_position_embeddings=64, use_cache=False)
+    torch.manual_seed(0)
+    return cfg, GptOssForCausalLM(cfg).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_install_router_keeps_device_dtype_and_values(dtype):
+    """The fused router replaces transformers' in place: on the old router's
+    device, in its dtype (no silent recast of a float32 router), with its
+    weight and bias values and their requires_grad."""
+    cfg, model = _tiny_gptoss(dtype)
+    model.model.layers[0].mlp.router.weight.requires_grad_(False)
+    olds = [(layer.mlp.router.weight.detach().clone(), layer.mlp.router.bias.detach().clone(),
+             layer.mlp.router.weight.requires_grad) for layer in model.model.layers]
+    assert gptoss.install_mxfp4_router(model, cfg) == 2
+    for layer, (w, b, rg) in zip(model.model.layers, olds):
+        r = layer.mlp.router
+        assert isinstance(r, gptoss.MXFP4TopKRouter)
+        assert r.weight.device == w.device and r.weight.dtype == dtype and r.bias.dtype == dtype
+        assert torch.equal(r.weight, w) and torch.equal(r.bias, b)
+        assert r.weight.requires_grad == rg
+    # an explicit dtype still wins
+    cfg, model = _tiny_gptoss(torch.float32)
+    assert gptoss.install_mxfp4_router(model, cfg, torch.bfloat16) == 2
+    assert model.model.layers[1].mlp.router.weight.dtype == torch.bfloat16
+
+
+def test_install_router_on_a_meta_model_stays_on_meta():
+    transformers = pytest.importorskip("transformers")
+    from transformers.models.gpt_oss.configuration_gpt_oss import GptOssConfig
+    from transformers.models.gpt_oss.modeling_gpt_oss import GptOssForCausalLM
+
+    cfg = GptOssConfig(vocab_size=64, hidden_size=64, intermediate_size=64, num_hidden_layers=1,
+                       num_attention_heads=4, num_key_value_heads=2, head_dim=16, num_local_experts=4,
+                       num_experts_per_tok=2, max_position_embeddings=64)
+    with torch.device("meta"):
+        model = GptOssForCausalLM(cfg)
+    assert gptoss.install_mxfp4_router(model, cfg) == 1
+    assert model.model.layers[0].mlp.router.weight.device.type == "meta"

@@ -38,10 +38,10 @@ def _fwd_args(T=4, H=2880, I=2880, E=128, k=4, hidden=FAKE, wdt=BF16, bdt=BF16, 
             ws, ws_bytes, None, path, layout, None)
 
 
-def _noalloc_args(T=4, H=2880, I=2880, E=128, k=4, hidden=FAKE, ptr=FAKE, path=0):
+def _noalloc_args(T=4, H=2880, I=2880, E=128, k=4, hidden=FAKE, ptr=FAKE, path=0, save=None):
     """bsa_moe_experts_fwd_noalloc: the forward's arguments without the workspace pair."""
     a = _fwd_args(T=T, H=H, I=I, E=E, k=k, hidden=hidden, ptr=ptr, path=path, ws_bytes=0)
-    return a[:20] + a[22:]
+    return a[:20] + (save,) + a[23:]
 
 
 def _bwd_args(T=4, H=2880, I=2880, E=128, k=4, gdt=BF16, blocks=FAKE, save=FAKE, bwd_ws=FAKE,
@@ -125,6 +125,8 @@ CASES = [
     ("no-alloc path", "bsa_moe_experts_fwd_noalloc", _noalloc_args(path=9), _lib.BSA_EINVAL, b"path"),
     ("no-alloc beyond the scratch", "bsa_moe_experts_fwd_noalloc", _noalloc_args(T=1024), _lib.BSA_EINVAL,
      b"static scratch"),
+    ("no-alloc save for backward", "bsa_moe_experts_fwd_noalloc", _noalloc_args(save=FAKE), _lib.BSA_EINVAL,
+     b"save_swiglu_grad must be null"),
     ("gate_up unknown layout", "bsa_moe_gate_up",
      (FAKE, 4, 64, 64, 8, 2, FAKE, FAKE, None, BF16, 1.702, 7.0, FAKE, 1 << 20, None, 0, 3, None),
      _lib.BSA_EINVAL, b"layout"),

@@ -121,10 +121,11 @@ def test_gptoss_120b_decode_realistic_scales_absolute(device):
     assert_layer_close(got.cpu()[tokens], want, "120b decode realistic", absolute=True)
 
 
-@pytest.mark.parametrize("path", PATHS)
+@pytest.mark.parametrize("path", PATHS + ["auto", "mx"])
 def test_gptoss_20b_full_layer(device, path):
     """32 experts, top-4, 2048 tokens: every token vs a float32 GPU reference,
-    a subset vs the CPU oracle."""
+    a subset vs the CPU oracle.  "auto" is the path the benchmark reports for
+    this workload (it resolves to the MX kernels at 256 rows per expert)."""
     shape = synthetic.MoEShape(32, 4, 2880, 2880, 2048)
     t = synthetic.moe_layer(shape, seed=3, scale_lo=115, scale_hi=131, router_bias_std=0.01,
                             device=device)
