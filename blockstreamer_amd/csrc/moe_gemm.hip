@@ -2567,20 +2567,63 @@ static bool persist_ok(const GemmArgs& a, int64_t P) {
 #endif
 constexpr int64_t PS_FUSE_MAX_P = BSA_FUSE_DISPATCH ? 1024 : 0;
 
+// A dispatch that has not run yet: the router indices and the workspace
+// arrays it fills (launch_gemm runs it, folded or as its own launch).
+struct PendingDispatch {
+  const int64_t* idx;
+  const Workspace* w;
+};
+
+static int run_dispatch(const int64_t* idx, int64_t P, int E, const Workspace& w, hipStream_t st) {
+  // the chunked dispatch's per-chunk histograms ([P/2048][E] int32) live in
+  // the activation buffer, which gate_up overwrites afterwards
+  return launch_dispatch(idx, (int)P, E, TL_BM, w.counts, w.offsets, w.row_pair, w.pair_pos, w.tiles,
+                         w.num_tiles, reinterpret_cast<int*>(w.act), st);
+}
+
+// `pending` (non-null for the first GEMM of a forward whose dispatch has not
+// run): the dispatch runs here, in the branch that picks the kernel, so that
+// it is folded into the prologue of the persistent kernel only, the one
+// kernel that builds it, and runs as its own launch before any other kernel.
+// No kernel can then read a workspace that nothing has dispatched into.
 template <int EPI>
-static int launch_gemm(const GemmArgs& a, int path, int64_t P, hipStream_t st) {
+static int launch_gemm(const GemmArgs& a, int path, int64_t P, hipStream_t st,
+                       const PendingDispatch* pending = nullptr) {
   const bool align16 = (reinterpret_cast<uintptr_t>(a.Bq) % 16) == 0;
   const int cus = cu_count();
   if (path == PATH_STREAM && persist_ok(a, P)) {
     // the gpt-oss hidden / intermediate size: persistent workgroups, 512
     // threads per CU
+    GemmArgs b = a;
+    if (pending && P <= PS_FUSE_MAX_P) {
+      const Workspace& w = *pending->w;
+      b.fuse_idx = pending->idx;
+      b.fuse_P = (int)P;
+      b.fuse_bm = TL_BM;
+      b.fuse_counts = w.counts;
+      b.fuse_offsets = w.offsets;
+      b.fuse_row_pair = w.row_pair;
+      b.fuse_pair_pos = w.pair_pos;
+      b.fuse_tiles = w.tiles;
+      b.fuse_num_tiles = w.num_tiles;
+    } else if (pending) {
+      int rc = run_dispatch(pending->idx, P, a.E, *pending->w, st);
+      if (rc) return rc;
+    }
     constexpr int ring = PS_TEAMS * PS_TEAM_NB * PsCfg<90>::SLOT;
     const void* fn = reinterpret_cast<const void*>(moe_stream_persist_kernel<EPI, 90, PS_TEAMS>);
     int rc = allow_big_lds(fn, 6, EPI, ring);
     if (rc) return rc;
     hipLaunchKernelGGL((moe_stream_persist_kernel<EPI, 90, PS_TEAMS>), dim3((unsigned)(cus * (3 - PS_TEAMS))),
-                       dim3(256 * PS_TEAMS), ring, st, a);
-  } else if (path == PATH_STREAM && a.K == 2880 && a.N % ST_BN == 0 && align16 &&
+                       dim3(256 * PS_TEAMS), ring, st, b);
+    BSA_LAUNCH_CHECK("grouped GEMM launch");
+    return BSA_OK;
+  }
+  if (pending) {
+    int rc = run_dispatch(pending->idx, P, a.E, *pending->w, st);
+    if (rc) return rc;
+  }
+  if (path == PATH_STREAM && a.K == 2880 && a.N % ST_BN == 0 && align16 &&
              reinterpret_cast<uintptr_t>(a.Bs) % 16 == 0) {
     // the gpt-oss hidden / intermediate size: the part-pipelined kernel
     const int64_t grid = (int64_t)a.E * (a.N / ST_BN);
@@ -2711,11 +2754,8 @@ static int check_ws(const MoeShape& m, void* workspace, int64_t bytes, Workspace
   return BSA_OK;
 }
 
-// The chunked dispatch's per-chunk histograms ([P/2048][E] int32) live in the
-// activation buffer, which gate_up overwrites afterwards.
 static int stage_dispatch(const MoeShape& m, const int64_t* idx, const Workspace& w, hipStream_t st) {
-  return launch_dispatch(idx, (int)(m.T * m.k), (int)m.E, TL_BM, w.counts, w.offsets, w.row_pair,
-                         w.pair_pos, w.tiles, w.num_tiles, reinterpret_cast<int*>(w.act), st);
+  return run_dispatch(idx, m.T * m.k, (int)m.E, w, st);
 }
 
 // blocks_layout of one packed weight with `rows` rows of K/32 groups.
@@ -2733,7 +2773,7 @@ static int check_layout(int layout, const void* blocks, int64_t rows, int64_t K,
 }
 
 // dispatch_idx: the router indices when the dispatch has not run yet (it then
-// runs here: folded into the decode GEMM's prologue when that GEMM is the
+// runs here: folded into the decode GEMM's prologue when launch_gemm picks the
 // persistent kernel and the batch is small, else as its own launch first);
 // null when the caller ran it.
 static int stage_gate_up(const MoeShape& m, const void* hidden, const void* blocks, const void* scales,
@@ -2769,28 +2809,17 @@ static int stage_gate_up(const MoeShape& m, const void* hidden, const void* bloc
   g.n_tiles_n = (int)((2 * m.I + TL_BN - 1) / TL_BN);
   const int64_t P = m.T * m.k;
   const int chosen = pick_path(path, P, m.E, m.H);
-  if (dispatch_idx) {
-    if (chosen == PATH_STREAM && P <= PS_FUSE_MAX_P && persist_ok(g, P)) {
-      g.fuse_idx = dispatch_idx;
-      g.fuse_P = (int)P;
-      g.fuse_bm = TL_BM;
-      g.fuse_counts = w.counts;
-      g.fuse_offsets = w.offsets;
-      g.fuse_row_pair = w.row_pair;
-      g.fuse_pair_pos = w.pair_pos;
-      g.fuse_tiles = w.tiles;
-      g.fuse_num_tiles = w.num_tiles;
-    } else {
-      int rc = stage_dispatch(m, dispatch_idx, w, st);
-      if (rc) return rc;
-    }
-  }
+  const PendingDispatch pending{dispatch_idx, &w};
   if (chosen == PATH_MX) {
     // each token's hidden row is split once and written to each of its pairs
     if (m.H % MX_BK != 0 || m.I % MX_BK != 0) {
       set_error("gate_up (MX path): hidden %lld and intermediate %lld must be multiples of 64",
                 (long long)m.H, (long long)m.I);
       return BSA_EINVAL;
+    }
+    if (dispatch_idx) {  // the split below writes through the dispatch's pair_pos
+      int rc = stage_dispatch(m, dispatch_idx, w, st);
+      if (rc) return rc;
     }
     // every token's hidden row split once and written to its pairs' sorted
     // rows, k-tile-major, so a tile's rows of one k-tile are one contiguous run
@@ -2810,7 +2839,7 @@ static int stage_gate_up(const MoeShape& m, const void* hidden, const void* bloc
     g.out_s_kt = w.rows_mx * 4;
     return launch_gemm_mx<EPI_SWIGLU_MX>(g, P, st);
   }
-  return launch_gemm<EPI_SWIGLU>(g, chosen, P, st);
+  return launch_gemm<EPI_SWIGLU>(g, chosen, P, st, dispatch_idx ? &pending : nullptr);
 }
 
 static int stage_down(const MoeShape& m, const void* blocks, const void* scales, const void* bias,

@@ -15,10 +15,14 @@ from .oracle import (  # noqa: F401
     bits_equal_or_both_nan,
     dequantize_expert_ref,
     dequant_table_c,
+    e2m3_decode,
     e4m3_decode,
+    experts_mx6_ref,
     experts_mx_ref,
     experts_ref,
     mlp_ref,
+    mxfp6_split_dequant_ref,
+    mxfp6_split_ref,
     mxfp8_dequant_ref,
     mxfp8_quant_ref,
     mxfp8_split_dequant_ref,

@@ -448,6 +448,112 @@ def experts_mx_ref(h: torch.Tensor, router_indices: torch.Tensor, routing_weight
     return out
 
 
+# OCP MX E2M3 (FP6): sign bit 5, two exponent bits (bias 1), three mantissa
+# bits, no infinities or NaN; largest magnitude 7.5, subnormal step 1/8.
+E2M3_MAX = 7.5
+
+
+def e2m3_decode(codes: np.ndarray) -> np.ndarray:
+    """OCP E2M3 codes (6 bits; sign = bit 5) -> float64."""
+    c = np.asarray(codes).astype(np.int64)
+    sign = np.where(c & 0x20, -1.0, 1.0)
+    e = (c >> 3) & 3
+    m = c & 7
+    mag = np.where(e == 0, m / 8.0, (1.0 + m / 8.0) * np.exp2(e - 1.0))
+    return sign * mag
+
+
+def _e2m3_codes(y: np.ndarray) -> np.ndarray:
+    """E2M3 codes (int64) of float64 values, round to nearest even,
+    saturating at 7.5; the sign bit follows the sign of y (-0 included).
+    The grid steps are 1/8 below 2 (subnormals and the first binade alike),
+    1/4 in [2, 4) and 1/2 in [4, 7.5], and a code is its value's position
+    on that grid, so ties to even codes are ties to even mantissas."""
+    mag = np.minimum(np.abs(y), E2M3_MAX)
+    code = np.where(mag < 2.0, np.rint(mag * 8.0),
+                    np.where(mag < 4.0, 16.0 + np.rint((mag - 2.0) * 4.0), 24.0 + np.rint((mag - 4.0) * 2.0)))
+    code = np.minimum(code, 31.0).astype(np.int64)
+    return code | (np.signbit(y).astype(np.int64) << 5)
+
+
+def _mx6_shared_exp(blk: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Blocks ``[..., 32]`` (float64) -> (X int64 [...], bad bool [...]).
+
+    X = ceil(log2(amax / 7.5)): floor(log2(amax)) - 2, plus 1 when amax's
+    significand exceeds 1.875 (7.5 = 1.875 * 2^2), so that no element of
+    the block saturates; clamped to [-127, 127]; -127 for an all-zero block."""
+    amax = np.abs(blk).max(-1)
+    bad = ~np.isfinite(blk).all(-1)
+    f, e = np.frexp(np.where(np.isfinite(amax), amax, 1.0))   # amax = f * 2^e, f in [0.5, 1)
+    X = np.clip(e - 1 - 2 + (2 * f > 1.875), -127, 127)
+    X = np.where(amax == 0, -127, X)
+    return X.astype(np.int64), bad
+
+
+def mxfp6_split_ref(x: torch.Tensor, terms: int = 2) -> tuple[np.ndarray, np.ndarray]:
+    """Multi-term MXFP6 (E2M3) split of ``[R, K]`` floats: ``(codes uint8
+    [terms, R, K], scale bytes uint8 [R, K/32])``.
+
+    No reference counterpart: the activation format of this build's FP6 MX
+    path.  Per 32-element block with shared exponent X (``_mx6_shared_exp``),
+    term t holds E2M3((x - sum of the earlier terms) / 2^Xt), Xt =
+    max(X - 4t, -127), rounded to nearest even; the residuals are exact in
+    float64.  The scale byte is that of X (term t's is max(byte - 4t, 0)).
+    Blocks holding inf or NaN: scale byte 255 (the E8M0 NaN), every code 0."""
+    a = x.detach().double().cpu().numpy()
+    R, K = a.shape
+    blk = a.reshape(R, K // 32, 32)
+    X, bad = _mx6_shared_exp(blk)
+    res = np.where(bad[..., None], 0.0, blk)
+    codes = []
+    for t in range(terms):
+        sc = np.exp2(np.maximum(X - 4 * t, -127).astype(np.float64))[..., None]
+        c = _e2m3_codes(res / sc)
+        res = res - e2m3_decode(c) * sc
+        codes.append(np.where(bad[..., None], 0, c).reshape(R, K))
+    scales = np.where(bad, 255, X + 127).astype(np.uint8)
+    return np.stack(codes).astype(np.uint8), scales
+
+
+def mxfp6_split_dequant_ref(codes: np.ndarray, scales: np.ndarray) -> torch.Tensor:
+    """sum over terms t of E2M3(codes[t]) * 2^max(X - 4t, -127) per 32-element
+    block (X = scale byte - 127) -> float32; NaN for blocks of scale 255."""
+    terms, R, K = codes.shape
+    s = np.asarray(scales).astype(np.int64)
+    X = s - 127
+    out = np.zeros((R, K // 32, 32))
+    for t in range(terms):
+        out += e2m3_decode(codes[t]).reshape(R, K // 32, 32) * np.exp2(np.maximum(X - 4 * t, -127))[..., None]
+    out = np.where((s == 255)[..., None], np.nan, out)
+    return torch.from_numpy(out.reshape(R, K).astype(np.float32))
+
+
+def experts_mx6_ref(h: torch.Tensor, router_indices: torch.Tensor, routing_weights: torch.Tensor,
+                    gate_up_blocks, gate_up_scales, gate_up_bias, down_blocks, down_scales,
+                    down_bias, alpha: float = 1.702, limit: float = 7.0, terms: int = 2) -> torch.Tensor:
+    """The FP6 MX path's arithmetic: ``experts_ref`` with both GEMMs'
+    activations replaced by their ``terms``-term MXFP6 split (hidden per
+    token; the gated activations after their rounding to bfloat16), float64
+    GEMMs."""
+    E = gate_up_blocks.shape[0]
+    hq = mxfp6_split_dequant_ref(*mxfp6_split_ref(h.float(), terms))
+    out = torch.zeros(h.shape, dtype=torch.float32)
+    mask = F.one_hot(router_indices.to(torch.int64), num_classes=E).permute(2, 1, 0)
+    for e in range(E):
+        top_k_pos, token_idx = torch.where(mask[e])
+        if token_idx.numel() == 0:
+            continue
+        w_gu = dequant_torch(gate_up_blocks[e:e + 1], gate_up_scales[e:e + 1], torch.float32)[0]
+        w_dn = dequant_torch(down_blocks[e:e + 1], down_scales[e:e + 1], torch.float32)[0]
+        gu = hq[token_idx].double() @ w_gu.double() + gate_up_bias[e].double()
+        act = apply_gate_ref(gu.float(), alpha, limit).to(torch.bfloat16)
+        aq = mxfp6_split_dequant_ref(*mxfp6_split_ref(act, terms))
+        o = (aq.double() @ w_dn.double() + down_bias[e].double()).float()
+        o = o * routing_weights[token_idx, top_k_pos, None].float()
+        out = out.index_add(0, token_idx, o)
+    return out
+
+
 def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
     """float32 -> bfloat16 bit patterns, round to nearest even, NaN -> 0x7FC0."""
     lib = _load()

@@ -150,3 +150,47 @@ def test_decode_with_every_pair_dropped(device, T):
     assert ntiles == 0
     assert int(torch.count_nonzero(out)) == 0
     assert torch.equal(out.view(torch.int16), staged.view(torch.int16))
+
+
+@pytest.mark.parametrize("T", [1, 64])
+def test_decode_part_kernel_runs_on_a_dispatched_workspace(device, T):
+    """A decode batch whose biases are only 2-byte aligned cannot take the
+    persistent kernel (it DMAs the bias), so its gate_up runs the part
+    kernel, which does not build the dispatch: the forward must then launch
+    the dispatch itself.  The workspace starts zeroed (an undispatched
+    workspace would give every expert zero rows and a bias-only layer, not
+    out-of-range indices), and must end up holding the restatement's
+    dispatch, with the layer equal to the staged call bit for bit."""
+    from blockstreamer_amd import synthetic
+    from tests.moe_util import expert_args
+
+    E, k, H, I = 128, 4, 2880, 2880
+    t = synthetic.moe_layer(synthetic.MoEShape(E, k, H, I, T), seed=61, scale_lo=116, scale_hi=120,
+                            device=device)
+    idx, w = synthetic.random_routing(T, E, k, seed=62, device=device)
+    gu_b, gu_s, gu_bias, dn_b, dn_s, dn_bias = expert_args(t)
+
+    def shifted(b):  # same values, storage 2 bytes past a 16-byte boundary
+        buf = torch.empty(b.numel() + 1, dtype=b.dtype, device=device)
+        buf[1:] = b.reshape(-1)
+        return buf[1:].view(b.shape)
+
+    gu_bias, dn_bias = shifted(gu_bias), shifted(dn_bias)
+    assert gu_bias.data_ptr() % 16 == 2
+    x = t["hidden"].contiguous()
+    out = torch.empty(T, H, dtype=x.dtype, device=device)
+    nb = kernels.moe_workspace_bytes(T, H, I, E, k)
+    ws = kernels._aligned_bytes(nb, device)
+    ws.zero_()
+    announce(f"decode part kernel on a zeroed workspace T={T}")
+    _lib.call("bsa_moe_experts_fwd", x.data_ptr(), T, H, I, E, k, idx.data_ptr(), w.data_ptr(),
+              _lib.dtype_code(w.dtype), gu_b.data_ptr(), gu_s.data_ptr(), gu_bias.data_ptr(), dn_b.data_ptr(),
+              dn_s.data_ptr(), dn_bias.data_ptr(), _lib.dtype_code(gu_bias.dtype), 1.702, 7.0, out.data_ptr(),
+              _lib.dtype_code(x.dtype), ws.data_ptr(), nb, None, 1, 0, _lib.stream_handle(device))
+    staged = kernels.MoEStages(x, idx, w, gu_b, gu_s, gu_bias, dn_b, dn_s, dn_bias, path="stream").run()
+    torch.cuda.synchronize()
+    counts, offsets, row_pair, pair_pos, tiles, ntiles = _read_workspace(ws, T, E, k)
+    rc, ro, rr, rp, rt = _reference(idx.cpu(), E)
+    assert torch.equal(counts, rc) and torch.equal(offsets, ro)
+    assert torch.equal(row_pair[: rr.numel()], rr) and torch.equal(pair_pos, rp)
+    assert torch.equal(out.view(torch.int16), staged.view(torch.int16))
