@@ -6,9 +6,12 @@ binding (streamer.py:151-180), the LoRA recompute backward
 (_autograd.py:125-175) and ``install_mxfp4_experts`` callers work unchanged.
 The arithmetic runs in hand-written gfx950 HIP kernels (``libbsamd.so``):
 
-* ``MXFP4Experts.forward`` is one device-side dispatch, two grouped GEMMs
-  that decode MXFP4 on the fly (bias and clamped SwiGLU fused), and a
-  combine -- no host synchronisation and no dense weight in memory;
+* ``MXFP4Experts.forward`` on bf16 hidden states (and under autocast) is
+  one device-side dispatch, two grouped GEMMs that decode MXFP4 on the fly
+  (bias and clamped SwiGLU fused), and a combine -- no host synchronisation
+  and no dense weight in memory; float32 and float16 hidden states keep
+  their precision: the reference's per-expert loop in their dtype, each
+  product on ``mxfp4_matmul``'s exact multi-term kernels;
 * ``mxfp4_matmul`` runs one expert's product and its input gradient on the
   packed GEMM kernels (float32 inputs to float32 accuracy);
 * ``dequantize_expert`` is the dequant kernel, bit-exact with the reference.
@@ -18,8 +21,6 @@ pointers or mutates them (the StreamedModel contract, streamer.py:159-174).
 """
 
 from __future__ import annotations
-
-import warnings
 
 import torch
 from torch import Tensor, nn
@@ -189,11 +190,8 @@ class MXFP4Experts(nn.Module):
             raise ValueError("MXFP4Experts.forward needs router_indices and routing_weights")
         shape = hidden_states.shape
         flat = hidden_states.reshape(-1, shape[-1])
-        if flat.dtype != torch.bfloat16 and not (flat.is_cuda and torch.is_autocast_enabled("cuda")):
-            warnings.warn(
-                f"MXFP4Experts: {flat.dtype} hidden states enter the fused expert GEMMs as bfloat16 (the "
-                "result keeps the input dtype); run the layer in bfloat16 or under torch.autocast, or use "
-                "mxfp4_matmul per expert for float32 products", stacklevel=2)
+        if flat.dtype in (torch.float32, torch.float16) and not (flat.is_cuda and torch.is_autocast_enabled("cuda")):
+            return self._forward_in_dtype(flat, router_indices, routing_weights).reshape(shape)
         out = _MoEExperts.apply(
             flat, router_indices, routing_weights,
             self.gate_up_proj_blocks, self.gate_up_proj_scales, self.gate_up_proj_bias,
@@ -201,6 +199,37 @@ class MXFP4Experts(nn.Module):
             float(self.alpha), float(self.limit),
         )
         return out.reshape(shape)
+
+
+    def _forward_in_dtype(self, hidden: Tensor, router_indices: Tensor, routing_weights: Tensor) -> Tensor:
+        """float32 / float16 hidden states: block_streamer/gptoss.py:143-176 op
+        for op in the hidden states' own dtype, one expert at a time, each
+        product on the packed kernels of ``mxfp4_matmul`` (the input split into
+        bf16 terms whose sum is it exactly -- three for float32, two for
+        float16 -- times the exactly decoded weights, summed in float32 and
+        rounded once to the input dtype).  So the rounding points are the
+        reference's: its ``x @ dequantize(..., x.dtype)``, the bias add, the
+        SwiGLU and the combine all happen in the input dtype.  Differentiable
+        through ``mxfp4_matmul``'s own backward.  Router indices outside
+        [0, E) are dropped, as in the fused path."""
+        E = self.gate_up_proj_blocks.shape[0]
+        out = torch.zeros_like(hidden)
+        idx = router_indices.reshape(hidden.shape[0], -1).to(torch.int64)
+        w = routing_weights.reshape(idx.shape)
+        with torch.no_grad():
+            valid = (idx >= 0) & (idx < E)
+            hit = torch.unique(idx[valid]).tolist()                      # ascending, as gptoss.py:148
+        for e in hit:
+            top_k_pos, token_idx = torch.where(idx.t() == e)             # (slot, token) order, gptoss.py:153
+            current = hidden[token_idx]
+            gate_up = (mxfp4_matmul(current, self.gate_up_proj_blocks[e:e + 1], self.gate_up_proj_scales[e:e + 1])
+                       + self.gate_up_proj_bias[e])
+            gated = self._apply_gate(gate_up)
+            o = (mxfp4_matmul(gated, self.down_proj_blocks[e:e + 1], self.down_proj_scales[e:e + 1])
+                 + self.down_proj_bias[e])
+            o = o * w[token_idx, top_k_pos, None]
+            out = out.index_add(0, token_idx, o.to(hidden.dtype))
+        return out
 
 
 class _Router(torch.autograd.Function):
