@@ -6,8 +6,11 @@ scratch instead of the caller.  It runs the same kernels, so its output must
 equal the workspace entry point's bit for bit.  Two calls run back to back,
 the second on a smaller batch, so the second reads a scratch that still holds
 the first call's larger contents.  Shapes: the gpt-oss-120b decode layer
-(128 experts, top-4, hidden = intermediate = 2880) at 64 then 8 tokens, and
-the tiny layer on the prefill tiles.
+(128 experts, top-4, hidden = intermediate = 2880) at 64 then 8 tokens (the
+weight-streaming kernels); a gpt-oss-20b-shaped layer (32 experts, top-4) at
+200 then 150 tokens, whose 25 and 19 rows per expert take the MX prefill
+kernels; and the tiny layer (8 experts, top-2, 256 wide) at 300 then 100
+tokens on the bf16 tiled kernels.
 """
 
 from __future__ import annotations
@@ -62,3 +65,25 @@ def test_noalloc_refuses_a_batch_beyond_the_scratch(device):
     t, idx, scores = _layer(shape, 73, device)
     with pytest.raises(ValueError, match="static scratch"):
         kernels.moe_experts_forward(t["hidden"], idx, scores, *expert_args(t), noalloc=True)
+
+
+@pytest.mark.parametrize("shape,path", [
+    ((32, 4, 2880, 2880, 200, 150), "auto"),     # 25 / 19 rows per expert: the MX kernels
+    ((8, 2, 256, 256, 300, 100), "tiled"),       # the bf16 tiled kernels
+], ids=["20b-width-mx", "tiny-tiled"])
+def test_noalloc_prefill_kernels_twice(device, shape, path):
+    E, k, H, I, T1, T2 = shape
+    t1, i1, s1 = _layer(synthetic.MoEShape(E, k, H, I, T1), 74, device)
+    t2, i2, s2 = _layer(synthetic.MoEShape(E, k, H, I, T2), 75, device)
+    assert kernels.moe_workspace_bytes(T1, H, I, E, k) <= 16 << 20
+    announce(f"no-alloc forward {shape} path={path}")
+    got1 = kernels.moe_experts_forward(t1["hidden"], i1, s1, *expert_args(t1), path=path, noalloc=True)
+    got2 = kernels.moe_experts_forward(t2["hidden"], i2, s2, *expert_args(t2), path=path, noalloc=True)
+    torch.cuda.synchronize()
+    want1 = kernels.moe_experts_forward(t1["hidden"], i1, s1, *expert_args(t1), path=path)
+    want2 = kernels.moe_experts_forward(t2["hidden"], i2, s2, *expert_args(t2), path=path)
+    torch.cuda.synchronize()
+    assert _same_bits(got1, want1), f"{T1} tokens: no-alloc differs from the workspace forward"
+    assert _same_bits(got2, want2), f"{T2} tokens after {T1}: no-alloc differs from the workspace forward"
+    tok = torch.arange(4)
+    assert_layer_close(got2.cpu()[tok], oracle_tokens(t2, i2, s2, tok), f"no-alloc {T2} tokens vs oracle")
