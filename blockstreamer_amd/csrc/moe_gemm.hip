@@ -1602,7 +1602,7 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
   const int n0 = nt * T2_BN;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;  // column quarter: weight rows 64*wave .. +64
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // column quarter: weight rows 64*wave .. +64
   const int G = a.K / 32;
   const int KT = a.K / T2_BK;
   const int l32 = lane & 31;
@@ -1898,7 +1898,7 @@ __global__ __launch_bounds__(64 * WM * WN, BSA_MX_WG_PER_CU) void moe_mx_kernel(
   const int n0 = nt * BN;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN;   // rows 32*MB*wm .. of the tile
   const int wn = wave % WN;   // weight rows WCOLS*wn .. of the tile
   const int G = a.K / 32;
@@ -2250,7 +2250,7 @@ template <int EPI, bool QW4, bool SW4, int NMB>
 __device__ __forceinline__ void bt_tile(const GemmArgs& a, uint8_t* smem, int e, int m0, int rows, int nt) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31;
   const int g = lane >> 5;
   const int KT = a.K / BT_BK;
