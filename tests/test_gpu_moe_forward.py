@@ -230,3 +230,18 @@ def test_combine_batched_equals_split(device, k):
                                          w[s].contiguous(), *args, path="tiled")
              for s in (slice(0, 550), slice(550, T))]
     assert torch.equal(full.view(torch.int16), torch.cat(parts).view(torch.int16))
+
+
+@pytest.mark.parametrize("path", PATHS + ["auto", "mx"])
+def test_gptoss_20b_full_layer_trained_scales_absolute(device, path):
+    """The 20b-shaped layer (2048 tokens) with E8M0 scales in [116, 120]:
+    outputs of order one, every token against the float32 GPU reference with
+    the layer bar's max-abs 2e-2 as an absolute bound."""
+    shape = synthetic.MoEShape(32, 4, 2880, 2880, 2048)
+    t = _realistic(device, shape, seed=13, bias_std=0.01)
+    _, scores, idx = oracle.router_ref(t["hidden"].cpu(), t["router_weight"].cpu(),
+                                       t["router_bias"].cpu(), 4)
+    idx, scores = idx.to(device), scores.to(device)
+    announce(f"moe 20b full layer, trained scales, path={path}")
+    got = kernels.moe_experts_forward(t["hidden"], idx, scores, *expert_args(t), path=path)
+    assert_layer_close(got, gpu_reference(t, idx, scores), f"20b trained scales {path}", absolute=True)

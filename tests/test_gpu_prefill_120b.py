@@ -63,6 +63,33 @@ def test_prefill_forward_every_token(layer, path, layout):
     assert_layer_close(got.cpu()[tok], layer["want"], f"120b prefill {path} {layout}: 64 tokens vs oracle")
 
 
+@pytest.fixture(scope="module")
+def trained_layer(device):
+    """The same layer shape with E8M0 scales in [116, 120], the range of a
+    trained checkpoint: outputs of order one, where the layer bar's max-abs
+    2e-2 applies as an absolute bound."""
+    announce("120b prefill at trained scales: inputs and references")
+    t = synthetic.moe_layer(SHAPE, seed=15, scale_lo=116, scale_hi=120, router_bias_std=0.0,
+                            device=device)
+    _, scores, idx = oracle.router_ref(t["hidden"].cpu(), t["router_weight"].cpu(),
+                                       t["router_bias"].cpu(), SHAPE.top_k)
+    idx, scores = idx.to(device), scores.to(device)
+    ref = gpu_reference(t, idx, scores)
+    torch.cuda.synchronize()
+    return dict(t=t, idx=idx, scores=scores, ref=ref)
+
+
+@pytest.mark.parametrize("path", ["auto", "tiled", "mx"])
+def test_prefill_forward_absolute_bar_at_trained_scales(trained_layer, path):
+    t = trained_layer["t"]
+    announce(f"120b prefill forward at trained scales path={path}")
+    got = kernels.moe_experts_forward(t["hidden"], trained_layer["idx"], trained_layer["scores"],
+                                      *expert_args(t), path=path)
+    torch.cuda.synchronize()
+    assert_layer_close(got, trained_layer["ref"], f"120b prefill {path}, trained scales: all tokens vs fp32 GPU",
+                       absolute=True)
+
+
 def test_prefill_layouts_bit_identical(layer):
     """Both blocks layouts give the same bits on the tiled path."""
     announce("120b prefill layouts bit for bit")
