@@ -383,35 +383,41 @@ def bench_moe(wl: Workload, T: int, steps: int, warmup: int, path: str = "auto",
         idx, w = route()
         g = (torch.randn(T, H, generator=torch.Generator().manual_seed(7)) * 0.1).to(torch.bfloat16).to(dev)
 
-        def fwd_only():
-            return kernels.moe_experts_forward(x, idx, w, *args, path=path, save=True)
+        def timed_training(train_path):
+            def fwd_only():
+                return kernels.moe_experts_forward(x, idx, w, *args, path=train_path, save=True)
 
-        def fwd_bwd():
-            out, ws, pre = fwd_only()
-            return kernels.moe_experts_backward(g, x, idx, w, args[0], args[1], args[3], args[4], ws, pre)
+            def fwd_bwd():
+                out, ws, pre = fwd_only()
+                return kernels.moe_experts_backward(g, x, idx, w, args[0], args[1], args[3], args[4], ws, pre)
 
-        for _ in range(2):
-            fwd_bwd()
-        torch.cuda.synchronize()
-        pairs, fpairs = [], []
-        for _ in range(max(steps // 2, 3)):
-            a0, a1, a2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
-            a0.record()
-            fwd_only()
-            a1.record()
-            fwd_bwd()
-            a2.record()
-            fpairs.append((a0, a1))
-            pairs.append((a1, a2))
-        torch.cuda.synchronize()
-        fb_ms = _median_ms(pairs)
-        f_ms = _median_ms(fpairs)
+            for _ in range(2):
+                fwd_bwd()
+            torch.cuda.synchronize()
+            pairs, fpairs = [], []
+            for _ in range(max(steps // 2, 3)):
+                a0, a1, a2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+                a0.record()
+                fwd_only()
+                a1.record()
+                fwd_bwd()
+                a2.record()
+                fpairs.append((a0, a1))
+                pairs.append((a1, a2))
+            torch.cuda.synchronize()
+            return _median_ms(pairs), _median_ms(fpairs)
+
+        fb_ms, f_ms = timed_training(path)
         # a forward that saves for the backward keeps the bf16 kernels where
         # automatic selection would take the MX ones
         res["train_forward_kernel_path"] = "tiled" if path == "auto" and kernel == "mx" else kernel
         res["fwd_bwd_ms"] = round(fb_ms, 4)
         res["bwd_ms"] = round(fb_ms - f_ms, 4)
         res["bwd_TFLOP_per_s"] = round(flops / ((fb_ms - f_ms) / 1e3) / 1e12, 1)
+        if path == "auto" and kernel == "mx":
+            # the opt-in MX training forward (MXFP4Experts.mx_training)
+            mfb, mf = timed_training("mx")
+            res["mx_training"] = {"fwd_ms": round(mf, 4), "fwd_bwd_ms": round(mfb, 4)}
     return res
 
 

@@ -102,12 +102,12 @@ class _MoEExperts(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, hidden, router_indices, routing_weights, gu_blocks, gu_scales, gu_bias,
-                dn_blocks, dn_scales, dn_bias, alpha, limit):
+                dn_blocks, dn_scales, dn_bias, alpha, limit, train_path="auto"):
         needs = ctx.needs_input_grad[0] or ctx.needs_input_grad[2]
         if needs:
             out, ws, fac = kernels.moe_experts_forward(
                 hidden, router_indices, routing_weights, gu_blocks, gu_scales, gu_bias,
-                dn_blocks, dn_scales, dn_bias, alpha, limit, save=True)
+                dn_blocks, dn_scales, dn_bias, alpha, limit, save=True, path=train_path)
             ctx.save_for_backward(hidden, router_indices, routing_weights, gu_blocks, gu_scales,
                                   gu_bias, dn_blocks, dn_scales, dn_bias, ws, fac)
             ctx.alpha, ctx.limit = alpha, limit
@@ -124,7 +124,7 @@ class _MoEExperts(torch.autograd.Function):
         grad_h, grad_w = kernels.moe_experts_backward(
             grad_out, hidden, idx, w, gu_b, gu_s, dn_b, dn_s, ws, fac, ctx.alpha, ctx.limit,
             need_hidden=ctx.needs_input_grad[0], need_weights=ctx.needs_input_grad[2])
-        return grad_h, None, grad_w, None, None, None, None, None, None, None, None
+        return grad_h, None, grad_w, None, None, None, None, None, None, None, None, None
 
 
 class MXFP4Experts(nn.Module):
@@ -136,6 +136,14 @@ class MXFP4Experts(nn.Module):
     The placeholders live on the meta device and use ``hidden_size // 32``
     groups for both projections, as gptoss.py:92 does; the kernels read every
     shape from the tensors actually bound at call time.
+
+    ``mx_training`` (default False): a forward that saves for the backward
+    (training) runs the bf16 kernels, whose clamp decisions at +-7 are the
+    closest to float32's; set it to run the native MX kernels there as well
+    for prefill-sized batches (faster).  Their products carry the block-scaled
+    MFMA's accumulation error, which moves a few more pre-activations across
+    the clamp than the bf16 kernels do -- far fewer than the reference's own
+    bf16 arithmetic, which rounds the pre-activations to bf16 first.
     """
 
     def __init__(self, config, dtype: torch.dtype = torch.bfloat16) -> None:
@@ -145,6 +153,7 @@ class MXFP4Experts(nn.Module):
         self.expert_dim = config.intermediate_size
         self.alpha = 1.702
         self.limit = getattr(config, "swiglu_limit", 7.0)
+        self.mx_training = False
         groups = self.hidden_size // 32
 
         def packed(rows: int) -> nn.Parameter:
@@ -192,11 +201,20 @@ class MXFP4Experts(nn.Module):
         flat = hidden_states.reshape(-1, shape[-1])
         if flat.dtype in (torch.float32, torch.float16) and not (flat.is_cuda and torch.is_autocast_enabled("cuda")):
             return self._forward_in_dtype(flat, router_indices, routing_weights).reshape(shape)
+        train_path = "auto"
+        if self.mx_training:
+            # where an inference forward would take the MX kernels: prefill-sized
+            # batches, widths multiples of 64, aligned blocks and scales
+            E, I = kernels._experts_dims(self.gate_up_proj_blocks)
+            if kernels._whole_forward_path("auto", flat.shape[0], router_indices.shape[-1], E, flat.shape[1], I,
+                                           self.gate_up_proj_blocks, self.gate_up_proj_scales,
+                                           self.down_proj_blocks, self.down_proj_scales) == kernels.PATHS["mx"]:
+                train_path = "mx"
         out = _MoEExperts.apply(
             flat, router_indices, routing_weights,
             self.gate_up_proj_blocks, self.gate_up_proj_scales, self.gate_up_proj_bias,
             self.down_proj_blocks, self.down_proj_scales, self.down_proj_bias,
-            float(self.alpha), float(self.limit),
+            float(self.alpha), float(self.limit), train_path,
         )
         return out.reshape(shape)
 

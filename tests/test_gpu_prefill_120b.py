@@ -207,3 +207,53 @@ def test_prefill_backward_full_size(layer):
     assert rel_h <= GRAD_REL_L2 and rel_w <= GRAD_REL_L2
     assert_grad_close(gh, mh, "120b prefill d hidden (kernel's clamp decisions)")
     assert_grad_close(gw, mw, "120b prefill d routing weights (kernel's clamp decisions)")
+
+
+def _bf16_arithmetic_flips(t, idx, limit=7.0):
+    """Clamp decisions that the reference's own bf16 arithmetic takes
+    differently from float32: it rounds the gate_up product to bf16 and adds
+    the bf16 bias in bf16 (block_streamer/gptoss.py:158-166 on bf16 hidden
+    states) before clamping (:131-133)."""
+    h = t["hidden"].float()
+    flips = 0
+    for e in torch.unique(idx).tolist():
+        tok, _ = torch.where(idx == e)
+        wgu = kernels.dequantize_mxfp4(t["gate_up_proj_blocks"][e:e + 1], t["gate_up_proj_scales"][e:e + 1],
+                                       torch.float32)[0]
+        prod = h[tok] @ wgu
+        bias = t["gate_up_proj_bias"][e]
+        gu32 = prod + bias.float()
+        gu16 = (prod.to(torch.bfloat16) + bias.to(torch.bfloat16)).float()
+        flips += int(((gu16[:, 0::2] <= limit) != (gu32[:, 0::2] <= limit)).sum())
+        flips += int(((gu16[:, 1::2].abs() <= limit) != (gu32[:, 1::2].abs() <= limit)).sum())
+    return flips
+
+
+def test_prefill_backward_mx_training(layer):
+    """The training forward on the MX kernels (``path="mx"`` with the save;
+    ``MXFP4Experts.mx_training``) at full size, followed by the backward.
+    The block-scaled MFMA's accumulation moves more gate_up pre-activations
+    across +-7 than the bf16 kernels do: the bars are the count of differing
+    clamp decisions (at most 1e-5 of them, and no more than the reference's own
+    bf16 arithmetic moves) and the gradients against float32 autograd whose
+    clamp decisions follow the kernel's."""
+    t = layer["t"]
+    idx = layer["idx"]
+    g = (torch.randn(SHAPE.tokens, SHAPE.hidden, generator=torch.Generator(device=t["hidden"].device)
+                     .manual_seed(57), device=t["hidden"].device) * 1e-3).to(torch.bfloat16)
+    w = layer["scores"].float()
+    announce("120b prefill backward after the MX training forward")
+    _, ws, fac = kernels.moe_experts_forward(t["hidden"], idx, w, *expert_args(t), save=True, path="mx")
+    gh, gw = kernels.moe_experts_backward(g, t["hidden"], idx, w, t["gate_up_proj_blocks"],
+                                          t["gate_up_proj_scales"], t["down_proj_blocks"],
+                                          t["down_proj_scales"], ws, fac)
+    torch.cuda.synchronize()
+    announce("120b prefill MX training: float32 references")
+    mh, mw, flips = _fp32_grads(t, idx, w, g, _save_by_pair(fac, idx))
+    ref_flips = _bf16_arithmetic_flips(t, idx)
+    n = SHAPE.tokens * SHAPE.top_k * 2 * SHAPE.intermediate
+    print(f"MX training: clamp decisions differing from float32: {flips} of {n}; the reference's bf16 "
+          f"arithmetic: {ref_flips}")
+    assert flips <= n * 1e-5 and flips <= ref_flips
+    assert_grad_close(gh, mh, "120b MX training d hidden (kernel's clamp decisions)")
+    assert_grad_close(gw, mw, "120b MX training d routing weights (kernel's clamp decisions)")
