@@ -1735,16 +1735,17 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
 //  * B stage [BN rows][2 groups][16 bytes], 2 lanes per row (32 contiguous
 //    bytes, 512 in the k-pair layout), the two halves of row q swapped when
 //    bit 3 of q is set;
-//  * A scales [128][4 B] per stage: the split writes the activations
+//  * A scales, 4 B per row, per stage: the split writes the activations
 //    k-tile-major (k-tile kt of sorted row p at kt*ldq + 128p, its two scale
 //    bytes at kt*ldas + 4p), so a stage's codes and scales are each one
 //    contiguous run; lo's scale byte is hi's minus 4;
 //  * the B scales of the tile's BN weight rows, one contiguous BN*G-byte
 //    span of the checkpoint tensor, are loaded once per tile.
-// A WM x WN grid of waves (default 2 x 2: each wave 64 rows x 128 weight rows,
+// A 2 x WN grid of waves (default 2 x 2: each wave 64 rows x 128 weight rows,
 // 2 x 4 blocks of 32 x 32, two workgroups per CU) splits the tile; 64 x 128
 // per wave reads 12 LDS fragments per 16 MFMAs where 128 x 64 reads 18.
-// Bound: MFMA at the FP8 rate, two instructions per step (the bf16 rate).
+// Bound: the L2-to-LDS DMA rate and MFMA issue at the FP8 rate (two
+// instructions per step: the bf16 rate), each alone close to the whole.
 // ---------------------------------------------------------------------------
 
 constexpr int MX_BM = 128;
@@ -1760,56 +1761,38 @@ __device__ __forceinline__ int64_t tile_src_row(const GemmArgs& a, int m0, int r
   return a.row_pair ? (int64_t)(a.row_pair[pos] / a.topk) : pos;
 }
 
-// Per-configuration sizes: WM x WN waves, wave (wm, wn) owning MB = 4/WM
-// row blocks and NB column blocks of 32 x 32 (rows 32*MB*wm .., weight rows
-// 32*NB*wn .. of the tile); BN = 32 * NB * WN weight rows per tile.  A stage
-// holds the A codes (16 KiB), the A scale bytes (4 per row) and the B codes;
-// the B scales of the tile's weight rows are loaded once per tile (per-stage
+// Per-configuration sizes: a 2 x WN wave grid, wave (wm, wn) owning the two
+// row blocks 2wm, 2wm+1 and NB column blocks of 32 x 32 (rows 64*wm ..,
+// weight rows 32*NB*wn .. of the tile); BN = 32 * NB * WN weight rows per
+// tile.  A stage holds the A codes (16 KiB), the A scale dwords and the B
+// codes.  The scale dwords sit in one 256-byte slot per wave: its AS_ROWS
+// rows, then padding that the wave's other lanes fill with copies, so the
+// scale DMA is a whole-wave instruction (no divergent branch in the k loop).
+// The B scales of the tile's weight rows are loaded once per tile (per-stage
 // loads of their two bytes per row measured slower: one request per row).
-constexpr int MX_AS_BYTES = MX_BM * 4;
-template <int WM, int WN, int NB>
+template <int WN, int NB>
 struct MxCfg {
-  static constexpr int W = WM * WN;                   // waves
-  static constexpr int MB = 4 / WM;
+  static constexpr int W = 2 * WN;                    // waves
   static constexpr int NBLK = NB;
   static constexpr int WCOLS = 32 * NB;
   static constexpr int BN = WCOLS * WN;
   static constexpr int B_BYTES = BN * 32;
-  static constexpr int B_OFF = MX_A_BYTES + MX_AS_BYTES;
+  static constexpr int AS_ROWS = MX_BM / W;           // A scale rows per wave (one dword each)
+  static constexpr int AS_BYTES = W * 256;
+  static constexpr int AS_BLOCK = 32 / AS_ROWS * 256; // slot bytes per 32-row block
+  static constexpr int B_OFF = MX_A_BYTES + AS_BYTES;
   static constexpr int STAGE = B_OFF + B_BYTES;
   static constexpr int A_DMA = 16 / W;                // A instructions per wave per stage
-  static constexpr int AS_ROWS = MX_BM / W;           // A scale rows per wave (one dword each)
   static constexpr int B_DMA = BN / 32 / W;           // B instructions per wave per stage
   static constexpr int DMA_PER_TILE = A_DMA + 1 + B_DMA;
-  static constexpr int EPI_LDS = epi_lds_bytes(MB, NB);  // per-wave epilogue staging bytes
+  static constexpr int EPI_LDS = epi_lds_bytes(2, NB);  // per-wave epilogue staging bytes
 };
 
-// Dynamic LDS bytes of moe_mx_kernel with ns stages and bn weight rows per
-// tile: the stages and the B scales.
-inline size_t mx_smem_bytes(int ns, int bn, int K) {
-  return (size_t)ns * (MX_A_BYTES + MX_AS_BYTES + (size_t)bn * 32) + (size_t)bn * (K / 32);
-}
-
-// One stage's DMA of the MX kernel (the A codes, A scales and B pieces of
-// k-tile kt).  A device function rather than a lambda: HIP-Clang does not
-// emit the host-side handle of these kernel templates when their bodies call
-// a capturing lambda.
-template <class C, int MX_NS>
-__device__ __forceinline__ void mx_issue(uint8_t* smem, int kt, int wave, int lane, const uint8_t* asrc,
-                                         const uint32_t* aoff, const uint8_t* ssrc, int64_t lda_kt,
-                                         int64_t lds_kt, const uint8_t* const* bsrc, int bkt) {
-  uint8_t* st = smem + (kt % MX_NS) * C::STAGE;
-  const uint8_t* a = asrc + kt * lda_kt;
-#pragma unroll
-  for (int j = 0; j < C::A_DMA; ++j)
-    __builtin_amdgcn_global_load_lds(a + aoff[j], (lds_void*)(st + (C::A_DMA * wave + j) * 1024), 16, 0, 0);
-  if (lane < C::AS_ROWS)
-    __builtin_amdgcn_global_load_lds(ssrc + kt * lds_kt, (lds_void*)(st + MX_A_BYTES + C::AS_ROWS * 4 * wave), 4,
-                                     0, 0);
-#pragma unroll
-  for (int h = 0; h < C::B_DMA; ++h)
-    __builtin_amdgcn_global_load_lds(bsrc[h] + kt * bkt, (lds_void*)(st + C::B_OFF + (C::B_DMA * wave + h) * 1024),
-                                     16, 0, 0);
+// Dynamic LDS bytes of moe_mx_kernel with ns stages: the stages and the B
+// scales.
+template <class C>
+inline size_t mx_smem_bytes(int ns, int K) {
+  return (size_t)ns * C::STAGE + (size_t)C::BN * (K / 32);
 }
 
 // Workgroups per CU (the launch bound); two hide each other's barrier and
@@ -1818,73 +1801,207 @@ __device__ __forceinline__ void mx_issue(uint8_t* smem, int kt, int wave, int la
 #define BSA_MX_WG_PER_CU 2
 #endif
 
-// One wave's operands of one 64-k step: its MB row blocks' hi and lo codes
-// with their scale bytes, its NB column blocks' packed weights and scales.
-template <int MB, int NB>
-struct MxFrags {
-  i32x8_t ahi[MB], alo[MB];
-  int sa[MB];  // hi's scale byte; lo's is max(sa - 4, 0)
+// Per-lane DMA sources (workgroup-uniform bases plus 32-bit per-lane
+// offsets) and LDS read offsets of one tile, set up once.
+template <class C>
+struct MxLane {
+  const uint8_t* abase;  // the tile's A codes, k-tile 0
+  const uint8_t* sbase;  // the tile's A scale dwords, k-tile 0
+  const uint8_t* bbase;  // the expert's packed weights
+  uint32_t aoff_src[C::A_DMA];
+  uint32_t soff_src;
+  uint32_t boff_src[C::B_DMA];
+  int64_t lda_kt, lds_kt;
+  int bkt, wave, lane, G;
+  uint32_t aoff0, aoff1, aoff2, aoff3, asoff, boff;
+  const uint8_t* sb_row;
+};
+
+// A workgroup-uniform pointer as scalar registers: the DMA addresses then
+// take the scalar-base form (base + 32-bit lane offset) instead of the
+// compiler strength-reducing them into 64-bit per-lane induction variables.
+__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
+}
+
+// Step kt's DMA into stage kt % MX_NS: the A codes, the A scale slot and
+// the B codes.  A device function rather than a lambda: HIP-Clang does not
+// emit the host-side handle of these kernel templates when their bodies call
+// a capturing lambda.
+template <class C, int MX_NS>
+__device__ __forceinline__ void mx_issue(uint8_t* smem, int kt, const MxLane<C>& l) {
+  uint8_t* st = smem + (kt % MX_NS) * C::STAGE;
+  const int wave = l.wave;
+  const uint8_t* a = uniform_ptr(l.abase + kt * l.lda_kt);
+#pragma unroll
+  for (int j = 0; j < C::A_DMA; ++j) {
+    const uint8_t* src = a + l.aoff_src[j];
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)(st + (C::A_DMA * wave + j) * 1024), 16, 0, 0);
+  }
+  const uint8_t* ssrc = uniform_ptr(l.sbase + kt * l.lds_kt) + l.soff_src;
+  __builtin_amdgcn_global_load_lds(ssrc, (lds_void*)(st + MX_A_BYTES + 256 * wave), 4, 0, 0);
+  const uint8_t* b = uniform_ptr(l.bbase + (int64_t)kt * l.bkt);
+#pragma unroll
+  for (int h = 0; h < C::B_DMA; ++h) {
+    const uint8_t* src = b + l.boff_src[h];
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)(st + C::B_OFF + (C::B_DMA * wave + h) * 1024), 16, 0, 0);
+  }
+}
+
+// --- split-step pipeline ---------------------------------------------------
+// Step kt's MFMAs run in two halves, row block 0 then row block 1, and every
+// LDS read is issued one half ahead of the MFMAs that use it:
+//   read A1(kt) | MFMAs row 0 (B(kt), A0(kt)) | wait for stage kt+1, barrier,
+//   DMA step kt+NS into stage kt, read B(kt+1), A0(kt+1) | MFMAs row 1
+//   (B(kt), A1(kt)).
+// So a wave does not wait on its own LDS reads; B alternates between two
+// register sets (row 1 still multiplies B(kt) while B(kt+1) lands), A0 and
+// A1 are overwritten in place once their MFMAs have issued.  The one barrier
+// per step certifies both that step kt+1 has landed and that every wave is
+// done reading stage kt (its A1 reads are waited for before the barrier).
+
+// Operands of one 32-row block of a 64-k step: hi and lo codes and hi's
+// scale byte (lo's is max(sa - 4, 0)).
+struct MxA {
+  i32x8_t hi, lo;
+  int sa;
+};
+// The NB column blocks' packed weights and scale bytes of a step.
+template <int NB>
+struct MxB {
   u32x4_t b[NB];
   int sb[NB];
 };
 
-// Read step kt's operands from stage st (offsets as set up in the kernel) for
-// the wave's first nmb row blocks, as plain LDS loads: the compiler tracks
-// each one, so the first MFMAs of a step start while the reads of the later
-// operands are still in flight.  (Reading step kt+1 into a second register
-// set during step kt's MFMAs measured slower: the second set does not fit
-// two workgroups per CU.)
-template <int MB, int NB>
-__device__ __forceinline__ void mx_read(MxFrags<MB, NB>& f, const uint8_t* st, uint32_t aoff0, uint32_t aoff1,
-                                        uint32_t aoff2, uint32_t aoff3, uint32_t asoff, uint32_t boff,
-                                        const uint8_t* sb_row, int G, int kt, int nmb) {
+template <int NB>
+__device__ __forceinline__ void mx_read_b(MxB<NB>& f, const uint8_t* st, uint32_t boff, const uint8_t* sb_row, int G,
+                                          int kt) {
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     f.sb[nb] = sb_row[nb * 32 * G + 2 * kt];
     f.b[nb] = *reinterpret_cast<const u32x4_t*>(st + boff + nb * 1024);
   }
+}
+
+// A row block's operands: ar = the stage's A codes + the block's first row,
+// as = its scale byte.
+__device__ __forceinline__ void mx_read_a(MxA& f, const uint8_t* ar, const uint8_t* as, uint32_t aoff0,
+                                          uint32_t aoff1, uint32_t aoff2, uint32_t aoff3) {
+  const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(ar + aoff0);
+  const u32x4_t w1 = *reinterpret_cast<const u32x4_t*>(ar + aoff1);
+  const u32x4_t w2 = *reinterpret_cast<const u32x4_t*>(ar + aoff2);
+  const u32x4_t w3 = *reinterpret_cast<const u32x4_t*>(ar + aoff3);
+  f.hi = i32x8_t{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3], (int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
+  f.lo = i32x8_t{(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3], (int)w3[0], (int)w3[1], (int)w3[2], (int)w3[3]};
+  f.sa = *as;
+}
+
+// One row block's MFMAs of a step, from the j0-th on: every column block's
+// hi term, then every lo term (so the two products into one accumulator are
+// NB MFMAs apart).  j0/j1 split the sequence, [j0, j1) of 2 * NB.
+template <int NB, int J0 = 0, int J1 = 2 * NB>
+__device__ __forceinline__ void mx_mfma_row(f32x16_t (&acc)[NB], const MxA& a, const MxB<NB>& b) {
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    if (mb >= nmb) continue;
-    const uint8_t* ar = st + mb * 32 * 128;
-    const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(ar + aoff0);
-    const u32x4_t w1 = *reinterpret_cast<const u32x4_t*>(ar + aoff1);
-    const u32x4_t w2 = *reinterpret_cast<const u32x4_t*>(ar + aoff2);
-    const u32x4_t w3 = *reinterpret_cast<const u32x4_t*>(ar + aoff3);
-    f.ahi[mb] = i32x8_t{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3], (int)w1[0], (int)w1[1], (int)w1[2],
-                        (int)w1[3]};
-    f.alo[mb] = i32x8_t{(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3], (int)w3[0], (int)w3[1], (int)w3[2],
-                        (int)w3[3]};
-    f.sa[mb] = st[asoff + mb * 32 * 4];
+  for (int j = J0; j < J1; ++j) {
+    const int nb = j % NB;
+    const i32x8_t bb = {(int)b.b[nb][0], (int)b.b[nb][1], (int)b.b[nb][2], (int)b.b[nb][3], 0, 0, 0, 0};
+    if (j < NB)
+      acc[nb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a.hi, bb, acc[nb], 0, 4, 0, a.sa, 0, b.sb[nb]);
+    else
+      acc[nb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a.lo, bb, acc[nb], 0, 4, 0, a.sa > 4 ? a.sa - 4 : 0,
+                                                                0, b.sb[nb]);
   }
 }
 
-// The MFMAs of one step for the wave's first nmb row blocks (the others hold
-// no rows of the tile; nmb is uniform across the wave).
-template <int MB, int NB>
-__device__ __forceinline__ void mx_mfma(f32x16_t (&acc)[MB][NB], const MxFrags<MB, NB>& f, int nmb = MB) {
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      if (mb >= nmb) continue;
-      const i32x8_t b = {(int)f.b[nb][0], (int)f.b[nb][1], (int)f.b[nb][2], (int)f.b[nb][3], 0, 0, 0, 0};
-      acc[mb][nb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.ahi[mb], b, acc[mb][nb], 0, 4, 0, f.sa[mb], 0,
-                                                                    f.sb[nb]);
-      acc[mb][nb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.alo[mb], b, acc[mb][nb], 0, 4, 0,
-                                                                    f.sa[mb] > 4 ? f.sa[mb] - 4 : 0, 0, f.sb[nb]);
-    }
+// s_waitcnt lgkmcnt(0) (vmcnt and expcnt not waited on)
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Step kt of the split-step pipeline for a wave holding NMB (0..2) row
+// blocks of the tile; bc holds B(kt) and a0 A0(kt) (reads issued), bn
+// receives B(kt+1).  ISSUE: whether this step issues step kt + MX_NS's DMA
+// (decided per call site, so the steady-state steps are one basic block and
+// the first half's MFMAs stay above the barrier).  On the last step the
+// reads of "step kt+1" fetch a stale stage (in bounds, never used) and the
+// wait and barrier are no-ops, so every wave passes KT + 1 barriers whatever
+// NMB is.
+template <class C, int MX_NS, int NMB, int ISSUE>
+__device__ __forceinline__ void mx_split_step(f32x16_t (&acc)[2][C::NBLK], MxB<C::NBLK>& bc, MxB<C::NBLK>& bn,
+                                              MxA& a0, MxA& a1, int kt, int KT, uint8_t* smem, const MxLane<C>& l) {
+  constexpr int NB = C::NBLK;
+  const uint8_t* st = smem + (kt % MX_NS) * C::STAGE;
+  // the first MFMA before the A1 reads: its operands were read a half step
+  // ago, and the wait the compiler puts before it then covers only them
+  if constexpr (NMB > 0) mx_mfma_row<NB, 0, 1>(acc[0], a0, bc);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (NMB > 1)
+    mx_read_a(a1, st + 32 * 128, st + l.asoff + C::AS_BLOCK, l.aoff0, l.aoff1, l.aoff2, l.aoff3);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (NMB > 0) mx_mfma_row<NB, 1, 2 * NB>(acc[0], a0, bc);
+  __builtin_amdgcn_sched_barrier(0);
+  // step kt+1 has landed for every wave, and every wave is done reading
+  // stage kt (its A1 reads waited for here)
+  if constexpr (ISSUE == 1)
+    wait_vmcnt<(MX_NS - 2) * C::DMA_PER_TILE>();
+  else
+    wait_tiles_ahead<C::DMA_PER_TILE, MX_NS - 2>(min(MX_NS - 2, KT - 2 - kt));
+  wait_lgkm0();
+  asm volatile("s_barrier" ::: "memory");
+  if constexpr (ISSUE == 1)
+    mx_issue<C, MX_NS>(smem, kt + MX_NS, l);
+  else if (kt + MX_NS < KT)
+    mx_issue<C, MX_NS>(smem, kt + MX_NS, l);
+  if constexpr (NMB > 0) {
+    const uint8_t* sn = smem + ((kt + 1) % MX_NS) * C::STAGE;
+    mx_read_b(bn, sn, l.boff, l.sb_row, l.G, min(kt + 1, KT - 1));
+    mx_read_a(a0, sn, sn + l.asoff, l.aoff0, l.aoff1, l.aoff2, l.aoff3);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (NMB > 1) mx_mfma_row(acc[1], a1, bc);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// The whole k loop: all MX_NS stages issued up front (after the B scales),
+// then the steps two at a time (B's register sets swap roles): the steps
+// that issue a later stage's DMA first (ISSUE = 1, no branch), then the
+// last few with a run-time test (ISSUE = 0).  Ends with every DMA and LDS
+// read complete.
+template <class C, int MX_NS, int NMB>
+__device__ __forceinline__ void mx_kloop(f32x16_t (&acc)[2][C::NBLK], int KT, uint8_t* smem, const MxLane<C>& l) {
+  for (int i = 0; i < MX_NS; ++i)
+    if (i < KT) mx_issue<C, MX_NS>(smem, i, l);
+  wait_tiles_ahead<C::DMA_PER_TILE, MX_NS - 1>(min(MX_NS - 1, KT - 1));
+  asm volatile("s_barrier" ::: "memory");
+  MxB<C::NBLK> b0, b1;
+  MxA a0, a1;
+  if constexpr (NMB > 0) {
+    mx_read_b(b0, smem, l.boff, l.sb_row, l.G, 0);
+    mx_read_a(a0, smem, smem + l.asoff, l.aoff0, l.aoff1, l.aoff2, l.aoff3);
+  }
+  int kt = 0;
+  for (; kt + 1 < KT - MX_NS; kt += 2) {
+    mx_split_step<C, MX_NS, NMB, 1>(acc, b0, b1, a0, a1, kt, KT, smem, l);
+    mx_split_step<C, MX_NS, NMB, 1>(acc, b1, b0, a0, a1, kt + 1, KT, smem, l);
+  }
+  for (; kt < KT; kt += 2) {
+    mx_split_step<C, MX_NS, NMB, 0>(acc, b0, b1, a0, a1, kt, KT, smem, l);
+    if (kt + 1 < KT) mx_split_step<C, MX_NS, NMB, 0>(acc, b1, b0, a0, a1, kt + 1, KT, smem, l);
+  }
+  wait_vmcnt<0>();
+  wait_lgkm0();
 }
 
 template <int EPI, int MX_NS, bool SB16, int WM, int WN, int NB>
 __global__ __launch_bounds__(64 * WM * WN, BSA_MX_WG_PER_CU) void moe_mx_kernel(GemmArgs a) {
-  using C = MxCfg<WM, WN, NB>;
-  constexpr int MB = C::MB;
+  static_assert(WM == 2, "two row blocks per wave (the split-step pipeline)");
+  using C = MxCfg<WN, NB>;
   constexpr int W = C::W;
   static_assert(MX_NS >= 2 && MX_NS <= 6, "pipeline depth");
-  static_assert(WM * MB == 4 && (W == 4 || W == 8), "wave grid");
+  static_assert(W == 4 || W == 8, "wave grid");
   static_assert(C::B_DMA * W * 32 == C::BN, "B stage split over the waves");
-  static_assert(C::AS_ROWS <= 64, "one scale DMA per wave");
+  static_assert(32 % C::AS_ROWS == 0, "whole scale slots per row block");
   constexpr int BN = C::BN;
   extern __shared__ __align__(1024) uint8_t smem[];
   const int L = xcd_tile_index(*a.num_tiles * a.n_tiles_n);
@@ -1899,7 +2016,7 @@ __global__ __launch_bounds__(64 * WM * WN, BSA_MX_WG_PER_CU) void moe_mx_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / WN;   // rows 32*MB*wm .. of the tile
+  const int wm = wave / WN;   // rows 64*wm .. of the tile
   const int wn = wave % WN;   // weight rows WCOLS*wn .. of the tile
   const int G = a.K / 32;
   const int KT = a.K / MX_BK;
@@ -1911,31 +2028,36 @@ __global__ __launch_bounds__(64 * WM * WN, BSA_MX_WG_PER_CU) void moe_mx_kernel(
   // --- per-lane stage DMA sources (every lane always issues all of them, so
   //     the per-wave vmcnt arithmetic is exact; rows or columns past the tile
   //     are loaded from valid addresses and never stored) ------------------
+  MxLane<C> l;
   // A: the tile's 128 sorted rows of k-tile kt are one contiguous 16 KiB run
   // (rows past the valid ones belong to the next expert, or to the 128 spare
   // rows at the end).  Instruction i = A_DMA*wave + j covers rows 8i .. 8i+7,
   // 8 lanes per row; row r's chunk c lands in slot c ^ ((r >> 1) & 7).
-  const uint8_t* asrc = a.Aq + (int64_t)m0 * 128;
-  uint32_t aoff_src[C::A_DMA];
+  l.abase = a.Aq + (int64_t)m0 * 128;
 #pragma unroll
   for (int j = 0; j < C::A_DMA; ++j) {
     const int r = 8 * (C::A_DMA * wave + j) + (lane >> 3);
-    aoff_src[j] = (uint32_t)(r * 128 + (((lane & 7) ^ ((r >> 1) & 7)) * 16));
+    l.aoff_src[j] = (uint32_t)(r * 128 + (((lane & 7) ^ ((r >> 1) & 7)) * 16));
   }
-  // A scales: one dword (two scale bytes, two spare) per row; wave w loads rows
-  // AS_ROWS*w .. +AS_ROWS
-  const uint8_t* ssrc = a.As + (int64_t)(m0 + C::AS_ROWS * wave + (lane < C::AS_ROWS ? lane : 0)) * 4;
+  // A scales: one dword (two scale bytes, two spare) per row; wave w's slot
+  // holds rows AS_ROWS*w .. +AS_ROWS (lanes past AS_ROWS repeat them)
+  l.sbase = a.As + (int64_t)m0 * 4;
+  l.soff_src = (uint32_t)((C::AS_ROWS * wave + lane % C::AS_ROWS) * 4);
   // B: instruction i = B_DMA*wave + h covers rows 32i .. 32i+31, 2 lanes per
   // row; row q's group g sits in half g ^ ((q >> 3) & 1) of its 32 bytes
-  const uint8_t* bsrc[C::B_DMA];
+  l.bbase = a.Bq + (int64_t)e * a.N * G * 16;
 #pragma unroll
   for (int h = 0; h < C::B_DMA; ++h) {
     const int q = 32 * (C::B_DMA * wave + h) + (lane >> 1);
-    const bool ok = n0 + q < a.N;
     const int grp = (lane & 1) ^ ((q >> 3) & 1);
-    bsrc[h] = a.Bq + (int64_t)e * a.N * G * 16 + bq_off(a.kp, ok ? n0 + q : n0, grp, G);
+    l.boff_src[h] = (uint32_t)bq_off(a.kp, n0 + q < a.N ? n0 + q : n0, grp, G);
   }
-  const int bkt = a.kp ? 512 : 32;  // bytes per k-tile (two groups) along a row
+  l.lda_kt = a.ldq;
+  l.lds_kt = a.ldas;
+  l.bkt = a.kp ? 512 : 32;  // bytes per k-tile (two groups) along a row
+  l.wave = wave;
+  l.lane = lane;
+  l.G = G;
 
   // this lane's B rows (one per 32-column block) and their bias
   int bq[NB];
@@ -1946,55 +2068,44 @@ __global__ __launch_bounds__(64 * WM * WN, BSA_MX_WG_PER_CU) void moe_mx_kernel(
     const bool ok = n0 + bq[nb] < a.N;
     bias[nb] = ok ? bias_at(a.bias, a.bias_dtype, (int64_t)e * a.N + n0 + bq[nb]) : 0.f;
   }
-  // LDS byte offsets of this lane's A chunks in row 32*(MB*wm + mb) + l32:
-  // hi codes in chunks lh and 2 + lh, lo codes in 4 + lh and 6 + lh (the
-  // row's swizzle (r >> 1) & 7 does not depend on the row block)
+  // LDS byte offsets of this lane's A chunks in row 64*wm + l32 (row block
+  // 1: 32 rows on): hi codes in chunks lh and 2 + lh, lo codes in 4 + lh and
+  // 6 + lh (the row's swizzle (r >> 1) & 7 does not depend on the row block)
   const int rsw = (l32 >> 1) & 7;
-  const uint32_t abase = (uint32_t)(MB * wm * 32 * 128 + l32 * 128);
-  const uint32_t aoff0 = abase + (uint32_t)((lh ^ rsw) * 16);
-  const uint32_t aoff1 = abase + (uint32_t)(((2 + lh) ^ rsw) * 16);
-  const uint32_t aoff2 = abase + (uint32_t)(((4 + lh) ^ rsw) * 16);
-  const uint32_t aoff3 = abase + (uint32_t)(((6 + lh) ^ rsw) * 16);
-  const uint32_t asoff = (uint32_t)(MX_A_BYTES + (MB * wm * 32 + l32) * 4 + lh);  // + mb*32*4
+  const uint32_t abase = (uint32_t)(64 * wm * 128 + l32 * 128);
+  l.aoff0 = abase + (uint32_t)((lh ^ rsw) * 16);
+  l.aoff1 = abase + (uint32_t)(((2 + lh) ^ rsw) * 16);
+  l.aoff2 = abase + (uint32_t)(((4 + lh) ^ rsw) * 16);
+  l.aoff3 = abase + (uint32_t)(((6 + lh) ^ rsw) * 16);
+  // the row's scale byte lh in its wave slot (row block 1: + AS_BLOCK)
+  const int srow = 64 * wm + l32;
+  l.asoff = (uint32_t)(MX_A_BYTES + (srow / C::AS_ROWS) * 256 + (srow % C::AS_ROWS) * 4 + lh);
   // B: half lh ^ bsw of row bq (bsw = bit 3 of the row, the same for every nb)
-  const uint32_t boff = (uint32_t)(C::B_OFF + bq[0] * 32 + ((lh ^ ((bq[0] >> 3) & 1)) * 16));
-  const uint8_t* sb_row = sbs + bq[0] * G + lh;  // + nb*32*G + 2kt
+  l.boff = (uint32_t)(C::B_OFF + bq[0] * 32 + ((lh ^ ((bq[0] >> 3) & 1)) * 16));
+  l.sb_row = sbs + bq[0] * G + lh;  // + nb*32*G + 2kt
 
-  f32x16_t acc[MB][NB];
+  f32x16_t acc[2][NB];
 #pragma unroll
-  for (int i = 0; i < MB; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  // Stage j % NS holds step j; step kt + NS - 1 is issued into the stage of
-  // step kt - 1 once every wave has passed step kt's barrier (its MFMAs of
-  // step kt - 1, and so the reads they used, are done).  Row blocks past the
-  // tile's rows are neither read nor multiplied (nmb: the wave's row blocks
-  // holding rows of the tile, uniform across the wave).
-  for (int i = 0; i < MX_NS - 1; ++i)
-    if (i < KT) mx_issue<C, MX_NS>(smem, i, wave, lane, asrc, aoff_src, ssrc, a.ldq, a.ldas, bsrc, bkt);
-  const int nmb = min(MB, max(0, (rows - MB * wm * 32 + 31) / 32));
-  MxFrags<MB, NB> f;
-  for (int kt = 0; kt < KT; ++kt) {
-    // step kt (and the B scales issued first) has landed once at most the
-    // steps issued after it are in flight; a bare s_barrier (a
-    // __syncthreads() fence would wait for those too)
-    wait_tiles_ahead<C::DMA_PER_TILE, MX_NS - 2>(min(MX_NS - 2, KT - 1 - kt));
-    asm volatile("s_barrier" ::: "memory");
-    if (kt + MX_NS - 1 < KT)
-      mx_issue<C, MX_NS>(smem, kt + MX_NS - 1, wave, lane, asrc, aoff_src, ssrc, a.ldq, a.ldas, bsrc, bkt);
-    if (nmb > 0) {
-      mx_read(f, smem + (kt % MX_NS) * C::STAGE, aoff0, aoff1, aoff2, aoff3, asoff, boff, sb_row, G, kt, nmb);
-      mx_mfma(acc, f, nmb);
-    }
-  }
+  // Row blocks past the tile's rows are neither read nor multiplied (nmb: the
+  // wave's row blocks holding rows of the tile, uniform across the wave; the
+  // loop's barrier count does not depend on it).
+  const int nmb = min(2, max(0, (rows - 64 * wm + 31) / 32));
+  if (nmb == 2)
+    mx_kloop<C, MX_NS, 2>(acc, KT, smem, l);
+  else if (nmb == 1)
+    mx_kloop<C, MX_NS, 1>(acc, KT, smem, l);
+  else
+    mx_kloop<C, MX_NS, 0>(acc, KT, smem, l);
 
   // epilogue through LDS: the stage buffers are free once every wave is done
   __syncthreads();
-  epilogue_staged<EPI, MB, NB>(a, acc, bias, m0, MB * wm * 32, rows, n0 + wn * C::WCOLS,
-                               smem + wave * C::EPI_LDS, lane);
+  epilogue_staged<EPI, 2, NB>(a, acc, bias, m0, 64 * wm, rows, n0 + wn * C::WCOLS, smem + wave * C::EPI_LDS, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -2475,7 +2586,7 @@ static int allow_big_lds(const void* fn, int kind, int epi, int bytes = 160 * 10
 
 template <int EPI, int NS, int WM, int WN, int NB>
 static int launch_mx_cfg(const GemmArgs& a, int64_t P, size_t smem, hipStream_t st) {
-  using C = MxCfg<WM, WN, NB>;
+  using C = MxCfg<WN, NB>;
   const int64_t max_tiles = (P + MX_BM - 1) / MX_BM + a.E;
   GemmArgs b = a;
   b.n_tiles_n = (a.N + C::BN - 1) / C::BN;
@@ -2502,11 +2613,12 @@ static int launch_mx_cfg(const GemmArgs& a, int64_t P, size_t smem, hipStream_t 
 // Block-scaled MX grouped GEMM (K % 64 == 0; 16-byte aligned blocks, 4-byte
 // aligned weight scales; a.Aq / a.As the k-tile-major split of the sorted
 // activation rows, with 128 spare rows after the last).
-// Pipeline depth BSA_MX_NS, a BSA_MX_WM x BSA_MX_WN wave grid with
-// BSA_MX_NB 32-column blocks per wave (a build-time choice; the defaults
-// measured fastest at the gpt-oss-120b prefill shapes: a third stage does not
-// fit two workgroups per CU, and 8-wave grids at one workgroup per CU ran
-// 7-10% slower).
+// Pipeline depth BSA_MX_NS, a 2 x BSA_MX_WN wave grid with BSA_MX_NB
+// 32-column blocks per wave (a build-time choice; the defaults measured
+// fastest at the gpt-oss-120b prefill shapes: a third stage does not fit two
+// workgroups per CU, and 8-wave grids at one workgroup per CU ran 7-10%
+// slower).  BSA_MX_WM stays 2: the split-step pipeline multiplies two row
+// blocks per wave.
 #ifndef BSA_MX_NS
 #define BSA_MX_NS 2
 #endif
@@ -2528,10 +2640,10 @@ static int launch_gemm_mx(const GemmArgs& a, int64_t P, hipStream_t st) {
               a.K);
     return BSA_EINVAL;
   }
-  using C = MxCfg<BSA_MX_WM, BSA_MX_WN, BSA_MX_NB>;
+  using C = MxCfg<BSA_MX_WN, BSA_MX_NB>;
   // the epilogue stages each wave's results in the (then idle) stages and
   // B-scale buffer
-  const size_t smem = std::max(mx_smem_bytes(BSA_MX_NS, C::BN, a.K), (size_t)C::W * C::EPI_LDS);
+  const size_t smem = std::max(mx_smem_bytes<C>(BSA_MX_NS, a.K), (size_t)C::W * C::EPI_LDS);
   if (smem > 160 * 1024) {
     set_error("MX GEMM: K=%d needs %zu bytes of LDS", a.K, smem);
     return BSA_EINVAL;
