@@ -156,6 +156,21 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return u >> 16;
 }
 
+// bf16 bits of f by gfx950's v_cvt_pk_bf16_f32 (round to nearest even, one
+// instruction; a NaN stays a quiet NaN of the same sign where
+// f32_to_bf16_bits returns the positive canonical one).
+__device__ __forceinline__ uint32_t bf16_bits_hw(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+// The value of lane ^ 1 / lane ^ 2 of the same quad: a DPP quad_perm operand
+// of one VALU move, not a round trip through the LDS crossbar (ds_bpermute)
+// as __shfl_xor compiles to.  Every lane of the quad must be active.
+__device__ __forceinline__ int quad_xor1(int x) { return __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int quad_xor2(int x) { return __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false); }
+__device__ __forceinline__ float quad_xor1(float x) { return __int_as_float(quad_xor1(__float_as_int(x))); }
+__device__ __forceinline__ float quad_xor2(float x) { return __int_as_float(quad_xor2(__float_as_int(x))); }
+
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
 }
@@ -232,10 +247,10 @@ __device__ __forceinline__ uint32_t mx_split8(const float (&v)[8], uint32_t (&hi
     bad |= !(a <= 3.402823466e38f);  // inf or NaN
     amax = fmaxf(amax, a);
   }
-  amax = fmaxf(amax, __shfl_xor(amax, 1));
-  amax = fmaxf(amax, __shfl_xor(amax, 2));
-  bad |= __shfl_xor(bad, 1);
-  bad |= __shfl_xor(bad, 2);
+  amax = fmaxf(amax, quad_xor1(amax));
+  amax = fmaxf(amax, quad_xor2(amax));
+  bad |= quad_xor1(bad);
+  bad |= quad_xor2(bad);
   const int X = mx_shared_exp(amax);
   hi[0] = hi[1] = lo[0] = lo[1] = 0;
   if (!bad && X >= -122) {

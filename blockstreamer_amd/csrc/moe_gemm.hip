@@ -163,11 +163,13 @@ __device__ __forceinline__ float bias_at(const void* bias, int dtype, int64_t i)
   return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
 }
 
-// block_streamer/gptoss.py:130-135 in float32.
+// block_streamer/gptoss.py:130-135 in float32 (the sigmoid's reciprocal by
+// v_rcp_f32, within 1 ulp: an IEEE division is ten instructions, and the
+// result is rounded to bf16 next).
 __device__ __forceinline__ float swiglu(float g, float u, float alpha, float limit) {
   g = fminf(g, limit);
   u = fminf(fmaxf(u, -limit), limit);
-  const float sig = 1.0f / (1.0f + __expf(-alpha * g));
+  const float sig = __builtin_amdgcn_rcpf(1.0f + __expf(-alpha * g));
   return (u + 1.0f) * (g * sig);
 }
 
@@ -183,7 +185,7 @@ __device__ __forceinline__ float swiglu_fwd_grad(float g, float u, float alpha, 
                                                  uint32_t* factors) {
   const float gc = fminf(g, limit);
   const float uc = fminf(fmaxf(u, -limit), limit);
-  const float sg = 1.0f / (1.0f + __expf(-alpha * gc));
+  const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-alpha * gc));
   const float glu = gc * sg;
   const float fu = (u >= -limit && u <= limit) ? glu : 0.0f;
   const float fg = (g <= limit) ? (uc + 1.0f) * (sg + alpha * gc * sg * (1.0f - sg)) : 0.0f;
@@ -290,7 +292,7 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& a, const f32x16_
         for (int v = 0; v < 8; ++v) {
           const float lo = acc[mb][nb][v] + bias[nb];
           const float hi = acc[mb][nb][v + 8] + bias[nb];
-          const float recv = __shfl_xor(odd ? lo : hi, 1);
+          const float recv = quad_xor1(odd ? lo : hi);
           const float g = odd ? recv : lo;
           const float u = odd ? hi : recv;
           const int vv = odd ? v + 8 : v;
@@ -303,7 +305,7 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& a, const f32x16_
           } else {
             act = swiglu(g, u, a.alpha, a.limit);
           }
-          t[r * AC + nb * 16 + (l32 >> 1)] = (uint16_t)f32_to_bf16_bits(act);
+          t[r * AC + nb * 16 + (l32 >> 1)] = (uint16_t)bf16_bits_hw(act);
         }
       }
     }
