@@ -171,6 +171,13 @@ __device__ __forceinline__ int quad_xor2(int x) { return __builtin_amdgcn_mov_dp
 __device__ __forceinline__ float quad_xor1(float x) { return __int_as_float(quad_xor1(__float_as_int(x))); }
 __device__ __forceinline__ float quad_xor2(float x) { return __int_as_float(quad_xor2(__float_as_int(x))); }
 
+// Two floats -> packed bf16 by one v_cvt_pk_bf16_f32 (the same bits as
+// pack_bf16x2 for every non-NaN input).
+__device__ __forceinline__ uint32_t pack_bf16x2_hw(float lo, float hi) {
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
 }

@@ -189,13 +189,13 @@ __device__ __forceinline__ float swiglu_fwd_grad(float g, float u, float alpha, 
   const float glu = gc * sg;
   const float fu = (u >= -limit && u <= limit) ? glu : 0.0f;
   const float fg = (g <= limit) ? (uc + 1.0f) * (sg + alpha * gc * sg * (1.0f - sg)) : 0.0f;
-  *factors = pack_bf16x2(fg, fu);
+  *factors = pack_bf16x2_hw(fg, fu);
   return (uc + 1.0f) * glu;
 }
 
 // d(gate, up) as one bf16 pair from d(act) and the saved factors.
 __device__ __forceinline__ uint32_t swiglu_bwd(uint32_t factors, float dout) {
-  return pack_bf16x2(dout * __uint_as_float(factors << 16), dout * __uint_as_float(factors & 0xFFFF0000u));
+  return pack_bf16x2_hw(dout * __uint_as_float(factors << 16), dout * __uint_as_float(factors & 0xFFFF0000u));
 }
 
 __device__ __forceinline__ void store_out(void* out, int dtype, int64_t i, float v) {
@@ -272,6 +272,46 @@ __host__ __device__ constexpr int epi_lds_bytes(int MB, int NBW) {
   return (1024 * MB * NBW > 4096 * (NBW < 2 ? NBW : 2)) ? 1024 * MB * NBW : 4096 * (NBW < 2 ? NBW : 2);
 }
 
+// The SwiGLU half of epilogue_staged: the wave's bf16 activations into its
+// LDS staging t ([32*MB][16*NBW]), and with SAVE the derivative factors
+// straight to a.save_grad (a separate instantiation, so the per-element
+// loop carries no run-time branch).
+template <bool SAVE, int MB, int NBW>
+__device__ __forceinline__ void swiglu_to_lds(const GemmArgs& a, const f32x16_t (&acc)[MB][NBW],
+                                              const float (&bias)[NBW], int m0, int r0w, int rows, int n0w,
+                                              uint16_t* t, int lane) {
+  constexpr int AC = 16 * NBW;  // activation columns of the wave
+  const int l32 = lane & 31;
+  const int lh = lane >> 5;
+  const bool odd = l32 & 1;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb) {
+      const int ng = n0w + nb * 32 + (l32 & ~1);
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const float lo = acc[mb][nb][v] + bias[nb];
+        const float hi = acc[mb][nb][v + 8] + bias[nb];
+        const float recv = quad_xor1(odd ? lo : hi);
+        const float g = odd ? recv : lo;
+        const float u = odd ? hi : recv;
+        const int vv = odd ? v + 8 : v;
+        const int r = mb * 32 + 8 * (vv >> 2) + 4 * lh + (vv & 3);
+        float act;
+        if constexpr (SAVE) {
+          uint32_t f;
+          act = swiglu_fwd_grad(g, u, a.alpha, a.limit, &f);
+          if (r0w + r < rows && ng + 1 < a.N) a.save_grad[(int64_t)(m0 + r0w + r) * (a.N >> 1) + (ng >> 1)] = f;
+        } else {
+          act = swiglu(g, u, a.alpha, a.limit);
+        }
+        t[r * AC + nb * 16 + (l32 >> 1)] = (uint16_t)bf16_bits_hw(act);
+      }
+    }
+  }
+}
+
 template <int EPI, int MB, int NBW>
 __device__ __forceinline__ void epilogue_staged(const GemmArgs& a, const f32x16_t (&acc)[MB][NBW],
                                                 const float (&bias)[NBW], int m0, int r0w, int rows,
@@ -282,33 +322,10 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& a, const f32x16_
   if constexpr (EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_MX) {
     constexpr int AC = 16 * NBW;                   // activation columns of the wave
     uint16_t* t = reinterpret_cast<uint16_t*>(wl);  // [32*MB][AC] bf16
-    const bool odd = l32 & 1;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-      for (int nb = 0; nb < NBW; ++nb) {
-        const int ng = n0w + nb * 32 + (l32 & ~1);
-#pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          const float lo = acc[mb][nb][v] + bias[nb];
-          const float hi = acc[mb][nb][v + 8] + bias[nb];
-          const float recv = quad_xor1(odd ? lo : hi);
-          const float g = odd ? recv : lo;
-          const float u = odd ? hi : recv;
-          const int vv = odd ? v + 8 : v;
-          const int r = mb * 32 + 8 * (vv >> 2) + 4 * lh + (vv & 3);
-          float act;
-          if (a.save_grad) {
-            uint32_t f;
-            act = swiglu_fwd_grad(g, u, a.alpha, a.limit, &f);
-            if (r0w + r < rows && ng + 1 < a.N) a.save_grad[(int64_t)(m0 + r0w + r) * (a.N >> 1) + (ng >> 1)] = f;
-          } else {
-            act = swiglu(g, u, a.alpha, a.limit);
-          }
-          t[r * AC + nb * 16 + (l32 >> 1)] = (uint16_t)bf16_bits_hw(act);
-        }
-      }
-    }
+    if (a.save_grad)
+      swiglu_to_lds<true>(a, acc, bias, m0, r0w, rows, n0w, t, lane);
+    else
+      swiglu_to_lds<false>(a, acc, bias, m0, r0w, rows, n0w, t, lane);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
