@@ -1699,6 +1699,9 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
+  // a wave whose 64 weight rows all lie past N (in the last column tile)
+  // multiplies nothing; it still issues its DMA share and meets every barrier
+  const bool live = n0 + wave * 64 < a.N;
   for (int i = 0; i < T2_NS - 1; ++i)
     if (i < KT) issue(i);
   for (int kt = 0; kt < KT; ++kt) {
@@ -1718,7 +1721,7 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
     uint32_t sc[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) sc[nb] = *reinterpret_cast<const uint16_t*>(sbs + bq[nb] * G + 2 * kt);
-    t2_ktile<SCHED>(acc, st, sc, aoff, boff, bsw, lh);
+    if (live) t2_ktile<SCHED>(acc, st, sc, aoff, boff, bsw, lh);
   }
 
   // epilogue through LDS: the stage buffers are free once every wave is done
@@ -2113,8 +2116,10 @@ __global__ __launch_bounds__(64 * WM * WN, BSA_MX_WG_PER_CU) void moe_mx_kernel(
 
   // Row blocks past the tile's rows are neither read nor multiplied (nmb: the
   // wave's row blocks holding rows of the tile, uniform across the wave; the
-  // loop's barrier count does not depend on it).
-  const int nmb = min(2, max(0, (rows - 64 * wm + 31) / 32));
+  // loop's barrier count does not depend on it).  Nor is anything of a wave
+  // whose weight rows all lie past N (in the last column tile: half of it at
+  // gate_up's N = 5760, and at down's N = 2880).
+  const int nmb = n0 + wn * C::WCOLS < a.N ? min(2, max(0, (rows - 64 * wm + 31) / 32)) : 0;
   if (nmb == 2)
     mx_kloop<C, MX_NS, 2>(acc, KT, smem, l);
   else if (nmb == 1)
