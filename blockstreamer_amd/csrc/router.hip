@@ -87,14 +87,13 @@ __device__ void topk_softmax_wave(const float* row, int E, int k, int lane, int 
   if (lane == 0) {
     float mx = vals[0];
     for (int r = 1; r < k; ++r) mx = fmaxf(mx, vals[r]);
-    float ex[RT_MAX_K], sum = 0.f;
-    for (int r = 0; r < k; ++r) {
-      ex[r] = __expf(vals[r] - mx);
-      sum += ex[r];
-    }
+    float sum = 0.f;
+    for (int r = 0; r < k; ++r) sum += __expf(vals[r] - mx);
     const float inv = 1.0f / sum;
+    // each exponential again rather than kept in a dynamically indexed array
+    // (such an array can go to scratch memory); the same expression, the same value
     for (int r = 0; r < k; ++r) {
-      st_any(scores, t * k + r, ex[r] * inv, out_dtype);
+      st_any(scores, t * k + r, __expf(vals[r] - mx) * inv, out_dtype);
       indices[t * k + r] = ids[r];
     }
   }
