@@ -50,6 +50,7 @@
 // runs in registers.
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include "bsa_common.h"
 #include "dispatch.h"
@@ -1561,8 +1562,10 @@ __device__ __forceinline__ void preload_b_scales(const uint8_t* Bs, int e, int N
 // pipelined by hand: the LDS reads for step s+1 are issued before the eight
 // MFMAs of step s, and sched_barrier fences keep the compiler from sinking
 // them back next to their uses, so each wait covers reads issued a full step
-// (8 x 32 MFMA cycles) earlier.  Branch free.
-template <int SCHED>
+// (8 x 32 MFMA cycles) earlier.  Branch free.  Only the first NMB 32-row
+// blocks are read and multiplied (the tile's rows; an expert's last row tile
+// often holds fewer than 128).
+template <int SCHED, int NMB>
 __device__ __forceinline__ void t2_ktile(f32x16_t (&acc)[4][2], const uint8_t* st,
                                          const uint32_t (&sc)[2], const uint32_t (&aoff)[4],
                                          const uint32_t (&boff)[2], uint32_t bsw, int lh) {
@@ -1571,7 +1574,7 @@ __device__ __forceinline__ void t2_ktile(f32x16_t (&acc)[4][2], const uint8_t* s
   auto loadA = [&](int step, s16x8_t (&dst)[4]) {
     const uint8_t* p = st + aoff[step];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) dst[mb] = *reinterpret_cast<const s16x8_t*>(p + mb * 4096);
+    for (int mb = 0; mb < NMB; ++mb) dst[mb] = *reinterpret_cast<const s16x8_t*>(p + mb * 4096);
   };
   auto loadB = [&](int h) {
 #pragma unroll
@@ -1599,7 +1602,7 @@ __device__ __forceinline__ void t2_ktile(f32x16_t (&acc)[4][2], const uint8_t* s
       }
     }
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int mb = 0; mb < NMB; ++mb) {
       acc[mb][0] = mfma32(afr[step & 1][mb], bop[0][m], acc[mb][0]);
       acc[mb][1] = mfma32(afr[step & 1][mb], bop[1][m], acc[mb][1]);
     }
@@ -1700,10 +1703,16 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
   // a wave whose 64 weight rows all lie past N (in the last column tile)
-  // multiplies nothing; it still issues its DMA share and meets every barrier
+  // multiplies nothing; it still issues its DMA share and meets every barrier.
+  // nmb: the tile's 32-row blocks holding rows (the same for every wave).
   const bool live = n0 + wave * 64 < a.N;
+  const int nmb = (rows + 31) >> 5;
   for (int i = 0; i < T2_NS - 1; ++i)
     if (i < KT) issue(i);
+  // the k loop, one instantiation per live row-block count (a run-time
+  // choice inside the loop body spilled the accumulators)
+  auto kloop = [&](auto nmb_c) {
+  constexpr int NMB = decltype(nmb_c)::value;
   for (int kt = 0; kt < KT; ++kt) {
     // this wave's DMA for tile kt has landed once at most one tile's worth
     // (the next tile's) is outstanding; the barrier then covers every wave.
@@ -1721,8 +1730,17 @@ __global__ __launch_bounds__(256, 2) void moe_tiled2_kernel(GemmArgs a) {
     uint32_t sc[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) sc[nb] = *reinterpret_cast<const uint16_t*>(sbs + bq[nb] * G + 2 * kt);
-    if (live) t2_ktile<SCHED>(acc, st, sc, aoff, boff, bsw, lh);
+    if (live) t2_ktile<SCHED, NMB>(acc, st, sc, aoff, boff, bsw, lh);
   }
+  };
+  if (nmb == 4)
+    kloop(std::integral_constant<int, 4>{});
+  else if (nmb == 3)
+    kloop(std::integral_constant<int, 3>{});
+  else if (nmb == 2)
+    kloop(std::integral_constant<int, 2>{});
+  else
+    kloop(std::integral_constant<int, 1>{});
 
   // epilogue through LDS: the stage buffers are free once every wave is done
   __syncthreads();
