@@ -2513,26 +2513,52 @@ __device__ __forceinline__ void bt_tile(const GemmArgs& a, uint8_t* smem, int e,
   // column 128 wave + 4 c + j
   const int n = nt * BT_BN + 128 * wave + 4 * c;
   if (n >= a.N) return;
+  if constexpr (EPI == EPI_SWIGLU_BWD) {
+    // The saved derivative factors, 8 rows (one half of a 32-row block's 16
+    // registers) per load batch, two batches in flight: the half after next
+    // is loaded while a half is stored, so one memory round trip per tile is
+    // exposed instead of one per row block.
+    u32x4_t fh[2][8];
+    auto load_half = [&](int hb, u32x4_t (&f)[8]) {
+      const int mb = hb >> 1;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int v = 8 * (hb & 1) + i;
+        const int r = 32 * mb + 8 * (v >> 2) + 4 * g + (v & 3);
+        f[i] = *reinterpret_cast<const u32x4_t*>(a.save_grad + (int64_t)(m0 + min(r, rows - 1)) * a.N + n);
+      }
+    };
+    load_half(0, fh[0]);
+    load_half(1, fh[1]);
 #pragma clang loop unroll(full)
-  for (int mb = 0; mb < NMB; ++mb) {
-    // one 32-row block at a time: its 16 rows' saved derivative factors are
-    // loaded together (the row loop would otherwise wait on each in turn)
-    u32x4_t fac[16];
-    if constexpr (EPI == EPI_SWIGLU_BWD) {
+    for (int hb = 0; hb < 2 * NMB; ++hb) {
+      const int mb = hb >> 1;
+      u32x4_t f[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = fh[hb & 1][i];
+      if (hb + 2 < 2 * NMB) load_half(hb + 2, fh[hb & 1]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int v = 8 * (hb & 1) + i;
+        const int r = 32 * mb + 8 * (v >> 2) + 4 * g + (v & 3);
+        if (r < rows) {
+          const float o[4] = {acc[mb][0][v], acc[mb][1][v], acc[mb][2][v], acc[mb][3][v]};
+          bt_store4<EPI>(a, m0 + r, n, o, f[i]);
+        }
+      }
+    }
+  } else {
+    const u32x4_t none{0u, 0u, 0u, 0u};
+#pragma clang loop unroll(full)
+    for (int mb = 0; mb < NMB; ++mb)
 #pragma clang loop unroll(full)
       for (int v = 0; v < 16; ++v) {
         const int r = 32 * mb + 8 * (v >> 2) + 4 * g + (v & 3);
-        fac[v] = *reinterpret_cast<const u32x4_t*>(a.save_grad + (int64_t)(m0 + min(r, rows - 1)) * a.N + n);
+        if (r < rows) {
+          const float o[4] = {acc[mb][0][v], acc[mb][1][v], acc[mb][2][v], acc[mb][3][v]};
+          bt_store4<EPI>(a, m0 + r, n, o, none);
+        }
       }
-    }
-#pragma clang loop unroll(full)
-    for (int v = 0; v < 16; ++v) {
-      const int r = 32 * mb + 8 * (v >> 2) + 4 * g + (v & 3);
-      if (r < rows) {
-        const float o[4] = {acc[mb][0][v], acc[mb][1][v], acc[mb][2][v], acc[mb][3][v]};
-        bt_store4<EPI>(a, m0 + r, n, o, fac[v]);
-      }
-    }
   }
 }
 
