@@ -768,7 +768,9 @@ def main() -> int:
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_dequant(),
     }
     if not args.no_moe:
-        n_pre = max(args.steps // 4, 5)
+        # the prefill lines take the full step count: with 5 timed steps they read
+        # 5-8 % slower than in steady state (measured, same box)
+        n_pre = max(args.steps, 10)
         moe = {
             "decode_t1": bench_moe(DECODE, 1, max(args.steps, 20), args.warmup),
             "decode_t8": bench_moe(DECODE, 8, max(args.steps, 20), args.warmup),
