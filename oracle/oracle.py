@@ -364,8 +364,9 @@ def _e4m3_codes(y: np.ndarray) -> np.ndarray:
     e2 = e2 - 1
     normal = q >= 2.0 ** -6
     mant = np.where(normal, q / np.exp2(e2.astype(np.float64)) * 8 - 8, q / 2.0 ** -9)
-    code = np.where(normal, ((e2 + 7) << 3) + np.rint(mant).astype(np.int64),
-                    np.rint(mant).astype(np.int64))
+    with np.errstate(invalid="ignore"):   # NaN inputs: their blocks are overwritten by the callers
+        m = np.rint(mant).astype(np.int64)
+    code = np.where(normal, ((e2 + 7) << 3) + m, m)
     return code | (np.signbit(y).astype(np.int64) << 7)
 
 

@@ -63,6 +63,9 @@ MX_CASES = [
     (16, 4, 512, 256, 300),
     (4, 1, 128, 192, 77),
     (32, 4, 2880, 2880, 96),
+    # one and three 64-wide k-steps: the k loop's prologue and tail alone
+    (4, 2, 64, 64, 40),
+    (8, 2, 192, 64, 130),
 ]
 
 
