@@ -268,6 +268,27 @@ def _resolved_kernel(path: str, T: int, wl: Workload) -> str:
     return "mx" if wl.H % 64 == 0 and wl.I % 64 == 0 else "tiled"
 
 
+def _graph_ms(fn, reps: int) -> float:
+    """Milliseconds per call of ``fn`` from ``reps`` calls captured in one
+    HIP graph, replayed five times between two HIP events."""
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(5):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / (5 * reps)
+
+
 def bench_moe(wl: Workload, T: int, steps: int, warmup: int, path: str = "auto", layout: str = "checkpoint",
               train: bool = False, fwd: bool = True, ref: bool = False) -> dict:
     """One MoE layer (router + dispatch + expert GEMMs + combine) of
@@ -337,6 +358,10 @@ def bench_moe(wl: Workload, T: int, steps: int, warmup: int, path: str = "auto",
         wbytes = hit * expert_bytes(H, I)
         res.update({"tokens_per_s": round(T * steps / wall, 1), "ms_per_layer": round(wall / steps * 1e3, 4),
                     "stage_ms": ms, "hit_experts": hit})
+        if kernel == "stream":
+            # GPU time of the layer without the host: ten layer steps captured
+            # in one HIP graph and replayed (how decode serving runs a layer)
+            res["graph_ms_per_layer"] = round(_graph_ms(step, 10), 4)
         hbm = wbytes / (gemm_ms / 1e3) / 1e9
         tfl = flops / (gemm_ms / 1e3) / 1e12
         if kernel == "stream":
