@@ -31,8 +31,13 @@
 //    DMA, packed B decoded from LDS into MFMA operands by the one wave that
 //    uses them, v_mfma_f32_32x32x16_bf16.  Bound: MFMA, in practice L1->L2
 //    requests.
-//  * moe_mx_kernel (prefill, opt-in): the same tiles on the block-scaled
-//    v_mfma_scale_f32_32x32x64_f8f6f4 with MXFP8 activations.
+//  * moe_mx_kernel (prefill: chosen automatically above 16 routed rows per
+//    expert on average):
+//    128x256 tiles of one expert on the block-scaled
+//    v_mfma_scale_f32_32x32x64_f8f6f4, the packed weights as they are
+//    against activations split into two MXFP8 terms (hi, lo), two stages
+//    of global_load_lds DMA and LDS reads issued half a step ahead of the
+//    MFMAs (mx_split_step).  Bound: MFMA issue and the L2->LDS stream.
 //  * moe_tiled_kernel (prefill for operands aligned to less than 16 bytes):
 //    128x128 tiles, BK=64, register-staged LDS double buffering.
 //  * moe_bwd_packed_kernel (the input-gradient backward): the packed weights
