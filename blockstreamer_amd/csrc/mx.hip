@@ -4,7 +4,11 @@
 //
 // No reference counterpart: BlockStreamer multiplies bf16/fp32 activations
 // by dequantised weights (block_streamer/gptoss.py:45-75).  This path trades
-// that for the gfx950 MXFP4 matrix cores and reports its error.
+// that for the gfx950 MXFP4 matrix cores.  Two kernels: mx_quant_kernel, one
+// MXFP8 term per element (the conversion below; 2.7 % relative L2 error on
+// N(0,1) rows, too coarse for float32 parity), and mx_split_kernel, the two
+// terms hi + lo the MX prefill kernels multiply (exact for bf16 elements
+// above ~2^-14 of their block's maximum; described at the kernel).
 //
 // Conversion, per 32-element block of a row (OCP Microscaling Formats v1.0,
 // section 6.3, with the shared exponent taken one higher where the
