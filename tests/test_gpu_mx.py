@@ -143,3 +143,29 @@ def test_mx_dropped_pairs(device):
     args = [a.cpu() for a in expert_args(t)]
     want = oracle.experts_ref(t["hidden"].cpu(), idx.clamp(0, E - 1).cpu(), (w * keep).cpu().float(), *args)
     assert_layer_close(got, want, "MX dropped pairs", absolute=True)
+
+
+def test_mx_scales_aligned_to_4_and_8_bytes_bit_identical(device):
+    """Scale tensors that start 4 or 8 bytes past a 16-byte boundary (the
+    reference's shard planner aligns tensors to 8 bytes) take the MX kernels'
+    4-byte B-scale preload instead of the 16-byte one; the products are the
+    same bit for bit."""
+    E, k, H, I, T = 8, 2, 256, 192, 300   # 600 pairs > 16 per expert: MX
+    t, idx, w = _layer(E, k, H, I, T, seed=31, device=device)
+    args = list(expert_args(t))
+    announce("MX with 4- and 8-byte aligned scales")
+    want = kernels.moe_experts_forward(t["hidden"], idx, w, *args, path="mx")
+
+    def at_offset(x, off):
+        buf = torch.empty(x.numel() + 32, dtype=torch.uint8, device=device)
+        base = (-buf.data_ptr()) % 16
+        v = buf[base + off:base + off + x.numel()].view(x.shape)
+        v.copy_(x)
+        assert v.data_ptr() % 16 == off
+        return v
+
+    args[1] = at_offset(args[1], 4)
+    args[4] = at_offset(args[4], 8)
+    got = kernels.moe_experts_forward(t["hidden"], idx, w, *args, path="mx")
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
