@@ -169,3 +169,22 @@ def test_mx_scales_aligned_to_4_and_8_bytes_bit_identical(device):
     got = kernels.moe_experts_forward(t["hidden"], idx, w, *args, path="mx")
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_mx_concentrated_and_duplicate_routing(device):
+    """The MX kernels when routing piles up: every token on the same two
+    experts (three row tiles each, the last one partial), and every token
+    sent twice to one expert (both pairs count), against the float32 oracle."""
+    E, k, H, I, T = 8, 2, 256, 256, 300
+    t, idx, w = _layer(E, k, H, I, T, seed=41, device=device)
+    args = expert_args(t)
+    cpu_args = [a.cpu() for a in args]
+    idx_two = torch.zeros_like(idx)
+    idx_two[:, 1] = 3
+    idx_dup = idx.clone()
+    idx_dup[:, 1] = idx_dup[:, 0]
+    for what, ix in (("two experts", idx_two), ("duplicate slot", idx_dup)):
+        announce(f"MX {what}")
+        got = kernels.moe_experts_forward(t["hidden"], ix, w, *args, path="mx")
+        want = oracle.experts_ref(t["hidden"].cpu(), ix.cpu(), w.cpu().float(), *cpu_args)
+        assert_layer_close(got, want, f"MX {what}", absolute=True)
