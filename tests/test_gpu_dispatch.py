@@ -74,13 +74,15 @@ def test_dispatch_matches_restatement(device, T, E, k):
     assert torch.equal(tiles[:ntiles], rt)
 
 
-@pytest.mark.parametrize("T", [1, 8, 64, 256])
+@pytest.mark.parametrize("T", [1, 8, 64, 256, 257, 400])
 def test_dispatch_folded_into_the_decode_gemm(device, T):
     """At decode batches the forward folds the dispatch into the persistent
     gate_up launch (every workgroup builds it and writes the same arrays).
     The workspace then holds exactly the dispatch of the restatement, dropped
     pairs included, and the layer equals the staged call (dispatch kernel,
-    then the GEMMs) bit for bit."""
+    then the GEMMs) bit for bit.  Above 1024 pairs (T = 257, 400 at top-4)
+    the decode kernels keep running with the dispatch as its own launch; the
+    workspace and the output are the same."""
     from blockstreamer_amd import synthetic
     from tests.moe_util import expert_args
 
